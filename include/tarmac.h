@@ -1,0 +1,115 @@
+/*
+ * tarmac.h -- C ABI of the MI355X-native TarMAC attention core (libtarmac.so).
+ *
+ * Every entry point takes plain device pointers to row-major contiguous
+ * [B, N, d] tensors (16-byte aligned), sizes, and an opaque stream handle
+ * (a hipStream_t; NULL is the null stream). Nothing is allocated, nothing is
+ * synchronised: the kernels are enqueued on `stream` and the call returns.
+ * Return value: TARMAC_OK, or an error code whose message is available from
+ * tarmac_last_error() on the calling thread. Calls are reentrant.
+ *
+ * Scores are q.k / sqrt(d) with the self pair (i == i) excluded, as in every
+ * path of the reference. Retained sets are the topk largest scores, ties to
+ * the lower agent index. fp32 scores are formed in a fixed fmaf order
+ * (element c = kk*(d/4) + t at step t, slot kk), so results are reproducible
+ * bit for bit.
+ *
+ * Reference paths below are relative to the MHHamdan/TopK-TarMAC checkout.
+ */
+#ifndef TARMAC_H_
+#define TARMAC_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TARMAC_OK 0
+#define TARMAC_ERR_INVALID 1     /* bad shape, dtype, k, pointer or alignment */
+#define TARMAC_ERR_UNSUPPORTED 2 /* valid request outside what the kernels cover */
+#define TARMAC_ERR_HIP 3         /* the HIP runtime rejected the launch */
+
+#define TARMAC_DTYPE_F32 0
+#define TARMAC_DTYPE_BF16 1
+
+#define TARMAC_IDX_I32 0
+#define TARMAC_IDX_I64 1
+
+/* ABI version of this header (bumped on any signature change). */
+int tarmac_abi_version(void);
+
+/* Message for the last non-OK return on this thread ("" if none). */
+const char* tarmac_last_error(void);
+
+/*
+ * Dense attention, softmax over all N-1 peers.
+ * Replaces src/kernels/fused_dense_attention.py:106-152 (fused_dense_attention)
+ * and the composed dense paths scripts/bench_attention_core.py:74-82
+ * (dense_unfused, dense_fused) / src/agents/mappo.py:174-190,361-372,418.
+ * key_chunk: keys staged per LDS pass (0 = whole row when it fits).
+ */
+int tarmac_dense_fwd(const void* q, const void* k, const void* v, void* out, int B, int N, int d,
+                     int dtype, int key_chunk, void* stream);
+
+/*
+ * Fused score-then-select top-k with the key row resident on chip.
+ * Replaces src/kernels/fused_topk_attention.py:296-355
+ * (fused_topk_attention_tiled, fused_topk_attention), the composed gather path
+ * src/kernels/fused_topk_attention.py:390-402 / src/agents/mappo.py:192-231,
+ * and the masked form src/agents/mappo.py:374-382 (same function).
+ * Requires 1 <= topk <= N-1. idx_out (nullable): int32 [B, N, topk], ordered
+ * by (score desc, index asc) for topk <= 8 and by ascending index above.
+ */
+int tarmac_topk_fused_fwd(const void* q, const void* k, const void* v, void* out, int32_t* idx_out,
+                          int B, int N, int d, int topk, int dtype, void* stream);
+
+/*
+ * Streaming top-k: keys pass through LDS in chunks of key_chunk rows, so the
+ * N-wide score row is never resident; no cap on N.
+ * Replaces src/kernels/streaming_topk_attention.py:206-258
+ * (streaming_topk_attention, including return_indices).
+ */
+int tarmac_topk_stream_fwd(const void* q, const void* k, const void* v, void* out,
+                           int32_t* idx_out, int B, int N, int d, int topk, int dtype,
+                           int key_chunk, void* stream);
+
+/*
+ * Attention over a given peer set idx [B, N, kk] (int32 or int64).
+ * Replaces src/kernels/fused_prescore_attention.py:88-114
+ * (fused_prescore_attention) and src/kernels/prescore_selection.py:184-195
+ * (prescore_attention). Out-of-range indices are never dereferenced; their
+ * query rows come out NaN.
+ */
+int tarmac_fixedset_fwd(const void* q, const void* k, const void* v, const void* idx,
+                        int idx_dtype, int kk, void* out, int B, int N, int d, int dtype,
+                        void* stream);
+
+/*
+ * Z-order selector: per-batch Morton codes of pos [B, N, 2] (fp32) at `bits`
+ * bits per axis, agents sorted by code (equal codes by agent index), and each
+ * agent's k curve neighbours (+1..+ceil(k/2), -1..-floor(k/2), wrapping).
+ * Replaces src/kernels/prescore_selection.py:62-84
+ * (_morton_code, select_morton_window). idx_out [B, N, k] (int32 or int64,
+ * nullable); codes_out int64 [B, N] (nullable). Requires 1 <= k <= N-1.
+ */
+int tarmac_morton_window(const float* pos, void* idx_out, int idx_dtype, int64_t* codes_out,
+                         int B, int N, int k, int bits, void* stream);
+
+/*
+ * Selector and attention in one launch: the zorder_k core of
+ * src/agents/mappo.py:265-292 and the "select+attend" total of
+ * scripts/bench_prescore.py:253-257. idx_out: int32 [B, N, topk], nullable.
+ */
+int tarmac_zorder_fwd(const void* q, const void* k, const void* v, const float* pos, void* out,
+                      int32_t* idx_out, int B, int N, int d, int topk, int bits, int dtype,
+                      void* stream);
+
+/* Writes 1.0f to *out: the launch-floor probe of scripts/launch_overhead.py:28-30. */
+int tarmac_noop(float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TARMAC_H_ */

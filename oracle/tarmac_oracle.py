@@ -1,0 +1,359 @@
+"""CPU oracle for the TarMAC attention core -- TEST INFRASTRUCTURE ONLY.
+
+This module is the checker, never the product. Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it. The product path (``topk-tarmac_amd/tarmac``) never imports it and
+fails loudly when its HIP library is missing.
+
+Two layers:
+
+* ``numpy`` restatements (float64 by default) of the reference's PyTorch
+  compositions, one function per reference symbol, each citing the reference
+  file:line it follows.  Paths are relative to the reference checkout.
+* ``canon_*`` wrappers around ``tarmac_oracle.c`` (built into
+  ``oracle/_build/libtarmac_oracle.so``): the fp32 score computed in the exact
+  rounding order the HIP kernels use, so that retained index sets can be
+  compared bit for bit.
+
+Pinning (what checks each function against something other than itself):
+
+==========================  ===================================================
+function                    pinned by
+==========================  ===================================================
+scores                      torch.matmul (float64) and unit-vector closed form
+dense_unfused               torch SDPA (float64, -inf diagonal mask); rows sum
+                            to 1; constant-V and equal-key closed forms
+topk_indices                torch.topk on tie-free rows; brute force over all
+                            k-subsets on tiny rows; constructed ties
+topk_gather                 masked formulation to 1e-10 (float64); k = N-1
+                            equals dense; exactly k nonzero weights
+topk_masked                 equals topk_gather on tie-free inputs (two
+                            independent formulations)
+morton_code                 bit-by-bit interleave loop; golden vectors written
+                            by the reference's own ``_morton_code``
+select_morton_window        golden vectors from the reference; k distinct
+                            peers, never self; curve-neighbour sets
+prescore_attention          dense softmax restricted to the selected set
+canon_topk (C)              numpy oracle: same sets off near-ties, outputs to
+                            1e-6; brute force of the fmaf chain in Python
+canon_morton_window (C)     numpy oracle bit-exact (codes and indices)
+==========================  ===================================================
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+
+# ---------------------------------------------------------------------------
+# numpy restatements of the reference compositions
+# ---------------------------------------------------------------------------
+
+
+def scores(q: np.ndarray, k: np.ndarray) -> np.ndarray:
+    """``S = Q K^T / sqrt(d)`` with the self-diagonal at -inf.
+
+    Follows ``scripts/bench_attention_core.py:69-71`` and
+    ``src/agents/mappo.py:210-211`` (division by sqrt(d), masked_fill of the
+    identity). Computed in the dtype of ``q``.
+    """
+    d = q.shape[-1]
+    s = np.matmul(q, np.swapaxes(k, -1, -2)) / q.dtype.type(np.sqrt(d))
+    n = q.shape[1]
+    s[:, np.arange(n), np.arange(n)] = -np.inf
+    return s
+
+
+def softmax(x: np.ndarray, axis: int = -1) -> np.ndarray:
+    """Numerically stable softmax (``torch.softmax`` semantics on finite rows)."""
+    m = np.max(x, axis=axis, keepdims=True)
+    e = np.exp(x - m)
+    return e / np.sum(e, axis=axis, keepdims=True)
+
+
+def k_eff(topk: int, n: int) -> int:
+    """``min(max(topk, 1), N - 1)`` -- ``src/agents/mappo.py:171-172``."""
+    return min(max(int(topk), 1), n - 1)
+
+
+def dense_unfused(q, k, v):
+    """``softmax(S) V`` -- ``scripts/bench_attention_core.py:74-75``;
+    ``src/agents/mappo.py:361-372,418``."""
+    return np.matmul(softmax(scores(q, k)), v)
+
+
+def topk_indices(s: np.ndarray, topk: int) -> np.ndarray:
+    """Indices of the ``topk`` largest entries of each row, ordered by
+    (score descending, index ascending).
+
+    The reference calls ``Tensor.topk(sorted=False)`` (``mappo.py:217``),
+    which documents no tie rule; this build fixes the rule of the reference's
+    fused kernels, "ties keep the lower index"
+    (``src/kernels/streaming_topk_attention.py:37-44``). A stable sort of the
+    negated row gives exactly that order.
+    """
+    order = np.argsort(-s, axis=-1, kind="stable")
+    return order[..., :topk]
+
+
+def gather_rows(x: np.ndarray, idx: np.ndarray) -> np.ndarray:
+    """``x[b, idx[b, i, j], :]`` -> ``[B, N, k, d]`` (``Tensor.gather`` on dim 1)."""
+    b = np.arange(x.shape[0])[:, None, None]
+    return x[b, idx]
+
+
+def topk_gather(q, k, v, topk):
+    """Score-then-select top-k attention, gathered aggregation.
+
+    ``src/agents/mappo.py:192-231``; ``scripts/bench_attention_core.py:94-101``;
+    ``src/kernels/fused_topk_attention.py:390-402``.
+    Returns ``(out[B,N,d], idx[B,N,k])``.
+    """
+    n = q.shape[1]
+    kk = k_eff(topk, n)
+    s = scores(q, k)
+    idx = topk_indices(s, kk)
+    w = softmax(np.take_along_axis(s, idx, axis=-1))
+    out = np.einsum("bnk,bnkd->bnd", w, gather_rows(v, idx))
+    return out, idx
+
+
+def topk_masked(q, k, v, topk):
+    """Dense softmax, a {0,1} top-k mask on the weights, renormalise, dense PV.
+
+    ``scripts/bench_attention_core.py:85-91``; ``src/agents/mappo.py:374-382``.
+    """
+    n = q.shape[1]
+    kk = k_eff(topk, n)
+    w = softmax(scores(q, k))
+    idx = topk_indices(w, kk)
+    keep = np.zeros_like(w)
+    np.put_along_axis(keep, idx, 1.0, axis=-1)
+    w = w * keep
+    w = w / np.maximum(w.sum(-1, keepdims=True), 1e-8)
+    return np.matmul(w, v)
+
+
+#: The standard shift-and-mask bit spread ("part 1 by 1"), the same table as
+#: ``src/kernels/prescore_selection.py:51-52``.
+_SPREAD = ((16, 0x0000FFFF), (8, 0x00FF00FF), (4, 0x0F0F0F0F),
+           (2, 0x33333333), (1, 0x55555555))
+
+
+def spread_bits(x: np.ndarray) -> np.ndarray:
+    """Insert a zero bit between consecutive bits -- ``prescore_selection.py:55-59``."""
+    x = x.astype(np.int64)
+    for shift, mask in _SPREAD:
+        x = (x | (x << shift)) & mask
+    return x
+
+
+def morton_code(pos: np.ndarray, bits: int = 10) -> np.ndarray:
+    """Per-batch normalised, quantised, interleaved 2-D Morton code.
+
+    ``src/kernels/prescore_selection.py:62-68``: fp32 ``amin/amax`` over the
+    agents, ``span.clamp_min(1e-6)``, ``((pos - lo) / span * (2**bits - 1))``
+    truncated to int64 and clamped, then x in the even bits and y in the odd.
+    ``pos`` must be float32 (the arithmetic is the fp32 arithmetic torch does).
+    """
+    pos = np.asarray(pos, dtype=np.float32)
+    lo = pos.min(axis=1, keepdims=True)
+    hi = pos.max(axis=1, keepdims=True)
+    span = np.maximum(hi - lo, np.float32(1e-6))
+    top = (1 << bits) - 1
+    g = ((pos - lo) / span * np.float32(top)).astype(np.int64)
+    g = np.clip(g, 0, top)
+    return spread_bits(g[..., 0]) | (spread_bits(g[..., 1]) << 1)
+
+
+def morton_order(code: np.ndarray) -> np.ndarray:
+    """Agents in curve order, equal codes by agent index (stable sort).
+
+    The reference's ``argsort`` (``prescore_selection.py:75``) is not stable;
+    this build pins equal codes to ascending agent index.
+    """
+    return np.argsort(code, axis=-1, kind="stable")
+
+
+def window_offsets(k: int) -> np.ndarray:
+    """``+1..+ceil(k/2)`` then ``-1..-floor(k/2)`` -- ``prescore_selection.py:80-82``."""
+    half = (k + 1) // 2
+    return np.array(list(range(1, half + 1)) + [-o for o in range(1, k - half + 1)],
+                    dtype=np.int64)
+
+
+def select_morton_window(pos: np.ndarray, k: int, bits: int = 10) -> np.ndarray:
+    """k peers adjacent along the Z-order curve, wrapping at the ends.
+
+    ``src/kernels/prescore_selection.py:71-84`` (``bits`` is fixed to 10 there;
+    it is a parameter here so the 16-bit configuration can be checked).
+    Returns int64 ``[B, N, k]`` in offset order.
+    """
+    B, N, _ = pos.shape
+    order = morton_order(morton_code(pos, bits))
+    rank = np.empty_like(order)
+    np.put_along_axis(rank, order, np.broadcast_to(np.arange(N), (B, N)), axis=-1)
+    nr = (rank[..., None] + window_offsets(k)[None, None, :]) % N
+    return np.take_along_axis(order, nr.reshape(B, N * k), axis=1).reshape(B, N, k)
+
+
+def prescore_attention(q, k, v, idx):
+    """Attention over a given peer set -- ``src/kernels/prescore_selection.py:184-195``
+    (gather K and V rows, k scores divided by sqrt(d), softmax, contract); the
+    same function as ``src/kernels/fused_prescore_attention.py:27-114``."""
+    d = q.shape[-1]
+    kg = gather_rows(k, idx)
+    vg = gather_rows(v, idx)
+    s = np.einsum("bnd,bnkd->bnk", q, kg) / q.dtype.type(np.sqrt(d))
+    return np.einsum("bnk,bnkd->bnd", softmax(s), vg)
+
+
+def zorder_attention(q, k, v, pos, topk, bits=10):
+    """``prescore_attention(select_morton_window(pos, k))`` --
+    ``src/agents/mappo.py:265-292``; ``scripts/bench_prescore.py:253-257``."""
+    idx = select_morton_window(pos, topk, bits)
+    return prescore_attention(q, k, v, idx), idx
+
+
+def near_tie_rows(s: np.ndarray, topk: int, eps: np.ndarray | float) -> np.ndarray:
+    """Rows whose k-th and (k+1)-th largest scores are within ``eps``.
+
+    On these rows the retained set legitimately depends on the rounding of the
+    scores (the reference attributes such rows in
+    ``scripts/verify_all_configurations.py:160-213``)."""
+    srt = -np.sort(-s, axis=-1)
+    if topk >= s.shape[-1]:
+        return np.zeros(s.shape[:-1], dtype=bool)
+    gap = srt[..., topk - 1] - srt[..., topk]
+    return gap <= eps
+
+
+def score_error_bound(q, k) -> np.ndarray:
+    """Forward error bound for an fp32 dot of length d, ``[B, N, N]``:
+    ``gamma_{d+1} * sum_c |q_c k_c| / sqrt(d)`` with ``gamma_m = m u / (1 - m u)``."""
+    d = q.shape[-1]
+    u = 2.0 ** -24
+    g = (d + 1) * u / (1 - (d + 1) * u)
+    a = np.matmul(np.abs(q.astype(np.float64)), np.abs(np.swapaxes(k, -1, -2)).astype(np.float64))
+    return 2 * g * a / np.sqrt(d)
+
+
+# ---------------------------------------------------------------------------
+# canonical-order C oracle (bit-exact twin of the HIP score rounding)
+# ---------------------------------------------------------------------------
+
+_LIB = None
+
+
+def _lib():
+    global _LIB
+    if _LIB is None:
+        path = _HERE / "_build" / "libtarmac_oracle.so"
+        if not path.exists():
+            build()
+        _LIB = ctypes.CDLL(str(path))
+        f = ctypes.c_void_p
+        i = ctypes.c_int
+        _LIB.or_canon_scores.argtypes = [f, f, i, i, i, f]
+        _LIB.or_canon_topk.argtypes = [f, f, f, i, i, i, i, f, f]
+        _LIB.or_morton_codes.argtypes = [f, i, i, i, f]
+        _LIB.or_morton_window.argtypes = [f, i, i, i, i, f]
+        _LIB.or_fixedset.argtypes = [f, f, f, f, i, i, i, i, f]
+        _LIB.or_dense.argtypes = [f, f, f, i, i, i, f]
+        for fn in (_LIB.or_canon_scores, _LIB.or_canon_topk, _LIB.or_morton_codes,
+                   _LIB.or_morton_window, _LIB.or_fixedset, _LIB.or_dense):
+            fn.restype = ctypes.c_int
+    return _LIB
+
+
+def build() -> None:
+    """Compile ``tarmac_oracle.c`` with gcc (no contraction, explicit fmaf)."""
+    import subprocess
+    out = _HERE / "_build"
+    out.mkdir(exist_ok=True)
+    subprocess.run(["make", "-s", "-C", str(_HERE)], check=True)
+    assert (out / "libtarmac_oracle.so").exists()
+
+
+def _ptr(a: np.ndarray):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def canon_scores(q, k) -> np.ndarray:
+    """fp32 scores in the HIP kernels' rounding order, ``[B, N, N]``, -inf diagonal."""
+    q, k = _f32(q), _f32(k)
+    B, N, d = q.shape
+    s = np.empty((B, N, N), np.float32)
+    rc = _lib().or_canon_scores(_ptr(q), _ptr(k), B, N, d, _ptr(s))
+    assert rc == 0, rc
+    return s
+
+
+def canon_topk(q, k, v, topk):
+    """Canonical fp32 selection + float64 aggregation. Returns (out f64, idx i32)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B, N, d = q.shape
+    kk = k_eff(topk, N)
+    out = np.empty((B, N, d), np.float64)
+    idx = np.empty((B, N, kk), np.int32)
+    rc = _lib().or_canon_topk(_ptr(q), _ptr(k), _ptr(v), B, N, d, kk, _ptr(out), _ptr(idx))
+    assert rc == 0, rc
+    return out, idx
+
+
+def canon_morton_codes(pos, bits) -> np.ndarray:
+    pos = _f32(pos)
+    B, N, _ = pos.shape
+    codes = np.empty((B, N), np.int64)
+    rc = _lib().or_morton_codes(_ptr(pos), B, N, bits, _ptr(codes))
+    assert rc == 0, rc
+    return codes
+
+
+def canon_morton_window(pos, k, bits) -> np.ndarray:
+    pos = _f32(pos)
+    B, N, _ = pos.shape
+    idx = np.empty((B, N, k), np.int64)
+    rc = _lib().or_morton_window(_ptr(pos), B, N, k, bits, _ptr(idx))
+    assert rc == 0, rc
+    return idx
+
+
+def canon_fixedset(q, k, v, idx):
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    idx = np.ascontiguousarray(idx, dtype=np.int64)
+    B, N, d = q.shape
+    kk = idx.shape[-1]
+    out = np.empty((B, N, d), np.float64)
+    rc = _lib().or_fixedset(_ptr(q), _ptr(k), _ptr(v), _ptr(idx), kk, B, N, d, _ptr(out))
+    assert rc == 0, rc
+    return out
+
+
+def canon_dense(q, k, v):
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B, N, d = q.shape
+    out = np.empty((B, N, d), np.float64)
+    rc = _lib().or_dense(_ptr(q), _ptr(k), _ptr(v), B, N, d, _ptr(out))
+    assert rc == 0, rc
+    return out
+
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16 (round to nearest even) -> float32, as ``Tensor.to(bf16)``."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32)
+
+
+__all__ = [n for n in dir() if not n.startswith("_")]
+del os

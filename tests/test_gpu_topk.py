@@ -1,0 +1,166 @@
+"""Fused and streaming top-k on the GPU against the oracle.
+
+fp32 bar: retained indices bit-exact against the canonical-order C oracle
+(same score rounding as the kernel), in the same (score desc, index asc) order
+for k <= 8; outputs within 1e-5 of max|ref| (normwise relative) against the
+float64 restatement of the reference's gather path wherever the k-th score is
+not a near-tie. bf16 bar: every retained set is admissible under the bf16-MFMA
+score error bound, and outputs are within 1e-2 of max|ref| against a float64
+evaluation over the kernel's own retained set.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import tarmac_oracle as O
+from conftest import qkv
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-5
+BF16_TOL = 1e-2
+
+
+def dev(*xs, dtype=torch.float32):
+    return [torch.from_numpy(np.ascontiguousarray(x)).to("cuda").to(dtype) for x in xs]
+
+
+def run_topk(q, k, v, kk, chunk=None):
+    from tarmac.kernels import topk_attention
+    qd, kd, vd = dev(q, k, v)
+    out, idx = topk_attention(qd, kd, vd, kk, return_indices=True, key_chunk=chunk)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), idx.cpu().numpy()
+
+
+def check_f32(q, k, v, kk, out, idx, exact_order=True):
+    out_c, idx_c = O.canon_topk(q, k, v, kk)
+    if exact_order:
+        assert np.array_equal(idx, idx_c), "retained indices differ from the canonical oracle"
+    else:
+        assert np.array_equal(np.sort(idx, -1), np.sort(idx_c, -1))
+    scale = max(np.abs(out_c).max(), 1e-30)
+    assert np.abs(out - out_c).max() <= F32_TOL * scale
+    # against the float64 reference path, off near-ties
+    out_r, idx_r = O.topk_gather(q.astype(np.float64), k.astype(np.float64),
+                                 v.astype(np.float64), kk)
+    s64 = O.scores(q.astype(np.float64), k.astype(np.float64))
+    amb = O.near_tie_rows(s64, kk, O.score_error_bound(q, k).max(-1))
+    same = np.all(np.sort(idx, -1) == np.sort(idx_r, -1), -1)
+    assert np.all(same | amb)
+    if same.any():
+        assert np.abs(out - out_r)[same].max() <= F32_TOL * max(np.abs(out_r).max(), 1e-30)
+
+
+CASES = [
+    (6, 16, 2), (6, 16, 1), (6, 8, 5), (2, 16, 1), (17, 16, 3), (32, 16, 1), (32, 16, 4),
+    (64, 8, 2), (64, 32, 2), (100, 16, 2), (128, 64, 1), (256, 16, 1), (256, 16, 2),
+    (256, 16, 4), (256, 32, 4), (384, 16, 2), (512, 16, 8), (512, 64, 3), (1024, 16, 2),
+    (1024, 16, 7),
+]
+
+
+@pytest.mark.parametrize("N,d,kk", CASES)
+def test_fused_topk_f32_parity(N, d, kk):
+    B = max(2, min(16, 4096 // N))
+    q, k, v = qkv(N * 131 + d * 17 + kk, B, N, d)
+    out, idx = run_topk(q, k, v, kk)
+    check_f32(q, k, v, kk, out, idx)
+
+
+@pytest.mark.parametrize("N,d,kk,chunk", [(256, 16, 2, 16), (256, 16, 4, 64), (300, 32, 1, 128),
+                                          (1024, 16, 2, 256), (2048, 16, 1, 256)])
+def test_streaming_topk_matches_fused_bitwise(N, d, kk, chunk):
+    B = 4
+    q, k, v = qkv(7 * N + kk, B, N, d)
+    out_s, idx_s = run_topk(q, k, v, kk, chunk=chunk)
+    out_f, idx_f = run_topk(q, k, v, kk)
+    assert np.array_equal(idx_s, idx_f)
+    assert np.array_equal(out_s, out_f)
+    check_f32(q, k, v, kk, out_s, idx_s)
+
+
+@pytest.mark.parametrize("N,d,kk", [(12, 16, 11), (24, 8, 23), (64, 16, 9), (200, 32, 40),
+                                    (300, 16, 299)])
+def test_wide_k_parity(N, d, kk):
+    q, k, v = qkv(N + 3 * kk, 3, N, d)
+    out, idx = run_topk(q, k, v, kk)
+    check_f32(q, k, v, kk, out, idx, exact_order=False)
+    assert np.all(np.diff(idx, axis=-1) > 0)  # ascending index order above k = 8
+
+
+def test_k_equal_n_minus_1_is_dense():
+    from tarmac.kernels import fused_dense_attention, fused_topk_attention
+    for N in (3, 6, 12, 24):
+        q, k, v = qkv(N, 3, N, 16)
+        qd, kd, vd = dev(q, k, v)
+        a = fused_topk_attention(qd, kd, vd, N - 1)
+        b = fused_dense_attention(qd, kd, vd)
+        assert (a - b).abs().max().item() < 1e-6
+
+
+def test_exact_ties_keep_lower_index():
+    """Duplicate key rows give bit-identical scores; zero queries tie everything."""
+    B, N, d = 4, 64, 16
+    q, k, v = qkv(5, B, N, d)
+    k[:, 1::2] = k[:, 0::2]        # keys 2j and 2j+1 identical
+    q[:, 0] = 0.0                  # query 0: all scores +0 -> lowest indices 1, 2, ...
+    for kk in (1, 2, 3, 4, 8):
+        out, idx = run_topk(q, k, v, kk)
+        check_f32(q, k, v, kk, out, idx)
+        assert idx[:, 0].tolist() == [list(range(1, kk + 1))] * B
+
+
+def test_topk_clamp_and_default_tiling():
+    from tarmac.kernels import (fused_topk_attention, fused_topk_attention_tiled,
+                                streaming_topk_attention)
+    q, k, v = qkv(11, 2, 6, 16)
+    qd, kd, vd = dev(q, k, v)
+    a = fused_topk_attention(qd, kd, vd, 99)     # clamped to N-1
+    b = fused_topk_attention_tiled(qd, kd, vd, 5)
+    c = fused_topk_attention(qd, kd, vd, 0)      # clamped to 1
+    d_ = streaming_topk_attention(qd, kd, vd, 1)
+    assert torch.equal(a, b) and torch.equal(c, d_)
+    out, idx = streaming_topk_attention(qd, kd, vd, 2, return_indices=True)
+    assert idx.dtype == torch.int32 and idx.shape == (2, 6, 2)
+
+
+def test_headline_shape_properties():
+    """B=1024, N=256, d=16, k=2 (the metric point): full-size properties, and
+    a sample of batch rows against the canonical oracle."""
+    B, N, d, kk = 1024, 256, 16, 2
+    q, k, v = qkv(1234 + 7 * N + d, B, N, d)
+    out, idx = run_topk(q, k, v, kk)
+    assert np.isfinite(out).all()
+    assert not np.any(idx == np.arange(N)[None, :, None])
+    assert np.all(idx[..., 0] != idx[..., 1])
+    rows = np.random.default_rng(0).choice(B, 48, replace=False)
+    check_f32(q[rows], k[rows], v[rows], kk, out[rows], idx[rows])
+
+
+@pytest.mark.parametrize("N,d,kk", [(64, 16, 1), (256, 16, 2), (256, 32, 4), (512, 64, 2),
+                                    (100, 16, 3), (1024, 16, 1), (256, 64, 12)])
+def test_topk_bf16(N, d, kk):
+    from tarmac.kernels import topk_attention
+    B = 8
+    q, k, v = qkv(77 + N + d, B, N, d)
+    qb, kb, vb = (O.bf16_round(x) for x in (q, k, v))
+    qd, kd, vd = dev(q, k, v, dtype=torch.bfloat16)
+    out, idx = topk_attention(qd, kd, vd, kk, return_indices=True)
+    torch.cuda.synchronize()
+    out = out.float().cpu().numpy()
+    idx = idx.cpu().numpy()
+    s = O.scores(qb.astype(np.float64), kb.astype(np.float64))
+    # admissible: no unselected score beats a selected one by more than the bound
+    eps = 2.0 * O.score_error_bound(qb, kb) + 1e-30
+    sel = np.zeros_like(s, dtype=bool)
+    np.put_along_axis(sel, idx.astype(np.int64), True, -1)
+    worst_sel = np.where(sel, s + eps, np.inf).min(-1)
+    best_out = np.where(sel | np.isneginf(s), -np.inf, s).max(-1)
+    assert np.all(best_out <= worst_sel)
+    ref = O.prescore_attention(qb.astype(np.float64), kb.astype(np.float64),
+                               vb.astype(np.float64), idx.astype(np.int64))
+    assert np.abs(out - ref).max() <= BF16_TOL * np.abs(ref).max()

@@ -1,0 +1,365 @@
+"""Pin the CPU oracle before trusting it (CPU only).
+
+Each oracle function is checked against something that is not a retyping of
+its own formula: a library routine (torch in float64), a closed form, brute
+force on tiny inputs, or golden vectors written by the reference's own code
+(tests/golden/make_golden.py). The mutation tests at the end plant plausible
+mistakes in copies of the oracle and check that these pins catch them.
+"""
+
+from __future__ import annotations
+
+import itertools
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+import tarmac_oracle as O
+from conftest import qkv
+
+F64 = np.float64
+
+
+def _sdpa_ref(q, k, v):
+    """torch's SDPA in float64 with the -inf diagonal mask (a library routine)."""
+    N = q.shape[1]
+    mask = torch.zeros(N, N, dtype=torch.float64)
+    mask.masked_fill_(torch.eye(N, dtype=torch.bool), float("-inf"))
+    t = [torch.from_numpy(np.asarray(x, F64)).unsqueeze(1) for x in (q, k, v)]
+    return torch.nn.functional.scaled_dot_product_attention(*t, attn_mask=mask).squeeze(1).numpy()
+
+
+# ---------------------------------------------------------------------------
+# pins as reusable predicates (so the mutation tests can run them on mutants)
+# ---------------------------------------------------------------------------
+
+def pin_scores(scores_fn) -> bool:
+    q, k, _ = qkv(1, 3, 9, 16, F64)
+    s = scores_fn(q, k)
+    ref = torch.matmul(torch.from_numpy(q), torch.from_numpy(k).transpose(-1, -2)).numpy() / 4.0
+    off = ~np.eye(9, dtype=bool)[None].repeat(3, 0)
+    ok = np.allclose(s[off], ref[off], rtol=1e-12, atol=1e-12)
+    ok &= bool(np.all(np.isneginf(s[:, np.arange(9), np.arange(9)])))
+    # unit-vector closed form: q = e_c gives column c of K / sqrt(d)
+    e = np.zeros((1, 4, 16)); e[0, :, :4] = np.eye(4)
+    kk = np.random.default_rng(3).standard_normal((1, 4, 16))
+    s2 = scores_fn(e, kk)
+    for i in range(4):
+        for j in range(4):
+            if i != j:
+                ok &= abs(s2[0, i, j] - kk[0, j, i] / 4.0) < 1e-15
+    return bool(ok)
+
+
+def pin_dense(dense_fn) -> bool:
+    q, k, v = qkv(2, 4, 11, 16, F64)
+    out = dense_fn(q, k, v)
+    ok = np.allclose(out, _sdpa_ref(q, k, v), rtol=1e-12, atol=1e-12)
+    # constant V rows -> the output is that constant
+    vc = np.broadcast_to(np.arange(16, dtype=F64), v.shape).copy()
+    ok &= np.allclose(dense_fn(q, k, vc), vc, atol=1e-12)
+    # equal keys -> uniform weights over the N-1 peers
+    ke = np.broadcast_to(k[:, :1, :], k.shape).copy()
+    want = (v.sum(1, keepdims=True) - v) / (v.shape[1] - 1)
+    ok &= np.allclose(dense_fn(q, ke, v), want, atol=1e-12)
+    return bool(ok)
+
+
+def pin_topk_indices(topk_fn) -> bool:
+    rng = np.random.default_rng(4)
+    ok = True
+    s = rng.standard_normal((5, 7, 13))
+    for kk in (1, 2, 5, 12):
+        got = topk_fn(s, kk)
+        ref = torch.from_numpy(s).topk(kk, dim=-1).indices.numpy()  # library, tie-free rows
+        ok &= np.array_equal(np.sort(got, -1), np.sort(ref, -1))
+    # brute force: the retained set is the k-subset whose worst beats the best outside
+    row = rng.standard_normal(7)
+    for kk in range(1, 7):
+        best = [c for c in itertools.combinations(range(7), kk)
+                if min(row[list(c)]) > max(np.delete(row, list(c)), default=-np.inf)]
+        ok &= sorted(topk_fn(row[None, None], kk)[0, 0].tolist()) == list(best[0])
+    # ties keep the lower index; order is score desc then index asc
+    tied = np.array([[[0.5, 1.0, 0.25, 1.0, 1.0, -2.0]]])
+    ok &= topk_fn(tied, 2)[0, 0].tolist() == [1, 3]
+    ok &= topk_fn(tied, 4)[0, 0].tolist() == [1, 3, 4, 0]
+    ok &= topk_fn(np.array([[[0.0, -0.0, 0.0]]]), 1)[0, 0].tolist() == [0]
+    return bool(ok)
+
+
+def pin_topk_gather(gather_fn, masked_fn, dense_fn) -> bool:
+    ok = True
+    for N in (6, 12, 24):
+        for kk in (1, 2, 3, N - 1):
+            q, k, v = qkv(N * 100 + kk, 8, N, 8, F64)
+            a = masked_fn(q, k, v, kk)
+            b, idx = gather_fn(q, k, v, kk)
+            ok &= float(np.abs(a - b).max()) < 1e-10       # test_comm_module.py:322-344
+            ok &= idx.shape == (8, N, kk)
+            ok &= not np.any(idx == np.arange(N)[None, :, None])  # never self
+        q, k, v = qkv(N, 3, N, 8, F64)
+        ok &= float(np.abs(gather_fn(q, k, v, N - 1)[0] - dense_fn(q, k, v)).max()) < 1e-12
+    return bool(ok)
+
+
+def _morton_bitloop(g0, g1, bits):
+    c = 0
+    for b in range(bits):
+        c |= ((g0 >> b) & 1) << (2 * b)
+        c |= ((g1 >> b) & 1) << (2 * b + 1)
+    return c
+
+
+def pin_morton(code_fn, golden) -> bool:
+    ok = True
+    for name in ("m6", "m64", "m512", "mgrid", "mflat", "mline"):
+        pos = golden[f"{name}_pos"]
+        for bits in (10, 16):
+            ok &= np.array_equal(code_fn(pos, bits), golden[f"{name}_code{bits}"].astype(np.int64))
+    # the interleave itself, against a bit-by-bit loop on every 8-bit pair
+    g = np.arange(256)
+    x, y = np.meshgrid(g, g, indexing="ij")
+    spread = O.spread_bits(x.ravel()) | (O.spread_bits(y.ravel()) << 1)
+    ok &= all(int(spread[i]) == _morton_bitloop(int(a), int(b), 8)
+              for i, (a, b) in enumerate(zip(x.ravel(), y.ravel())) if i % 37 == 0)
+    return bool(ok)
+
+
+# ---------------------------------------------------------------------------
+# the pins, applied to the oracle
+# ---------------------------------------------------------------------------
+
+def test_scores_pinned():
+    assert pin_scores(O.scores)
+
+
+def test_dense_pinned():
+    assert pin_dense(O.dense_unfused)
+
+
+def test_dense_rows_are_distributions_excluding_self():
+    q, k, _ = qkv(5, 4, 6, 16, F64)
+    w = O.softmax(O.scores(q, k))
+    assert np.allclose(w.sum(-1), 1.0, atol=1e-12)
+    assert np.abs(w[:, np.arange(6), np.arange(6)]).max() == 0.0
+
+
+def test_topk_indices_pinned():
+    assert pin_topk_indices(O.topk_indices)
+
+
+def test_topk_gather_pinned():
+    assert pin_topk_gather(O.topk_gather, O.topk_masked, O.dense_unfused)
+
+
+def test_topk_exactly_k_nonzero_weights():
+    for N in (6, 12):
+        for kk in (1, 2, N - 1):
+            q, k, v = qkv(N + kk, 3, N, 16, F64)
+            s = O.scores(q, k)
+            idx = O.topk_indices(s, kk)
+            w = np.zeros_like(s)
+            np.put_along_axis(w, idx, O.softmax(np.take_along_axis(s, idx, -1)), -1)
+            assert np.all((w > 0).sum(-1) == kk)
+            assert np.allclose(w.sum(-1), 1.0, atol=1e-12)
+
+
+def test_k_eff_clamp():
+    assert [O.k_eff(k, 6) for k in (-3, 0, 1, 5, 6, 99)] == [1, 1, 1, 5, 5, 5]
+
+
+def test_morton_pinned(golden):
+    assert pin_morton(O.morton_code, golden)
+
+
+def test_morton_window_golden(golden):
+    """select_morton_window against the reference's own outputs (bits = 10),
+    on batch rows whose codes are distinct (the reference's argsort is not
+    stable, so rows with equal codes have no pinned order)."""
+    checked = 0
+    for name in ("m6", "m64", "m512", "mgrid"):
+        pos = golden[f"{name}_pos"]
+        distinct = golden[f"{name}_distinct10"]
+        for kk in (1, 2, 3, 4):
+            key = f"{name}_win{kk}"
+            if key not in golden:
+                continue
+            got = O.select_morton_window(pos, kk, 10)
+            ref = golden[key].astype(np.int64)
+            for b in np.flatnonzero(distinct):
+                assert np.array_equal(got[b], ref[b]), (name, kk, b)
+                checked += 1
+    assert checked >= 10
+
+
+@pytest.mark.parametrize("N,kk", [(6, 1), (6, 2), (6, 4), (12, 3), (64, 5)])
+def test_morton_window_properties(N, kk):
+    rng = np.random.default_rng(N * 10 + kk)
+    pos = (rng.random((16, N, 2)) * 2 - 1).astype(np.float32)
+    idx = O.select_morton_window(pos, kk, 16)
+    assert idx.shape == (16, N, kk)
+    assert not np.any(idx == np.arange(N)[None, :, None])
+    srt = np.sort(idx, -1)
+    assert np.all(srt[..., 1:] != srt[..., :-1])
+    # curve neighbours, from an independent ordering by the bit-loop code
+    half = (kk + 1) // 2
+    offs = list(range(1, half + 1)) + [-o for o in range(1, kk - half + 1)]
+    for b in range(4):
+        lo, hi = pos[b].min(0), pos[b].max(0)
+        span = np.maximum(hi - lo, np.float32(1e-6))
+        g = ((pos[b] - lo) / span * np.float32(65535)).astype(np.int64).clip(0, 65535)
+        codes = [_morton_bitloop(int(x), int(y), 16) for x, y in g]
+        order = sorted(range(N), key=lambda i: (codes[i], i))
+        rank = {a: r for r, a in enumerate(order)}
+        for i in range(N):
+            assert set(idx[b, i].tolist()) == {order[(rank[i] + o) % N] for o in offs}
+
+
+def test_prescore_equals_dense_restricted_to_selected():
+    """src tests/test_zorder_comm.py:74-89, on the oracle."""
+    q, k, v = qkv(9, 5, 10, 16, F64)
+    rng = np.random.default_rng(9)
+    pos = rng.random((5, 10, 2)).astype(np.float32)
+    idx = O.select_morton_window(pos, 3, 10)
+    got = O.prescore_attention(q, k, v, idx)
+    s = O.scores(q, k)
+    keep = np.zeros_like(s, dtype=bool)
+    np.put_along_axis(keep, idx, True, -1)
+    w = O.softmax(np.where(keep, np.matmul(q, np.swapaxes(k, -1, -2)) / 4.0, -np.inf))
+    assert np.abs(got - w @ v).max() < 1e-12
+
+
+# ---------------------------------------------------------------------------
+# the canonical-order C oracle
+# ---------------------------------------------------------------------------
+
+def _rf32(fr: Fraction) -> np.float32:
+    """Correctly rounded Fraction -> float32 (round to nearest even)."""
+    if fr == 0:
+        return np.float32(0.0)
+    x = np.float32(float(fr))
+    best = None
+    for c in (np.nextafter(x, np.float32(-np.inf)), x, np.nextafter(x, np.float32(np.inf))):
+        e = abs(Fraction(float(c)) - fr)
+        if best is None or e < best[0] or (e == best[0] and int(c.view(np.uint32)) & 1 == 0):
+            best = (e, c)
+    return best[1]
+
+
+def test_canon_scores_match_exact_fmaf_chain():
+    """Brute force: the C oracle's score equals an exactly-rounded fmaf chain in
+    slot order (c = kk*(d/4)+t), times fp32(1/sqrt(d))."""
+    for d in (8, 16, 32):
+        q, k, _ = qkv(d, 1, 5, d)
+        s = O.canon_scores(q, k)
+        sc = np.float32(1.0 / np.sqrt(d))
+        for i in range(5):
+            for j in range(5):
+                if i == j:
+                    continue
+                acc = np.float32(0.0)
+                for t in range(d // 4):
+                    for kk in range(4):
+                        c = kk * (d // 4) + t
+                        acc = _rf32(Fraction(float(q[0, i, c])) * Fraction(float(k[0, j, c]))
+                                    + Fraction(float(acc)))
+                want = _rf32(Fraction(float(acc)) * Fraction(float(sc)))
+                assert s[0, i, j] == want, (d, i, j)
+
+
+@pytest.mark.parametrize("N,d,kk", [(6, 16, 2), (32, 16, 1), (64, 8, 4), (100, 32, 3), (128, 64, 8)])
+def test_canon_topk_matches_float64_oracle(N, d, kk):
+    q, k, v = qkv(N * 131 + d * 17 + kk, 6, N, d)
+    out_c, idx_c = O.canon_topk(q, k, v, kk)
+    out_r, idx_r = O.topk_gather(q.astype(F64), k.astype(F64), v.astype(F64), kk)
+    s64 = O.scores(q.astype(F64), k.astype(F64))
+    ambiguous = O.near_tie_rows(s64, kk, O.score_error_bound(q, k).max(-1))
+    same = np.all(np.sort(idx_c, -1) == np.sort(idx_r, -1), -1)
+    assert np.all(same | ambiguous)
+    assert ambiguous.mean() < 0.01
+    scale = np.abs(out_r).max()
+    assert np.abs(out_c - out_r)[same].max() <= 1e-6 * scale
+
+
+def test_canon_morton_matches_numpy_oracle(golden):
+    for name in ("m6", "m64", "m512", "mgrid", "mflat", "mline"):
+        pos = golden[f"{name}_pos"]
+        for bits in (10, 16):
+            assert np.array_equal(O.canon_morton_codes(pos, bits), O.morton_code(pos, bits))
+            n = pos.shape[1]
+            for kk in (1, 2, min(5, n - 1)):
+                assert np.array_equal(O.canon_morton_window(pos, kk, bits),
+                                      O.select_morton_window(pos, kk, bits))
+
+
+def test_canon_dense_and_fixedset():
+    q, k, v = qkv(21, 3, 17, 16)
+    ref = O.dense_unfused(q.astype(F64), k.astype(F64), v.astype(F64))
+    assert np.abs(O.canon_dense(q, k, v) - ref).max() < 1e-12
+    pos = np.random.default_rng(2).random((3, 17, 2)).astype(np.float32)
+    idx = O.select_morton_window(pos, 4, 16)
+    ref = O.prescore_attention(q.astype(F64), k.astype(F64), v.astype(F64), idx)
+    assert np.abs(O.canon_fixedset(q, k, v, idx) - ref).max() < 1e-12
+
+
+def test_bf16_round_matches_torch():
+    x = np.random.default_rng(0).standard_normal(4096).astype(np.float32) * 100
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(O.bf16_round(x), want)
+
+
+# ---------------------------------------------------------------------------
+# planted mistakes: the pins must reject these mutants
+# ---------------------------------------------------------------------------
+
+def test_pins_reject_planted_mistakes(golden):
+    def scores_mul_sqrt(q, k):         # multiplies by sqrt(d) instead of dividing
+        s = O.scores(q, k)
+        return s * q.shape[-1]
+
+    def scores_no_mask(q, k):          # forgets the self-diagonal
+        return np.matmul(q, np.swapaxes(k, -1, -2)) / np.sqrt(q.shape[-1])
+
+    def scores_transposed(q, k):       # Q^T K-style index mix-up (S_ji)
+        return np.swapaxes(O.scores(q, k), -1, -2) if q is not k else O.scores(q, k)
+
+    assert not pin_scores(scores_mul_sqrt)
+    assert not pin_scores(scores_no_mask)
+
+    def dense_uses_k_for_v(q, k, v):
+        return np.matmul(O.softmax(O.scores(q, k)), k)
+
+    def dense_transposed_weights(q, k, v):
+        return np.matmul(np.swapaxes(O.softmax(O.scores(q, k)), -1, -2), v)
+
+    assert not pin_dense(dense_uses_k_for_v)
+    assert not pin_dense(dense_transposed_weights)
+    assert not pin_dense(lambda q, k, v: np.matmul(O.softmax(scores_transposed(q, k)), v))
+
+    assert not pin_topk_indices(lambda s, kk: np.argsort(s, -1, kind="stable")[..., :kk])
+    assert not pin_topk_indices(lambda s, kk: np.argsort(-s, -1, kind="stable")[..., -kk:])
+    # ties resolved to the higher index
+    assert not pin_topk_indices(
+        lambda s, kk: (s.shape[-1] - 1 - np.argsort(-s[..., ::-1], -1, kind="stable"))[..., :kk])
+
+    def gather_softmax_all(q, k, v, topk):   # softmax over all N, not the kept k
+        out, idx = O.topk_gather(q, k, v, topk)
+        w = O.softmax(O.scores(q, k))
+        return np.einsum("bnk,bnkd->bnd", np.take_along_axis(w, idx, -1), O.gather_rows(v, idx)), idx
+
+    assert not pin_topk_gather(gather_softmax_all, O.topk_masked, O.dense_unfused)
+
+    def morton_swapped_axes(pos, bits):
+        return O.morton_code(pos[..., ::-1].copy(), bits)
+
+    def morton_rounding(pos, bits):     # rounds instead of truncating
+        pos = np.asarray(pos, np.float32)
+        lo, hi = pos.min(1, keepdims=True), pos.max(1, keepdims=True)
+        span = np.maximum(hi - lo, np.float32(1e-6))
+        g = np.rint((pos - lo) / span * np.float32((1 << bits) - 1)).astype(np.int64)
+        return O.spread_bits(g[..., 0]) | (O.spread_bits(g[..., 1]) << 1)
+
+    assert not pin_morton(morton_swapped_axes, golden)
+    assert not pin_morton(morton_rounding, golden)

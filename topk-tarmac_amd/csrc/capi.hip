@@ -1,0 +1,197 @@
+// extern "C" boundary of libtarmac.so: argument validation, launch-shape
+// policy, error reporting. Declarations and reference citations: include/tarmac.h.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/tarmac.h"
+#include "tarmac_internal.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return TARMAC_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(TARMAC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+constexpr size_t kLdsBudget = 64 * 1024;
+
+float inv_sqrt(int d) { return static_cast<float>(1.0 / std::sqrt(static_cast<double>(d))); }
+
+int check_core(const void* q, const void* k, const void* v, const void* out, int B, int N, int d,
+               int dtype, const char* fn) {
+  if (!q || !k || !v || !out) return fail(TARMAC_ERR_INVALID, "%s: null tensor pointer", fn);
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16))
+    return fail(TARMAC_ERR_INVALID, "%s: q, k, v and out must be 16-byte aligned", fn);
+  if (B < 1 || N < 2)
+    return fail(TARMAC_ERR_INVALID, "%s: need B >= 1 and N >= 2 (got B=%d, N=%d)", fn, B, N);
+  if (dtype == tarmac::kF32) {
+    if (d != 8 && d != 16 && d != 32 && d != 64)
+      return fail(TARMAC_ERR_UNSUPPORTED, "%s: fp32 head dim must be 8, 16, 32 or 64 (got %d)", fn, d);
+  } else if (dtype == tarmac::kBf16) {
+    if (d != 16 && d != 32 && d != 64)
+      return fail(TARMAC_ERR_UNSUPPORTED, "%s: bf16 head dim must be 16, 32 or 64 (got %d)", fn, d);
+  } else {
+    return fail(TARMAC_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
+  }
+  if (static_cast<long long>(B) * N * d >= (1ll << 40))
+    return fail(TARMAC_ERR_UNSUPPORTED, "%s: tensor too large", fn);
+  return TARMAC_OK;
+}
+
+// Largest multiple of 16 keys whose padded LDS copy fits the budget.
+int max_topk_chunk(int dtype, int d) {
+  const int row = tarmac::topk_lds_row_bytes(dtype, d);
+  int kc = static_cast<int>(kLdsBudget / row) / 16 * 16;
+  return kc < 16 ? 16 : kc;
+}
+
+int topk_common(const void* q, const void* k, const void* v, void* out, int32_t* idx_out, int B,
+                int N, int d, int topk, int dtype, int key_chunk, void* stream, const char* fn) {
+  int rc = check_core(q, k, v, out, B, N, d, dtype, fn);
+  if (rc) return rc;
+  if (topk < 1 || topk > N - 1)
+    return fail(TARMAC_ERR_INVALID, "%s: need 1 <= topk <= N-1 (got topk=%d, N=%d)", fn, topk, N);
+  if (idx_out && !aligned(idx_out, 4)) return fail(TARMAC_ERR_INVALID, "%s: idx_out misaligned", fn);
+  if (topk > tarmac::kTopkSmallMax && N + topk > 16384)
+    return fail(TARMAC_ERR_UNSUPPORTED, "%s: topk > 8 needs N + topk <= 16384", fn);
+  const int kmax = max_topk_chunk(dtype, d);
+  const int n16 = (N + 15) / 16 * 16;
+  int kc;
+  if (key_chunk <= 0) {
+    kc = n16 < kmax ? n16 : kmax;
+  } else {
+    if (key_chunk % 16 != 0)
+      return fail(TARMAC_ERR_INVALID, "%s: key_chunk must be a multiple of 16 (got %d)", fn, key_chunk);
+    if (key_chunk > kmax)
+      return fail(TARMAC_ERR_UNSUPPORTED, "%s: key_chunk %d exceeds the LDS budget (max %d at d=%d)",
+                  fn, key_chunk, kmax, d);
+    kc = key_chunk;
+  }
+  tarmac::TopkArgs a{q, k, v, out, idx_out, B, N, d, topk, dtype, kc, inv_sqrt(d), stream};
+  return hip_status(tarmac::run_topk(a), fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+int tarmac_abi_version(void) { return 1; }
+
+const char* tarmac_last_error(void) { return g_last_error.c_str(); }
+
+int tarmac_dense_fwd(const void* q, const void* k, const void* v, void* out, int B, int N, int d,
+                     int dtype, int key_chunk, void* stream) {
+  const char* fn = "tarmac_dense_fwd";
+  int rc = check_core(q, k, v, out, B, N, d, dtype, fn);
+  if (rc) return rc;
+  int kc = key_chunk;
+  if (kc <= 0) {
+    kc = (N + 63) / 64 * 64;
+    while (kc > 64 && tarmac::dense_lds_bytes(dtype, d, kc) > kLdsBudget) kc -= 64;
+  } else if (kc % 16 != 0) {
+    return fail(TARMAC_ERR_INVALID, "%s: key_chunk must be a multiple of 16 (got %d)", fn, kc);
+  }
+  if (tarmac::dense_lds_bytes(dtype, d, kc) > kLdsBudget)
+    return fail(TARMAC_ERR_UNSUPPORTED, "%s: key_chunk %d exceeds the LDS budget at d=%d", fn, kc, d);
+  tarmac::DenseArgs a{q, k, v, out, B, N, d, dtype, kc, inv_sqrt(d), stream};
+  return hip_status(tarmac::run_dense(a), fn);
+}
+
+int tarmac_topk_fused_fwd(const void* q, const void* k, const void* v, void* out, int32_t* idx_out,
+                          int B, int N, int d, int topk, int dtype, void* stream) {
+  return topk_common(q, k, v, out, idx_out, B, N, d, topk, dtype, 0, stream, "tarmac_topk_fused_fwd");
+}
+
+int tarmac_topk_stream_fwd(const void* q, const void* k, const void* v, void* out,
+                           int32_t* idx_out, int B, int N, int d, int topk, int dtype,
+                           int key_chunk, void* stream) {
+  const char* fn = "tarmac_topk_stream_fwd";
+  if (key_chunk <= 0) key_chunk = 256;
+  const int kmax = max_topk_chunk(dtype, d);
+  if (key_chunk > kmax) key_chunk = kmax;
+  return topk_common(q, k, v, out, idx_out, B, N, d, topk, dtype, key_chunk, stream, fn);
+}
+
+int tarmac_fixedset_fwd(const void* q, const void* k, const void* v, const void* idx,
+                        int idx_dtype, int kk, void* out, int B, int N, int d, int dtype,
+                        void* stream) {
+  const char* fn = "tarmac_fixedset_fwd";
+  int rc = check_core(q, k, v, out, B, N, d, dtype, fn);
+  if (rc) return rc;
+  if (kk < 1) return fail(TARMAC_ERR_INVALID, "%s: need kk >= 1 (got %d)", fn, kk);
+  if (!idx) return fail(TARMAC_ERR_INVALID, "%s: null idx", fn);
+  if (idx_dtype != TARMAC_IDX_I32 && idx_dtype != TARMAC_IDX_I64)
+    return fail(TARMAC_ERR_INVALID, "%s: unknown idx dtype %d", fn, idx_dtype);
+  if (!aligned(idx, idx_dtype == TARMAC_IDX_I64 ? 8 : 4))
+    return fail(TARMAC_ERR_INVALID, "%s: idx misaligned", fn);
+  tarmac::FixedsetArgs a{q, k, v, idx, idx_dtype == TARMAC_IDX_I64, out, B, N, d, kk, dtype,
+                         inv_sqrt(d), stream};
+  return hip_status(tarmac::run_fixedset(a), fn);
+}
+
+int tarmac_morton_window(const float* pos, void* idx_out, int idx_dtype, int64_t* codes_out,
+                         int B, int N, int k, int bits, void* stream) {
+  const char* fn = "tarmac_morton_window";
+  if (!pos) return fail(TARMAC_ERR_INVALID, "%s: null pos", fn);
+  if (!aligned(pos, 8)) return fail(TARMAC_ERR_INVALID, "%s: pos must be 8-byte aligned", fn);
+  if (B < 1 || N < 2) return fail(TARMAC_ERR_INVALID, "%s: need B >= 1 and N >= 2", fn);
+  if (bits < 1 || bits > 16) return fail(TARMAC_ERR_INVALID, "%s: bits must be 1..16 (got %d)", fn, bits);
+  if (idx_out) {
+    if (k < 1 || k > N - 1)
+      return fail(TARMAC_ERR_INVALID, "%s: need 1 <= k <= N-1 (got k=%d, N=%d)", fn, k, N);
+    if (idx_dtype != TARMAC_IDX_I32 && idx_dtype != TARMAC_IDX_I64)
+      return fail(TARMAC_ERR_INVALID, "%s: unknown idx dtype %d", fn, idx_dtype);
+    if (!aligned(idx_out, idx_dtype == TARMAC_IDX_I64 ? 8 : 4))
+      return fail(TARMAC_ERR_INVALID, "%s: idx_out misaligned", fn);
+  }
+  if (codes_out && !aligned(codes_out, 8)) return fail(TARMAC_ERR_INVALID, "%s: codes_out misaligned", fn);
+  if (tarmac::zorder_lds_bytes(N) > kLdsBudget)
+    return fail(TARMAC_ERR_UNSUPPORTED, "%s: N=%d exceeds the per-row sort capacity", fn, N);
+  tarmac::MortonArgs a{pos, idx_out, idx_dtype == TARMAC_IDX_I64, codes_out, B, N, k, bits, stream};
+  return hip_status(tarmac::run_morton_window(a), fn);
+}
+
+int tarmac_zorder_fwd(const void* q, const void* k, const void* v, const float* pos, void* out,
+                      int32_t* idx_out, int B, int N, int d, int topk, int bits, int dtype,
+                      void* stream) {
+  const char* fn = "tarmac_zorder_fwd";
+  int rc = check_core(q, k, v, out, B, N, d, dtype, fn);
+  if (rc) return rc;
+  if (!pos || !aligned(pos, 8)) return fail(TARMAC_ERR_INVALID, "%s: pos null or misaligned", fn);
+  if (topk < 1 || topk > N - 1)
+    return fail(TARMAC_ERR_INVALID, "%s: need 1 <= topk <= N-1 (got topk=%d, N=%d)", fn, topk, N);
+  if (bits < 1 || bits > 16) return fail(TARMAC_ERR_INVALID, "%s: bits must be 1..16 (got %d)", fn, bits);
+  if (idx_out && !aligned(idx_out, 4)) return fail(TARMAC_ERR_INVALID, "%s: idx_out misaligned", fn);
+  if (tarmac::zorder_lds_bytes(N) > kLdsBudget)
+    return fail(TARMAC_ERR_UNSUPPORTED, "%s: N=%d exceeds the per-row sort capacity", fn, N);
+  tarmac::ZorderArgs a{q, k, v, pos, out, idx_out, B, N, d, topk, bits, dtype, inv_sqrt(d), stream};
+  return hip_status(tarmac::run_zorder(a), fn);
+}
+
+int tarmac_noop(float* out, void* stream) {
+  if (!out) return fail(TARMAC_ERR_INVALID, "tarmac_noop: null out");
+  return hip_status(tarmac::run_noop(out, stream), "tarmac_noop");
+}
+
+}  // extern "C"

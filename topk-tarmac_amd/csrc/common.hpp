@@ -1,0 +1,76 @@
+// Shared device helpers for the TarMAC attention-core kernels (gfx950 / CDNA4).
+//
+// Layout conventions used by every kernel in this directory:
+//   * q, k, v, out are row-major contiguous [B, N, d] (fp32 or bf16);
+//   * one wavefront (64 lanes) owns a tile of 16 query rows;
+//   * scores are formed as an S^T tile (16 keys x 16 queries) with MFMA, so
+//     after the instruction lane l holds the four scores of query (l % 16)
+//     against keys 4*(l/16) + r, r = 0..3 -- every lane works on exactly one
+//     query and selection / softmax state stays in that lane's registers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tarmac {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t bf16;  // raw bfloat16 storage
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(bf16 h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (the rounding Tensor.to(torch.bfloat16) uses).
+__device__ __forceinline__ bf16 f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<bf16>(u >> 16);
+}
+
+// D += A(16x4) * B(4x16), fp32. Lane l supplies A[l%16][l/16] and B[l/16][l%16];
+// returns D[4*(l/16)+r][l%16] in element r. Rounds like a sequential fmaf chain
+// over the four contraction slots, in slot order.
+__device__ __forceinline__ f32x4 mfma_f32_16x16x4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// D += A(16x16) * B(16x16), bf16 inputs, fp32 accumulate. Lane l supplies
+// A[l%16][4*(l/16)+e] and B[4*(l/16)+e][l%16], e = 0..3.
+__device__ __forceinline__ f32x4 mfma_bf16_16x16x16(i16x4 a, i16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// D += A(16x32) * B(32x16), bf16 inputs (gfx950). Lane l supplies
+// A[l%16][8*(l/16)+e] and B[8*(l/16)+e][l%16], e = 0..7.
+__device__ __forceinline__ f32x4 mfma_bf16_16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (id % 8). Remap the
+// hardware id so that consecutive logical ids run on the same XCD and share
+// its L2 (all query tiles of one batch row read the same K and V).
+__device__ __forceinline__ int xcd_logical_block(int hw, int nblocks) {
+  constexpr int X = 8;
+  const int q = nblocks / X, r = nblocks % X;
+  const int x = hw % X, local = hw / X;
+  return (x < r) ? x * (q + 1) + local : r * (q + 1) + (x - r) * q + local;
+}
+
+__device__ __forceinline__ bool is_pow2_scale(float s) {
+  uint32_t u = __float_as_uint(s);
+  return (u & 0x007fffffu) == 0u;
+}
+
+// (a, ia) ranks before (b, ib): higher score first, lower index on ties.
+__device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
+  return a > b || (a == b && ia < ib);
+}
+
+}  // namespace tarmac

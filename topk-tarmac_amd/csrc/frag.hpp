@@ -1,0 +1,194 @@
+// Register / LDS fragments for the score contraction S^T = K_tile * Q_tile^T.
+//
+// The query tile (MFMA B operand) lives in registers for a wave's whole pass
+// over the keys; the key tile (A operand) is read from an LDS copy of K whose
+// rows are padded to break bank conflicts.
+//
+// fp32: d/4 chained v_mfma_f32_16x16x4_f32. Contraction slot kk (= lane/16) of
+// instruction t carries element c = kk*(d/4) + t, so each lane reads d/4
+// contiguous elements of its row. The resulting rounding is the "canonical"
+// score order restated in oracle/tarmac_oracle.c.
+// bf16: v_mfma_f32_16x16x16_bf16 (d = 16) or v_mfma_f32_16x16x32_bf16
+// (d = 32, 64), fp32 accumulation.
+#pragma once
+
+#include "common.hpp"
+
+namespace tarmac {
+
+template <int E>
+__device__ __forceinline__ void ld_f32(float (&dst)[E], const float* src) {
+  if constexpr (E % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < E / 4; ++i) {
+      f32x4 v = *reinterpret_cast<const f32x4*>(src + 4 * i);
+      dst[4 * i] = v[0]; dst[4 * i + 1] = v[1]; dst[4 * i + 2] = v[2]; dst[4 * i + 3] = v[3];
+    }
+  } else if constexpr (E == 2) {
+    f32x2 v = *reinterpret_cast<const f32x2*>(src);
+    dst[0] = v[0]; dst[1] = v[1];
+  } else {
+#pragma unroll
+    for (int i = 0; i < E; ++i) dst[i] = src[i];
+  }
+}
+
+template <int E>
+__device__ __forceinline__ void st_f32(float* dst, const float (&src)[E]) {
+  if constexpr (E % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < E / 4; ++i) {
+      f32x4 v = {src[4 * i], src[4 * i + 1], src[4 * i + 2], src[4 * i + 3]};
+      *reinterpret_cast<f32x4*>(dst + 4 * i) = v;
+    }
+  } else if constexpr (E == 2) {
+    f32x2 v = {src[0], src[1]};
+    *reinterpret_cast<f32x2*>(dst) = v;
+  } else {
+#pragma unroll
+    for (int i = 0; i < E; ++i) dst[i] = src[i];
+  }
+}
+
+// E bf16 elements (E a multiple of 4) -> fp32.
+template <int E>
+__device__ __forceinline__ void ld_bf16(float (&dst)[E], const bf16* src) {
+  static_assert(E % 4 == 0, "bf16 vector width");
+#pragma unroll
+  for (int i = 0; i < E / 4; ++i) {
+    uint2 v = *reinterpret_cast<const uint2*>(src + 4 * i);
+    dst[4 * i + 0] = __uint_as_float(v.x << 16);
+    dst[4 * i + 1] = __uint_as_float(v.x & 0xffff0000u);
+    dst[4 * i + 2] = __uint_as_float(v.y << 16);
+    dst[4 * i + 3] = __uint_as_float(v.y & 0xffff0000u);
+  }
+}
+
+template <int E>
+__device__ __forceinline__ void st_bf16(bf16* dst, const float (&src)[E]) {
+  static_assert(E % 4 == 0, "bf16 vector width");
+#pragma unroll
+  for (int i = 0; i < E / 4; ++i) {
+    uint2 v;
+    v.x = static_cast<uint32_t>(f32_to_bf16(src[4 * i])) |
+          (static_cast<uint32_t>(f32_to_bf16(src[4 * i + 1])) << 16);
+    v.y = static_cast<uint32_t>(f32_to_bf16(src[4 * i + 2])) |
+          (static_cast<uint32_t>(f32_to_bf16(src[4 * i + 3])) << 16);
+    *reinterpret_cast<uint2*>(dst + 4 * i) = v;
+  }
+}
+
+template <typename T, int E>
+__device__ __forceinline__ void ld_row(float (&dst)[E], const T* src) {
+  if constexpr (sizeof(T) == 4) ld_f32<E>(dst, reinterpret_cast<const float*>(src));
+  else ld_bf16<E>(dst, reinterpret_cast<const bf16*>(src));
+}
+
+template <typename T, int E>
+__device__ __forceinline__ void st_row(T* dst, const float (&src)[E]) {
+  if constexpr (sizeof(T) == 4) st_f32<E>(reinterpret_cast<float*>(dst), src);
+  else st_bf16<E>(reinterpret_cast<bf16*>(dst), src);
+}
+
+template <typename T, int D>
+struct Frag;
+
+// ---- fp32 -----------------------------------------------------------------
+template <int D>
+struct Frag<float, D> {
+  static_assert(D % 4 == 0 && D >= 8 && D <= 64, "fp32 head dim must be 8..64, multiple of 4");
+  static constexpr int E = D / 4;       // elements per lane = MFMAs per tile
+  static constexpr int LDK = D + 4;     // padded LDS row stride, in elements
+  float q[E];
+
+  // qrow: start of this lane's query row. pre: 1 or the power-of-two scale.
+  __device__ __forceinline__ void load_q(const float* qrow, int grp, float pre) {
+    ld_f32<E>(q, qrow + grp * E);
+#pragma unroll
+    for (int t = 0; t < E; ++t) q[t] *= pre;
+  }
+  // krow: LDS row of key (tile base + lane % 16).
+  __device__ __forceinline__ f32x4 score(const float* krow, int grp) const {
+    float kf[E];
+    ld_f32<E>(kf, krow + grp * E);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < E; ++t) acc = mfma_f32_16x16x4(kf[t], q[t], acc);
+    return acc;
+  }
+};
+
+// ---- bf16 -----------------------------------------------------------------
+__device__ __forceinline__ bf16 scale_bf16(bf16 x, float pre) {
+  return f32_to_bf16(bf16_to_f32(x) * pre);  // exact for a power-of-two pre
+}
+
+template <>
+struct Frag<bf16, 16> {
+  static constexpr int LDK = 16 + 8;
+  i16x4 q;
+  __device__ __forceinline__ void load_q(const bf16* qrow, int grp, float pre) {
+    uint2 v = *reinterpret_cast<const uint2*>(qrow + 4 * grp);
+    bf16 e[4] = {static_cast<bf16>(v.x), static_cast<bf16>(v.x >> 16),
+                 static_cast<bf16>(v.y), static_cast<bf16>(v.y >> 16)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = static_cast<short>(scale_bf16(e[i], pre));
+  }
+  __device__ __forceinline__ f32x4 score(const bf16* krow, int grp) const {
+    i16x4 kf = *reinterpret_cast<const i16x4*>(krow + 4 * grp);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    return mfma_bf16_16x16x16(kf, q, acc);
+  }
+};
+
+template <int D>
+struct FragBf16Wide {
+  static_assert(D == 32 || D == 64, "bf16 wide fragment");
+  static constexpr int NI = D / 32;     // 16x16x32 instructions per tile
+  static constexpr int LDK = D + 8;
+  bf16x8 q[NI];
+  __device__ __forceinline__ void load_q(const bf16* qrow, int grp, float pre) {
+#pragma unroll
+    for (int h = 0; h < NI; ++h) {
+      const bf16* p = qrow + 32 * h + 8 * grp;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        bf16 x = scale_bf16(p[e], pre);
+        q[h][e] = __builtin_bit_cast(__bf16, x);
+      }
+    }
+  }
+  __device__ __forceinline__ f32x4 score(const bf16* krow, int grp) const {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int h = 0; h < NI; ++h) {
+      bf16x8 kf = *reinterpret_cast<const bf16x8*>(krow + 32 * h + 8 * grp);
+      acc = mfma_bf16_16x16x32(kf, q[h], acc);
+    }
+    return acc;
+  }
+};
+
+template <>
+struct Frag<bf16, 32> : FragBf16Wide<32> {};
+template <>
+struct Frag<bf16, 64> : FragBf16Wide<64> {};
+
+// Cooperative copy of `rows` rows of a [*, D] matrix into LDS with row stride
+// LDK, zero-filling rows [rows, rows_pad). 16-byte vectors; every thread of
+// the workgroup participates.
+template <typename T, int D, int LDK>
+__device__ __forceinline__ void stage_rows(T* lds, const T* src, int rows, int rows_pad) {
+  constexpr int VE = 16 / sizeof(T);
+  constexpr int VPR = D / VE;
+  static_assert(D % VE == 0 && (LDK * sizeof(T)) % 16 == 0, "16-byte staging");
+  const int total = rows_pad * VPR;
+  for (int v = threadIdx.x; v < total; v += blockDim.x) {
+    const int row = v / VPR, cv = v - row * VPR;
+    uint4 x = make_uint4(0u, 0u, 0u, 0u);
+    if (row < rows) x = *reinterpret_cast<const uint4*>(src + static_cast<size_t>(row) * D + cv * VE);
+    *reinterpret_cast<uint4*>(lds + row * LDK + cv * VE) = x;
+  }
+}
+
+}  // namespace tarmac

@@ -1,0 +1,87 @@
+// Internal launch descriptors shared by the kernels and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace tarmac {
+
+enum Dtype : int { kF32 = 0, kBf16 = 1 };
+
+constexpr int kTopkSmallMax = 8;  // k handled by the register-list kernel
+
+inline int next_pow2(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
+struct TopkArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  int32_t* idx;     // nullable: retained indices [B, N, topk]
+  int B, N, d, topk, dtype;
+  int key_chunk;    // keys per LDS chunk (multiple of 16)
+  float scale;      // fp32(1/sqrt(d))
+  void* stream;
+};
+
+struct DenseArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  int B, N, d, dtype;
+  int key_chunk;
+  float scale;
+  void* stream;
+};
+
+struct FixedsetArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* idx;
+  int idx_is_i64;
+  void* out;
+  int B, N, d, kk, dtype;
+  float scale;
+  void* stream;
+};
+
+struct MortonArgs {
+  const float* pos;
+  void* idx;          // nullable
+  int idx_is_i64;
+  int64_t* codes;     // nullable: Morton codes [B, N]
+  int B, N, k, bits;
+  void* stream;
+};
+
+struct ZorderArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* pos;
+  void* out;
+  int32_t* idx;  // nullable
+  int B, N, d, topk, bits, dtype;
+  float scale;
+  void* stream;
+};
+
+hipError_t run_topk(const TopkArgs& a);
+hipError_t run_dense(const DenseArgs& a);
+hipError_t run_fixedset(const FixedsetArgs& a);
+hipError_t run_morton_window(const MortonArgs& a);
+hipError_t run_zorder(const ZorderArgs& a);
+hipError_t run_noop(float* out, void* stream);
+
+int topk_lds_row_bytes(int dtype, int d);
+size_t dense_lds_bytes(int dtype, int d, int kc);
+size_t zorder_lds_bytes(int N);
+
+}  // namespace tarmac

@@ -1,0 +1,372 @@
+// Score-then-select top-k attention, fused: scores, selection, k-softmax and
+// the gathered aggregation in one launch; no score row, index tensor or
+// gathered value tensor reaches HBM.
+//
+// Reference behaviour: src/kernels/fused_topk_attention.py:211-333
+// (fused_topk_attention_tiled) and src/kernels/streaming_topk_attention.py:
+// 66-258 (streaming_topk_attention, incl. the optional retained-index output).
+//
+// Small k (1..8), one launch shape for both the resident and the streamed
+// variants:
+//   * workgroup = (batch row b, block of 16*nw queries), nw waves;
+//   * keys are staged through LDS in chunks of `kc` rows (kc >= N: the whole
+//     K[b] is resident; otherwise the chunks stream);
+//   * each wave forms 16x16 S^T tiles with MFMA; lane l owns query l%16 and,
+//     per tile, the 4 keys 4*(l/16)+r, so the four lanes l, l^16, l^32, l^48
+//     see disjoint interleaved key subsets of one query, each in ascending key
+//     order;
+//   * every lane keeps a sorted (score desc, index asc) list of its best k in
+//     registers; strict '>' insertion keeps the lower index on ties;
+//   * two xor-shuffle merge steps (16, 32) combine the four lists, after which
+//     the 4 lanes of a query each compute d/4 output channels from the k
+//     gathered V rows.
+//
+// Large k (> 8): one wave per query, the score row in LDS, an exact threshold
+// found by bisection on the order-preserving integer key, ties at the
+// threshold resolved to the lowest indices.
+#include "frag.hpp"
+#include "tarmac_internal.hpp"
+
+namespace tarmac {
+
+constexpr int kIdxSentinel = 0x3fffffff;
+
+template <int K>
+__device__ __forceinline__ void topk_insert(float (&val)[K], int (&ix)[K], float s, int j) {
+  // New keys arrive in ascending index order, so a strict '>' keeps the
+  // earlier (lower-index) entry ahead on equal scores.
+#pragma unroll
+  for (int m = K - 1; m > 0; --m) {
+    const bool cm = s > val[m];
+    const bool cp = s > val[m - 1];
+    val[m] = cp ? val[m - 1] : (cm ? s : val[m]);
+    ix[m] = cp ? ix[m - 1] : (cm ? j : ix[m]);
+  }
+  const bool c0 = s > val[0];
+  val[0] = c0 ? s : val[0];
+  ix[0] = c0 ? j : ix[0];
+}
+
+template <int K>
+__device__ __forceinline__ void topk_insert_lex(float (&val)[K], int (&ix)[K], float s, int j) {
+#pragma unroll
+  for (int m = K - 1; m > 0; --m) {
+    const bool cm = ranks_before(s, j, val[m], ix[m]);
+    const bool cp = ranks_before(s, j, val[m - 1], ix[m - 1]);
+    const float vm = val[m - 1];
+    const int im = ix[m - 1];
+    val[m] = cp ? vm : (cm ? s : val[m]);
+    ix[m] = cp ? im : (cm ? j : ix[m]);
+  }
+  const bool c0 = ranks_before(s, j, val[0], ix[0]);
+  val[0] = c0 ? s : val[0];
+  ix[0] = c0 ? j : ix[0];
+}
+
+template <typename T, int D, int K>
+__global__ void __launch_bounds__(256)
+topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
+                  T* __restrict__ O, int32_t* __restrict__ Idx, int N, int n_qblk, int kc,
+                  float scale, int nblocks) {
+  using F = Frag<T, D>;
+  constexpr int LDK = F::LDK;
+  constexpr int EO = D / 4;  // output channels per lane
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* Ks = reinterpret_cast<T*>(smem_raw);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int blk = xcd_logical_block(blockIdx.x, nblocks);
+  const int b = blk / n_qblk, qblk = blk - b * n_qblk;
+  const int q0 = qblk * (16 * nw) + wave * 16;
+  const int col = lane & 15, grp = lane >> 4;
+  const int qi = q0 + col;
+  const size_t boff = static_cast<size_t>(b) * N * D;
+  const bool pow2 = is_pow2_scale(scale);
+
+  F frag;
+  frag.load_q(Q + boff + static_cast<size_t>(min(qi, N - 1)) * D, grp, pow2 ? scale : 1.f);
+
+  float val[K];
+  int ix[K];
+#pragma unroll
+  for (int m = 0; m < K; ++m) { val[m] = -INFINITY; ix[m] = kIdxSentinel; }
+
+  for (int c0 = 0; c0 < N; c0 += kc) {
+    const int cn = min(kc, N - c0);
+    const int cn16 = (cn + 15) & ~15;
+    __syncthreads();
+    stage_rows<T, D, LDK>(Ks, Kx + boff + static_cast<size_t>(c0) * D, cn, cn16);
+    __syncthreads();
+    if (q0 < N) {
+      for (int kb = 0; kb < cn16; kb += 16) {
+        f32x4 s = frag.score(Ks + (kb + col) * LDK, grp);
+        if (!pow2) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s[r] *= scale;
+        }
+        const int kabs = c0 + kb;
+        const int kend = c0 + cn;  // rows past the chunk end are zero padding
+        if (kabs == q0 || kabs + 16 > kend) {  // wave-uniform: diagonal or ragged tile
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = kabs + 4 * grp + r;
+            if (key >= kend || key == qi) s[r] = -INFINITY;
+          }
+        }
+        // index recorded without the lane-group offset (uniform), added after
+#pragma unroll
+        for (int r = 0; r < 4; ++r) topk_insert<K>(val, ix, s[r], kabs + r);
+      }
+    }
+  }
+  if (q0 >= N) return;
+
+#pragma unroll
+  for (int m = 0; m < K; ++m) ix[m] += 4 * grp;
+
+#pragma unroll
+  for (int step = 16; step <= 32; step <<= 1) {
+    float pv[K];
+    int pi[K];
+#pragma unroll
+    for (int m = 0; m < K; ++m) {
+      pv[m] = __shfl_xor(val[m], step);
+      pi[m] = __shfl_xor(ix[m], step);
+    }
+#pragma unroll
+    for (int m = 0; m < K; ++m) topk_insert_lex<K>(val, ix, pv[m], pi[m]);
+  }
+
+  if (qi >= N) return;
+  const float mx = val[0];
+  float acc[EO];
+#pragma unroll
+  for (int c = 0; c < EO; ++c) acc[c] = 0.f;
+  float den = 0.f;
+#pragma unroll
+  for (int m = 0; m < K; ++m) {
+    const float w = expf(val[m] - mx);
+    den += w;
+    const int row = min(max(ix[m], 0), N - 1);
+    float vr[EO];
+    ld_row<T, EO>(vr, V + boff + static_cast<size_t>(row) * D + grp * EO);
+#pragma unroll
+    for (int c = 0; c < EO; ++c) acc[c] = fmaf(w, vr[c], acc[c]);
+  }
+#pragma unroll
+  for (int c = 0; c < EO; ++c) acc[c] = acc[c] / den;
+  st_row<T, EO>(O + boff + static_cast<size_t>(qi) * D + grp * EO, acc);
+  if (Idx != nullptr && grp == 0) {
+    int32_t* dst = Idx + (static_cast<size_t>(b) * N + qi) * K;
+#pragma unroll
+    for (int m = 0; m < K; ++m) dst[m] = ix[m];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// large k: one wave per query row
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int ordered_key(float x) {
+  // Monotone fp32 -> int32 (src/kernels/fused_topk_attention.py:113-124).
+  const int i = __float_as_int(x);
+  return i ^ ((i >> 31) & 0x7fffffff);
+}
+
+__device__ __forceinline__ int wave_sum(int x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+template <typename T, int D>
+__device__ __forceinline__ float canon_score(const float (&q)[D], const T* krow) {
+  // Same fmaf order as the MFMA chain: slot kk of step t holds c = kk*(D/4)+t.
+  float kf[D];
+  ld_row<T, D>(kf, krow);
+  float acc = 0.f;
+#pragma unroll
+  for (int t = 0; t < D / 4; ++t)
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) acc = fmaf(q[kk * (D / 4) + t], kf[kk * (D / 4) + t], acc);
+  return acc;
+}
+
+// mode 0: ties at the threshold keep the lowest indices (exact top-k).
+template <typename T, int D>
+__global__ void __launch_bounds__(256)
+topk_wide_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
+                 T* __restrict__ O, int32_t* __restrict__ Idx, int B, int N, int topk, float scale) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const long row_raw = static_cast<long>(blockIdx.x) * nw + wave;  // (b, i) flattened
+  const bool live = row_raw < static_cast<long>(B) * N;  // wave-uniform
+  const long row = live ? row_raw : 0;
+  const int b = static_cast<int>(row / N), i = static_cast<int>(row - static_cast<long>(b) * N);
+  float* S = reinterpret_cast<float*>(smem_raw) + static_cast<size_t>(wave) * (N + topk);
+  int* sel = reinterpret_cast<int*>(S + N);
+  const size_t boff = static_cast<size_t>(b) * N * D;
+  const bool pow2 = is_pow2_scale(scale);
+
+  float q[D];
+  ld_row<T, D>(q, Q + boff + static_cast<size_t>(i) * D);
+  if (pow2) {
+#pragma unroll
+    for (int c = 0; c < D; ++c) q[c] *= scale;
+  }
+  for (int j = lane; j < N; j += kWave) {
+    float s = canon_score<T, D>(q, Kx + boff + static_cast<size_t>(j) * D);
+    if (!pow2) s *= scale;
+    S[j] = (j == i) ? -INFINITY : s;
+  }
+  __syncthreads();
+
+  // Largest t with count(key >= t) >= topk.
+  long lo = -2147483648L, hi = 2147483647L;
+  while (lo < hi) {
+    const long mid = lo + (hi - lo + 1) / 2;
+    int cnt = 0;
+    for (int j = lane; j < N; j += kWave) cnt += (ordered_key(S[j]) >= mid) ? 1 : 0;
+    cnt = wave_sum(cnt);
+    if (cnt >= topk) lo = mid; else hi = mid - 1;
+  }
+  const int thr = static_cast<int>(lo);
+  int gt = 0;
+  for (int j = lane; j < N; j += kWave) gt += (ordered_key(S[j]) > thr) ? 1 : 0;
+  gt = wave_sum(gt);
+  const int need_ties = topk - gt;
+
+  // Compact the selected indices in ascending index order.
+  int taken = 0, ties = 0;
+  float mx = -INFINITY;
+  for (int j0 = 0; j0 < N; j0 += kWave) {
+    const int j = j0 + lane;
+    const int key = (j < N) ? ordered_key(S[j]) : -2147483647 - 1;
+    const bool is_tie = (j < N) && key == thr;
+    const unsigned long long tie_mask = __ballot(is_tie);
+    const int tie_rank = ties + __popcll(tie_mask & ((1ull << lane) - 1ull));
+    const bool pick = (j < N) && (key > thr || (is_tie && tie_rank < need_ties));
+    const unsigned long long pick_mask = __ballot(pick);
+    if (pick) {
+      sel[taken + __popcll(pick_mask & ((1ull << lane) - 1ull))] = j;
+      mx = fmaxf(mx, S[j]);
+    }
+    taken += __popcll(pick_mask);
+    ties += __popcll(tie_mask);
+  }
+  mx = wave_max(mx);
+  __syncthreads();
+  if (!live) return;
+
+  // Lane c < D accumulates channel c over the selected rows.
+  if (lane < D) {
+    float acc = 0.f, den = 0.f;
+    for (int m = 0; m < topk; ++m) {
+      const int j = sel[m];
+      const float w = expf(S[j] - mx);
+      den += w;
+      const T* vr = V + boff + static_cast<size_t>(j) * D + lane;
+      float x;
+      if constexpr (sizeof(T) == 4) x = *reinterpret_cast<const float*>(vr);
+      else x = bf16_to_f32(*reinterpret_cast<const bf16*>(vr));
+      acc = fmaf(w, x, acc);
+    }
+    const float o = acc / den;
+    T* dst = O + boff + static_cast<size_t>(i) * D + lane;
+    if constexpr (sizeof(T) == 4) *reinterpret_cast<float*>(dst) = o;
+    else *reinterpret_cast<bf16*>(dst) = f32_to_bf16(o);
+  }
+  if (Idx != nullptr) {
+    int32_t* dst = Idx + (static_cast<size_t>(b) * N + i) * topk;
+    for (int m = lane; m < topk; m += kWave) dst[m] = sel[m];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+
+template <typename T, int D>
+static hipError_t launch_small(const TopkArgs& a, int kc) {
+  const int nw = a.N >= 64 ? 4 : (a.N + 15) / 16;
+  const int qb = 16 * nw;
+  const int n_qblk = (a.N + qb - 1) / qb;
+  const int nblocks = a.B * n_qblk;
+  const size_t lds = static_cast<size_t>(kc) * Frag<T, D>::LDK * sizeof(T);
+  const T* q = static_cast<const T*>(a.q);
+  const T* k = static_cast<const T*>(a.k);
+  const T* v = static_cast<const T*>(a.v);
+  T* o = static_cast<T*>(a.out);
+  hipStream_t st = static_cast<hipStream_t>(a.stream);
+#define TARMAC_TOPK_CASE(KK)                                                                   \
+  case KK:                                                                                     \
+    hipLaunchKernelGGL((topk_small_kernel<T, D, KK>), dim3(nblocks), dim3(64 * nw), lds, st, \
+                       q, k, v, o, a.idx, a.N, n_qblk, kc, a.scale, nblocks);                 \
+    break;
+  switch (a.topk) {
+    TARMAC_TOPK_CASE(1)
+    TARMAC_TOPK_CASE(2)
+    TARMAC_TOPK_CASE(3)
+    TARMAC_TOPK_CASE(4)
+    TARMAC_TOPK_CASE(5)
+    TARMAC_TOPK_CASE(6)
+    TARMAC_TOPK_CASE(7)
+    TARMAC_TOPK_CASE(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef TARMAC_TOPK_CASE
+  return hipGetLastError();
+}
+
+template <typename T, int D>
+static hipError_t launch_wide(const TopkArgs& a) {
+  // nw waves per workgroup, each holding N + topk words of LDS (<= 64 KiB total)
+  int nw = 16384 / (a.N + a.topk);
+  nw = nw < 1 ? 1 : (nw > 4 ? 4 : nw);
+  const long rows = static_cast<long>(a.B) * a.N;
+  const int grid = static_cast<int>((rows + nw - 1) / nw);
+  const size_t lds = static_cast<size_t>(nw) * (a.N + a.topk) * sizeof(float);
+  hipLaunchKernelGGL((topk_wide_kernel<T, D>), dim3(grid), dim3(64 * nw), lds,
+                     static_cast<hipStream_t>(a.stream), static_cast<const T*>(a.q),
+                     static_cast<const T*>(a.k), static_cast<const T*>(a.v), static_cast<T*>(a.out),
+                     a.idx, a.B, a.N, a.topk, a.scale);
+  return hipGetLastError();
+}
+
+template <typename T, int D>
+static hipError_t dispatch_topk(const TopkArgs& a) {
+  if (a.topk > kTopkSmallMax) return launch_wide<T, D>(a);
+  return launch_small<T, D>(a, a.key_chunk);
+}
+
+hipError_t run_topk(const TopkArgs& a) {
+  if (a.dtype == kF32) {
+    switch (a.d) {
+      case 8: return dispatch_topk<float, 8>(a);
+      case 16: return dispatch_topk<float, 16>(a);
+      case 32: return dispatch_topk<float, 32>(a);
+      case 64: return dispatch_topk<float, 64>(a);
+    }
+  } else {
+    switch (a.d) {
+      case 16: return dispatch_topk<bf16, 16>(a);
+      case 32: return dispatch_topk<bf16, 32>(a);
+      case 64: return dispatch_topk<bf16, 64>(a);
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+int topk_lds_row_bytes(int dtype, int d) {
+  if (dtype == kF32) return (d + 4) * 4;
+  return (d + 8) * 2;
+}
+
+}  // namespace tarmac

