@@ -1,0 +1,331 @@
+"""Benchmark of the TarMAC attention core on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Workload (the point the metric is quoted on):
+B=1024 episodes, N=256 agents, d=16, fp32, Q/K/V ~ N(0, 1) drawn on the CPU
+from seed 1234 + 7N + d (scripts/bench_attention_core.py:341) and copied to
+HBM before timing. A "step" is one call of the fused score-then-select top-k
+core at k=2 over the whole batch (scores, selection, k-softmax, gathered
+aggregation). ``value`` is its device time per call in microseconds.
+
+Alongside, with the reference's protocol (interleaved event timing and graph
+replay, minimum over samples): the dense core, top-k at k=1/2/4, the fixed-set
+kernel given the exact top-k set (selection-time share), the streaming kernel
+at B=256 N=1024, the Z-order select+attend at B=1024 N=512 k=2
+(configs[4]), a bf16 point and the launch floor.
+
+Prints ONE JSON line. Exits non-zero (with a message) for --gpus > 1: this
+build measures one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "topk-tarmac_amd"))
+
+B, N, D = 1024, 256, 16
+KS = (1, 2, 4)
+VALUE_K = 2
+METRIC_FALLBACK = "µs/call attention core, top-k vs dense ratio, N=256 d=16 k=1,2,4; %HBM peak"
+
+
+def _metric() -> str:
+    try:
+        return json.loads((ROOT / "BASELINE.json").read_text())["metric"]
+    except Exception:
+        return METRIC_FALLBACK
+
+
+def _traffic_from_profiles(kernel_tag: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
+    f = ROOT / "profiles" / f"traffic_{kernel_tag}.txt"
+    if not f.exists():
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read_text(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(seconds_budget: float = 15.0) -> dict:
+    """The numpy oracle's top-k gather path (k=2) on a bounded sample of the
+    workload, single thread, scaled to the full batch."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import numpy as np
+    import tarmac_oracle as O
+    try:
+        from threadpoolctl import threadpool_limits
+    except Exception:  # pragma: no cover
+        threadpool_limits = None
+    bs = 64
+    rng = np.random.default_rng(1234 + 7 * N + D)
+    q, k, v = (rng.standard_normal((bs, N, D)).astype(np.float32) for _ in range(3))
+    ctx = threadpool_limits(1) if threadpool_limits else None
+    times = []
+    try:
+        if ctx:
+            ctx.__enter__()
+        O.topk_gather(q, k, v, VALUE_K)  # warm-up
+        t_end = time.perf_counter() + seconds_budget
+        while time.perf_counter() < t_end and len(times) < 30:
+            t0 = time.perf_counter()
+            O.topk_gather(q, k, v, VALUE_K)
+            times.append(time.perf_counter() - t0)
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    per_call_us = min(times) * (B / bs) * 1e6
+    return {"value": per_call_us, "unit": "µs/call", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle topk_gather (fp32, k={VALUE_K}) on {bs} of {B} batch rows "
+                      f"(N={N}, d={D}), min of {len(times)} calls, x{B // bs} to the full batch"}
+
+
+def profile_one(args, q, k, v, dev) -> int:
+    """Launch one kernel repeatedly (no timing logic) so profiler counters
+    cover a single shape."""
+    import numpy as np
+    import torch
+    from tarmac import bound
+    name = args.profile_kernel
+    if name == "dense":
+        fn = bound.dense(q, k, v)
+    elif name.startswith("topk"):
+        fn = bound.topk(q, k, v, int(name[4:]))
+    elif name == "fixedset2":
+        idx = bound.topk(q, k, v, 2, with_idx=True)
+        idx()
+        fn = bound.fixedset(q, k, v, idx.idx)
+    elif name == "stream2":
+        g = np.random.default_rng(4242)
+        q4, k4, v4 = (torch.from_numpy(g.standard_normal((256, 1024, D)).astype(np.float32)).to(dev)
+                      for _ in range(3))
+        fn = bound.topk(q4, k4, v4, 2, key_chunk=256)
+    else:  # zorder
+        g = np.random.default_rng(4242 + 512)
+        q5, k5, v5 = (torch.from_numpy(g.standard_normal((1024, 512, D)).astype(np.float32)).to(dev)
+                      for _ in range(3))
+        pos = torch.from_numpy(g.random((1024, 512, 2)).astype(np.float32)).to(dev)
+        fn = bound.zorder(q5, k5, v5, pos, 2, 16)
+    for _ in range(args.warmup + args.steps):
+        fn()
+    torch.cuda.synchronize()
+    print(json.dumps({"profiled": name, "calls": args.warmup + args.steps}), flush=True)
+    return 0
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--reps", type=int, default=40, help="interleaved repetitions per run")
+    ap.add_argument("--runs", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--value-only", action="store_true",
+                    help="time only the value kernel (for profiler runs)")
+    ap.add_argument("--profile-kernel", default=None,
+                    choices=["dense", "topk1", "topk2", "topk4", "fixedset2", "zorder", "stream2"],
+                    help="run only this kernel (headline shape; zorder/stream at their configs) "
+                         "--warmup + --steps times, for profiler counter passes")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a 64 MiB device copy (calibrates rocprofv3 byte counters)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus > 1 or world > 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the attention core shards by batch row with no exchange, so a multi-GPU run "
+              "would time the same kernel on a smaller batch.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from tarmac import bound, harness
+    from tarmac.kernels import fused_dense_attention, fused_prescore_attention, topk_attention
+    from tarmac.kernels import zorder_attention
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    rng = np.random.default_rng(1234 + 7 * N + D)
+    q, k, v = (torch.from_numpy(rng.standard_normal((B, N, D)).astype(np.float32)).to(dev)
+               for _ in range(3))
+
+    if args.profile_kernel:
+        return profile_one(args, q, k, v, dev)
+
+    # ---- timed region: K steps of the value kernel -----------------------
+    step = bound.topk(q, k, v, VALUE_K)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for s, e in evs:
+        s.record(st)
+        step()
+        e.record(st)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    dur_ms = [s.elapsed_time(e) for s, e in evs]
+    kernel_ms = sum(dur_ms) / len(dur_ms)
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+
+    flops_v = harness.analytic_flops("topk", B, N, D, VALUE_K)
+    bytes_v = harness.analytic_bytes("topk", B, N, D, VALUE_K)
+    achieved = flops_v / (kernel_ms * 1e-3)
+    line = {
+        "metric": _metric(),
+        "value": round(kernel_ms * 1e3, 3),
+        "unit": "µs/call",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: Q,K,V ~ N(0,1) fp32 from a seeded CPU generator, resident in HBM",
+        "config": {"workload": "TarMAC attention core, fused score-then-select top-k (configs[1])",
+                   "B": B, "N": N, "d": D, "k": VALUE_K, "parallelism": "none (1 GPU)"},
+        "roofline": {
+            "bound": "mfma", "achieved": round(achieved / 1e12, 3),
+            "peak": harness.PEAK_FP32_FLOPS / 1e12, "unit": "TFLOP/s",
+            "frac": round(achieved / harness.PEAK_FP32_FLOPS, 4),
+            "traffic": _traffic_from_profiles("topk_fused_k2_B1024_N256_d16"),
+            "kernel": "tarmac::topk_small_kernel<float,16,2>",
+            "algorithmic_flops_per_launch": flops_v,
+            "algorithmic_bytes_per_launch": bytes_v,
+            "hbm_frac": round(bytes_v / (kernel_ms * 1e-3) / harness.PEAK_HBM_BYTES_PER_S, 4),
+        },
+    }
+    if args.copy_probe:
+        src = torch.ones(16 << 20, device=dev)   # 64 MiB of fp32
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        line["copy_probe_bytes"] = src.numel() * 4
+    if args.value_only:
+        print(json.dumps(line), flush=True)
+        return 0
+
+    # ---- interleaved comparison at the metric point ----------------------
+    detail: dict = {}
+    idx = {kk: topk_attention(q, k, v, kk, return_indices=True)[1] for kk in KS}
+    fns = {"dense": bound.dense(q, k, v)}
+    for kk in KS:
+        fns[f"topk_k{kk}"] = bound.topk(q, k, v, kk)
+        fns[f"fixedset_k{kk}"] = bound.fixedset(q, k, v, idx[kk])
+    fns["noop"] = bound.noop(dev)
+    eager = harness.time_interleaved(fns, args.reps, 5, args.runs)
+    gfns = {"dense": lambda: fused_dense_attention(q, k, v)}
+    for kk in KS:
+        gfns[f"topk_k{kk}"] = (lambda kk=kk: topk_attention(q, k, v, kk))
+        gfns[f"fixedset_k{kk}"] = (lambda kk=kk: fused_prescore_attention(q, k, v, idx[kk]))
+    graph = harness.time_interleaved(harness.as_graphs(gfns), args.reps, 5, args.runs)
+    est = {n: harness.stats(s) for n, s in eager.items()}
+    gst = {n: harness.stats(s) for n, s in graph.items()}
+    dense_min = min(est["dense"]["min_us"], gst["dense"]["min_us"])
+    pt = {}
+    for kk in KS:
+        t_top = min(est[f"topk_k{kk}"]["min_us"], gst[f"topk_k{kk}"]["min_us"])
+        t_fix = min(est[f"fixedset_k{kk}"]["min_us"], gst[f"fixedset_k{kk}"]["min_us"])
+        pt[f"k{kk}"] = {
+            "topk_us": round(t_top, 3),
+            "ratio_vs_dense": round(t_top / dense_min, 4),
+            "paired_median_ratio_eager": round(harness.paired_ratio(eager[f"topk_k{kk}"],
+                                                                    eager["dense"]), 4),
+            "fixedset_us": round(t_fix, 3),
+            "selection_time_share": round(1.0 - t_fix / t_top, 4),
+            "mfma_frac": round(harness.analytic_flops("topk", B, N, D, kk)
+                               / (t_top * 1e-6) / harness.PEAK_FP32_FLOPS, 4),
+            "hbm_frac": round(harness.analytic_bytes("topk", B, N, D, kk)
+                              / (t_top * 1e-6) / harness.PEAK_HBM_BYTES_PER_S, 4),
+        }
+    detail["metric_point"] = {
+        "dense_us": round(dense_min, 3),
+        "dense_mfma_frac": round(harness.analytic_flops("dense", B, N, D)
+                                 / (dense_min * 1e-6) / harness.PEAK_FP32_FLOPS, 4),
+        "dense_hbm_frac": round(harness.analytic_bytes("dense", B, N, D)
+                                / (dense_min * 1e-6) / harness.PEAK_HBM_BYTES_PER_S, 4),
+        "topk": pt,
+        "launch_floor_us": round(est["noop"]["min_us"], 3),
+        "eager": {n: {kk: round(vv, 3) for kk, vv in s.items() if kk in ("min_us", "median_us")}
+                  for n, s in est.items()},
+        "graph": {n: {kk: round(vv, 3) for kk, vv in s.items() if kk in ("min_us", "median_us")}
+                  for n, s in gst.items()},
+    }
+    del fns, gfns
+
+    # ---- streaming top-k, B=256, N=1024 ------------------------
+    b4, n4 = 256, 1024
+    g4 = np.random.default_rng(4242)
+    q4, k4, v4 = (torch.from_numpy(g4.standard_normal((b4, n4, D)).astype(np.float32)).to(dev)
+                  for _ in range(3))
+    f4 = {"dense": lambda: fused_dense_attention(q4, k4, v4)}
+    for kk in KS:
+        f4[f"stream_k{kk}"] = (lambda kk=kk: topk_attention(q4, k4, v4, kk, key_chunk=256))
+    s4 = {n: harness.stats(s) for n, s in
+          harness.time_interleaved(harness.as_graphs(f4), args.reps, 5, 2).items()}
+    detail["streaming_B256_N1024"] = {
+        n: round(s["min_us"], 3) for n, s in s4.items()}
+    detail["streaming_B256_N1024"].update(
+        {f"ratio_k{kk}": round(s4[f"stream_k{kk}"]["min_us"] / s4["dense"]["min_us"], 4)
+         for kk in KS})
+    del q4, k4, v4, f4
+
+    # ---- Z-order select+attend, B=1024, N=512, k=2, 16 bits ---
+    b5, n5, k5 = 1024, 512, 2
+    g5 = np.random.default_rng(4242 + n5)
+    q5, k5t, v5 = (torch.from_numpy(g5.standard_normal((b5, n5, D)).astype(np.float32)).to(dev)
+                   for _ in range(3))
+    pos5 = torch.from_numpy(g5.random((b5, n5, 2)).astype(np.float32)).to(dev)
+    f5 = {"dense": lambda: fused_dense_attention(q5, k5t, v5),
+          "zorder_total": lambda: zorder_attention(q5, k5t, v5, pos5, k5, 16)}
+    s5 = {n: harness.stats(s) for n, s in
+          harness.time_interleaved(harness.as_graphs(f5), args.reps, 5, 2).items()}
+    tz = s5["zorder_total"]["min_us"]
+    detail["zorder_B1024_N512_k2"] = {
+        "zorder_total_us": round(tz, 3), "dense_us": round(s5["dense"]["min_us"], 3),
+        "ratio_vs_dense": round(tz / s5["dense"]["min_us"], 4),
+        "hbm_frac": round(harness.analytic_bytes("zorder", b5, n5, D, k5)
+                          / (tz * 1e-6) / harness.PEAK_HBM_BYTES_PER_S, 4)}
+    del q5, k5t, v5, pos5, f5
+
+    # ---- one bf16 point, B=1024, N=256, d=16 -------------------
+    qb, kb, vb = (t.to(torch.bfloat16) for t in (q, k, v))
+    f3 = {"dense_bf16": lambda: fused_dense_attention(qb, kb, vb)}
+    for kk in (1, 2):
+        f3[f"topk_bf16_k{kk}"] = (lambda kk=kk: topk_attention(qb, kb, vb, kk))
+    s3 = {n: harness.stats(s) for n, s in
+          harness.time_interleaved(harness.as_graphs(f3), args.reps, 5, 2).items()}
+    td = s3["dense_bf16"]["min_us"]
+    detail["bf16_B1024_N256_d16"] = {n: round(s["min_us"], 3) for n, s in s3.items()}
+    detail["bf16_B1024_N256_d16"]["dense_hbm_frac"] = round(
+        harness.analytic_bytes("dense", B, N, D, itemsize=2) / (td * 1e-6)
+        / harness.PEAK_HBM_BYTES_PER_S, 4)
+
+    line["detail"] = detail
+    line["device"] = torch.cuda.get_device_name(dev)
+    line["host"] = {"cpu": platform.processor() or platform.machine(),
+                    "affinity_cores": len(os.sched_getaffinity(0))}
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

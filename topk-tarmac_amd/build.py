@@ -26,6 +26,9 @@ HIPCC_FLAGS = [
     # keep the compiler from emitting packed-fp32 VALU ops (v_pk_*_f32)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-result",
+    # keep MFMA accumulators in arch VGPRs: the softmax / selection code reads
+    # every score, and AGPR residency costs a v_accvgpr_read per element
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -59,11 +59,11 @@ int check_core(const void* q, const void* k, const void* v, const void* out, int
   return TARMAC_OK;
 }
 
-// Largest multiple of 16 keys whose padded LDS copy fits the budget.
+// Largest multiple of 64 keys whose padded LDS copy fits the budget.
 int max_topk_chunk(int dtype, int d) {
-  const int row = tarmac::topk_lds_row_bytes(dtype, d);
-  int kc = static_cast<int>(kLdsBudget / row) / 16 * 16;
-  return kc < 16 ? 16 : kc;
+  int kc = 64;
+  while (tarmac::topk_lds_bytes(dtype, d, kc + 64) <= kLdsBudget) kc += 64;
+  return kc;
 }
 
 int topk_common(const void* q, const void* k, const void* v, void* out, int32_t* idx_out, int B,
@@ -76,14 +76,14 @@ int topk_common(const void* q, const void* k, const void* v, void* out, int32_t*
   if (topk > tarmac::kTopkSmallMax && N + topk > 16384)
     return fail(TARMAC_ERR_UNSUPPORTED, "%s: topk > 8 needs N + topk <= 16384", fn);
   const int kmax = max_topk_chunk(dtype, d);
-  const int n16 = (N + 15) / 16 * 16;
+  const int n64 = (N + 63) / 64 * 64;
   int kc;
   if (key_chunk <= 0) {
-    kc = n16 < kmax ? n16 : kmax;
+    kc = n64 < kmax ? n64 : kmax;
   } else {
     if (key_chunk % 16 != 0)
       return fail(TARMAC_ERR_INVALID, "%s: key_chunk must be a multiple of 16 (got %d)", fn, key_chunk);
-    if (key_chunk > kmax)
+    if (tarmac::topk_lds_bytes(dtype, d, key_chunk) > kLdsBudget)
       return fail(TARMAC_ERR_UNSUPPORTED, "%s: key_chunk %d exceeds the LDS budget (max %d at d=%d)",
                   fn, key_chunk, kmax, d);
     kc = key_chunk;

@@ -63,9 +63,27 @@ __device__ __forceinline__ int xcd_logical_block(int hw, int nblocks) {
   return (x < r) ? x * (q + 1) + local : r * (q + 1) + (x - r) * q + local;
 }
 
+// 2^x on the transcendental unit (v_exp_f32), without the denormal-range
+// fix-up exp2f adds: softmax terms below 2^-126 of the row maximum flush to 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+constexpr float kLog2eF = 1.4426950408889634f;
+
 __device__ __forceinline__ bool is_pow2_scale(float s) {
   uint32_t u = __float_as_uint(s);
   return (u & 0x007fffffu) == 0u;
+}
+
+// Ask the scheduler for a pipeline of NM groups {1 MFMA, VPM VALU}, preceded
+// by NDS LDS reads, within the current basic block.
+template <int NDS, int NM, int VPM>
+__device__ __forceinline__ void interleave_mfma_valu() {
+  if constexpr (NDS > 0) __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);
+#pragma unroll
+  for (int i = 0; i < NM; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+  }
 }
 
 // (a, ia) ranks before (b, ib): higher score first, lower index on ties.

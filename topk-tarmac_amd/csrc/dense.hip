@@ -22,24 +22,28 @@ namespace tarmac {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kDenseBlockTiles = 4;  // 64 keys per online-softmax step
+constexpr int kDenseQueryTiles = 2;  // 16-query tiles per wavefront
 
 template <typename T, int D>
 struct PvOperand;
 
-// fp32: O^T block h (channels 16h..16h+15) += V^T(16 x 4 keys) * P^T(4 keys x 16 q)
+// fp32: O^T block h (channels 16h..16h+15) += V^T(16 x 4 keys) * P^T(4 keys x 16 q).
+// The V^T fragment of a (tile, h) is read once and used by every query tile.
 template <int D>
 struct PvOperand<float, D> {
   static constexpr int NH = (D + 15) / 16;  // output blocks of 16 channels
   static constexpr int CP = NH * 16;        // padded channel count in LDS
-  static constexpr int LDV = 0;             // set by kernel (kc + 4)
-  __device__ __forceinline__ static void pv_tile(f32x4 (&acc)[NH], const float* Vt, int ldv,
-                                                 int kb, int lane, const float (&p)[4]) {
+  template <int QT>
+  __device__ __forceinline__ static void pv_tile(f32x4 (&acc)[QT][NH], const float* Vt, int ldv,
+                                                 int kb, int lane, const float (&p)[QT][4]) {
     const int col = lane & 15, grp = lane >> 4;
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
       const f32x4 vv = *reinterpret_cast<const f32x4*>(Vt + (16 * h + col) * ldv + kb + 4 * grp);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) acc[h] = mfma_f32_16x16x4(vv[u], p[u], acc[h]);
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) acc[qt][h] = mfma_f32_16x16x4(vv[u], p[qt][u], acc[qt][h]);
     }
   }
 };
@@ -49,16 +53,20 @@ template <int D>
 struct PvOperand<bf16, D> {
   static constexpr int NH = D / 16;
   static constexpr int CP = NH * 16;
-  __device__ __forceinline__ static void pv_tile(f32x4 (&acc)[NH], const bf16* Vt, int ldv, int kb,
-                                                 int lane, const float (&p)[4]) {
+  template <int QT>
+  __device__ __forceinline__ static void pv_tile(f32x4 (&acc)[QT][NH], const bf16* Vt, int ldv,
+                                                 int kb, int lane, const float (&p)[QT][4]) {
     const int col = lane & 15, grp = lane >> 4;
-    i16x4 pb;
+    i16x4 pb[QT];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) pb[u] = static_cast<short>(f32_to_bf16(p[u]));
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) pb[qt][u] = static_cast<short>(f32_to_bf16(p[qt][u]));
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
       const i16x4 vv = *reinterpret_cast<const i16x4*>(Vt + (16 * h + col) * ldv + kb + 4 * grp);
-      acc[h] = mfma_bf16_16x16x16(vv, pb, acc[h]);
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) acc[qt][h] = mfma_bf16_16x16x16(vv, pb[qt], acc[qt][h]);
     }
   }
 };
@@ -92,7 +100,7 @@ __device__ __forceinline__ void stage_vt(T* Vt, int ldv, const T* src, int rows,
   }
 }
 
-template <typename T, int D>
+template <typename T, int D, int QT>
 __global__ void __launch_bounds__(256)
 dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
              T* __restrict__ O, int N, int n_qblk, int kc, float scale, int nblocks) {
@@ -100,7 +108,8 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
   using PV = PvOperand<T, D>;
   constexpr int LDK = F::LDK;
   constexpr int NH = PV::NH;
-  constexpr int BK = 16 * kDenseBlockTiles;
+  constexpr int BT = kDenseBlockTiles;
+  constexpr int BK = 16 * BT;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int kcp = (kc + BK - 1) / BK * BK;  // chunk rows padded to whole blocks
   const int ldv = kcp + 4;
@@ -110,27 +119,30 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int blk = xcd_logical_block(blockIdx.x, nblocks);
   const int b = blk / n_qblk, qblk = blk - b * n_qblk;
-  const int q0 = qblk * (16 * nw) + wave * 16;
+  const int q0 = (qblk * nw + wave) * 16 * QT;
   const int col = lane & 15, grp = lane >> 4;
-  const int qi = q0 + col;
   const size_t boff = static_cast<size_t>(b) * N * D;
 
-  // Scores come out pre-multiplied by scale*log2(e), ready for exp2.
-  F frag;
-  {
-    const float pre = scale * kLog2e;
-    if constexpr (sizeof(T) == 4) {
-      frag.load_q(Q + boff + static_cast<size_t>(min(qi, N - 1)) * D, grp, pre);
-    } else {
-      frag.load_q(Q + boff + static_cast<size_t>(min(qi, N - 1)) * D, grp, 1.f);
-    }
+  // fp32 scores come out pre-multiplied by scale*log2(e), ready for exp2;
+  // bf16 scores are scaled after the product (the factor is not exact in bf16).
+  F frag[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qi = q0 + 16 * qt + col;
+    frag[qt].load_q(Q + boff + static_cast<size_t>(min(qi, N - 1)) * D, grp,
+                    sizeof(T) == 4 ? scale * kLog2e : 1.f);
   }
   const float post = (sizeof(T) == 4) ? 1.f : scale * kLog2e;
 
-  f32x4 acc[NH];
+  f32x4 acc[QT][NH];
+  float m_run[QT], l_run[QT];
 #pragma unroll
-  for (int h = 0; h < NH; ++h) acc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
+  for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+    for (int h = 0; h < NH; ++h) acc[qt][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_run[qt] = -INFINITY;
+    l_run[qt] = 0.f;
+  }
 
   for (int c0 = 0; c0 < N; c0 += kc) {
     const int cn = min(kc, N - c0);
@@ -140,76 +152,93 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
     stage_vt<T, D, PV::CP>(Vt, ldv, V + boff + static_cast<size_t>(c0) * D, cn, cnp);
     __syncthreads();
     if (q0 >= N) continue;
+    const int kend = c0 + cn;  // rows past the chunk end are zero padding
     for (int kb0 = 0; kb0 < cnp; kb0 += BK) {
-      float s[kDenseBlockTiles][4];
+      f32x4 st[QT][BT];
+      block_scores<F, QT, BT>(frag, Ks, kb0, LDK, lane, st);
+      float s[QT][BT][4];
 #pragma unroll
-      for (int t = 0; t < kDenseBlockTiles; ++t) {
-        const f32x4 st = frag.score(Ks + (kb0 + 16 * t + col) * LDK, grp);
+      for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s[t][r] = st[r] * post;
-      }
+        for (int t = 0; t < BT; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s[qt][t][r] = st[qt][t][r] * post;
       const int kabs = c0 + kb0;
-      const int kend = c0 + cn;  // rows past the chunk end are zero padding
-      if (kabs + BK > kend || (q0 >= kabs && q0 < kabs + BK)) {  // wave-uniform
+      if ((q0 < kabs + BK && kabs < q0 + 16 * QT) || kabs + BK > kend) {  // wave-uniform
 #pragma unroll
-        for (int t = 0; t < kDenseBlockTiles; ++t)
+        for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+          for (int t = 0; t < BT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int key = kabs + 16 * t + 4 * grp + r;
+              if (key >= kend || key == q0 + 16 * qt + col) s[qt][t][r] = -INFINITY;
+            }
+      }
+      float m_use[QT];
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < BT; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[qt][t][r]);
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+        const float m_new = fmaxf(m_run[qt], mloc);
+        m_use[qt] = (m_new == -INFINITY) ? 0.f : m_new;
+        const float alpha = fast_exp2(m_run[qt] - m_use[qt]);  // 0 while nothing has been seen
+        l_run[qt] *= alpha;
+#pragma unroll
+        for (int h = 0; h < NH; ++h) acc[qt][h] *= alpha;
+        m_run[qt] = m_new;
+      }
+#pragma unroll
+      for (int t = 0; t < BT; ++t) {
+        float p[QT][4];
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int key = kabs + 16 * t + 4 * grp + r;
-            if (key >= kend || key == qi) s[t][r] = -INFINITY;
+            p[qt][r] = fast_exp2(s[qt][t][r] - m_use[qt]);
+            l_run[qt] += p[qt][r];
           }
-      }
-      float mloc = -INFINITY;
-#pragma unroll
-      for (int t = 0; t < kDenseBlockTiles; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[t][r]);
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-      const float m_new = fmaxf(m_run, mloc);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = exp2f(m_run - m_use);  // 0 while nothing has been seen
-      l_run *= alpha;
-#pragma unroll
-      for (int h = 0; h < NH; ++h) acc[h] *= alpha;
-      m_run = m_new;
-#pragma unroll
-      for (int t = 0; t < kDenseBlockTiles; ++t) {
-        float p[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          p[r] = exp2f(s[t][r] - m_use);
-          l_run += p[r];
-        }
-        PV::pv_tile(acc, Vt, ldv, kb0 + 16 * t, lane, p);
+        PV::template pv_tile<QT>(acc, Vt, ldv, kb0 + 16 * t, lane, p);
       }
     }
   }
   if (q0 >= N) return;
-  float l_tot = l_run + __shfl_xor(l_run, 16);
-  l_tot += __shfl_xor(l_tot, 32);
-  if (qi >= N) return;
-  // lane l holds O^T[c = 16h + 4*(l/16) + r][q = l%16]
 #pragma unroll
-  for (int h = 0; h < NH; ++h) {
-    const int cbase = 16 * h + 4 * grp;
-    if (cbase < D) {
-      float o[4];
+  for (int qt = 0; qt < QT; ++qt) {
+    float l_tot = l_run[qt] + __shfl_xor(l_run[qt], 16);
+    l_tot += __shfl_xor(l_tot, 32);
+    const int qi = q0 + 16 * qt + col;
+    if (qi >= N) continue;
+    // lane l holds O^T[c = 16h + 4*(l/16) + r][q = l%16]
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[r] = acc[h][r] / l_tot;
-      st_row<T, 4>(O + boff + static_cast<size_t>(qi) * D + cbase, o);
+    for (int h = 0; h < NH; ++h) {
+      const int cbase = 16 * h + 4 * grp;
+      if (cbase < D) {
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = acc[qt][h][r] / l_tot;
+        st_row<T, 4>(O + boff + static_cast<size_t>(qi) * D + cbase, o);
+      }
     }
   }
 }
 
 template <typename T, int D>
 static hipError_t launch_dense(const DenseArgs& a) {
-  const int nw = a.N >= 64 ? 4 : (a.N + 15) / 16;
-  const int qb = 16 * nw;
+  constexpr int QT = kDenseQueryTiles;
+  const int per_wave = 16 * QT;
+  const int waves = (a.N + per_wave - 1) / per_wave;
+  const int nw = waves >= 4 ? 4 : waves;
+  const int qb = per_wave * nw;
   const int n_qblk = (a.N + qb - 1) / qb;
   const int nblocks = a.B * n_qblk;
   const size_t lds = dense_lds_bytes(a.dtype, a.d, a.key_chunk);
-  hipLaunchKernelGGL((dense_kernel<T, D>), dim3(nblocks), dim3(64 * nw), lds,
+  hipLaunchKernelGGL((dense_kernel<T, D, QT>), dim3(nblocks), dim3(64 * nw), lds,
                      static_cast<hipStream_t>(a.stream), static_cast<const T*>(a.q),
                      static_cast<const T*>(a.k), static_cast<const T*>(a.v), static_cast<T*>(a.out),
                      a.N, n_qblk, a.key_chunk, a.scale, nblocks);

@@ -107,13 +107,23 @@ struct Frag<float, D> {
 #pragma unroll
     for (int t = 0; t < E; ++t) q[t] *= pre;
   }
+  static constexpr int NI = E;          // MFMA steps per 16x16 score tile
+  struct KF { float v[E]; };
   // krow: LDS row of key (tile base + lane % 16).
+  __device__ __forceinline__ static KF load_k(const float* krow, int grp) {
+    KF f;
+    ld_f32<E>(f.v, krow + grp * E);
+    return f;
+  }
+  // Step i of the tile's MFMA chain (steps must run in order 0..NI-1).
+  __device__ __forceinline__ f32x4 step(const KF& kf, int i, f32x4 acc) const {
+    return mfma_f32_16x16x4(kf.v[i], q[i], acc);
+  }
   __device__ __forceinline__ f32x4 score(const float* krow, int grp) const {
-    float kf[E];
-    ld_f32<E>(kf, krow + grp * E);
+    const KF kf = load_k(krow, grp);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < E; ++t) acc = mfma_f32_16x16x4(kf[t], q[t], acc);
+    for (int t = 0; t < NI; ++t) acc = step(kf, t, acc);
     return acc;
   }
 };
@@ -134,10 +144,17 @@ struct Frag<bf16, 16> {
 #pragma unroll
     for (int i = 0; i < 4; ++i) q[i] = static_cast<short>(scale_bf16(e[i], pre));
   }
+  static constexpr int NI = 1;
+  struct KF { i16x4 v; };
+  __device__ __forceinline__ static KF load_k(const bf16* krow, int grp) {
+    return KF{*reinterpret_cast<const i16x4*>(krow + 4 * grp)};
+  }
+  __device__ __forceinline__ f32x4 step(const KF& kf, int, f32x4 acc) const {
+    return mfma_bf16_16x16x16(kf.v, q, acc);
+  }
   __device__ __forceinline__ f32x4 score(const bf16* krow, int grp) const {
-    i16x4 kf = *reinterpret_cast<const i16x4*>(krow + 4 * grp);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    return mfma_bf16_16x16x16(kf, q, acc);
+    return step(load_k(krow, grp), 0, acc);
   }
 };
 
@@ -158,13 +175,21 @@ struct FragBf16Wide {
       }
     }
   }
+  struct KF { bf16x8 v[NI]; };
+  __device__ __forceinline__ static KF load_k(const bf16* krow, int grp) {
+    KF f;
+#pragma unroll
+    for (int h = 0; h < NI; ++h) f.v[h] = *reinterpret_cast<const bf16x8*>(krow + 32 * h + 8 * grp);
+    return f;
+  }
+  __device__ __forceinline__ f32x4 step(const KF& kf, int i, f32x4 acc) const {
+    return mfma_bf16_16x16x32(kf.v[i], q[i], acc);
+  }
   __device__ __forceinline__ f32x4 score(const bf16* krow, int grp) const {
+    const KF kf = load_k(krow, grp);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int h = 0; h < NI; ++h) {
-      bf16x8 kf = *reinterpret_cast<const bf16x8*>(krow + 32 * h + 8 * grp);
-      acc = mfma_bf16_16x16x32(kf, q[h], acc);
-    }
+    for (int h = 0; h < NI; ++h) acc = step(kf, h, acc);
     return acc;
   }
 };
@@ -173,6 +198,60 @@ template <>
 struct Frag<bf16, 32> : FragBf16Wide<32> {};
 template <>
 struct Frag<bf16, 64> : FragBf16Wide<64> {};
+
+// 1/sqrt(d) is a power of two (d = 4^m): it can be folded into q exactly.
+template <int D>
+constexpr bool pow2_scale() {
+  return D == 4 || D == 16 || D == 64 || D == 256;
+}
+
+// Scores of QT query tiles against BT consecutive 16-key tiles starting at
+// LDS row `kb` (row stride LDK). The QT*BT MFMA chains are independent and
+// issued round-robin; each chain still runs its steps in order 0..NI-1, so
+// the rounding is that of a single tile.
+template <typename F, int QT, int BT, typename T>
+__device__ __forceinline__ void block_scores(const F (&frag)[QT], const T* Ks, int kb, int ldk,
+                                             int lane, f32x4 (&s)[QT][BT]) {
+  const int col = lane & 15, grp = lane >> 4;
+  typename F::KF kf[BT];
+#pragma unroll
+  for (int t = 0; t < BT; ++t) kf[t] = F::load_k(Ks + (kb + 16 * t + col) * ldk, grp);
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int t = 0; t < BT; ++t) s[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < F::NI; ++i)
+#pragma unroll
+    for (int t = 0; t < BT; ++t)
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) s[qt][t] = frag[qt].step(kf[t], i, s[qt][t]);
+}
+
+// The same product split in two halves, so a caller can issue the LDS reads
+// of the next block early and its MFMAs next to unrelated VALU work.
+template <typename F, int BT, typename T>
+__device__ __forceinline__ void load_block_k(const T* Ks, int kb, int ldk, int lane,
+                                             typename F::KF (&kf)[BT]) {
+  const int col = lane & 15, grp = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < BT; ++t) kf[t] = F::load_k(Ks + (kb + 16 * t + col) * ldk, grp);
+}
+
+template <typename F, int QT, int BT>
+__device__ __forceinline__ void mma_block(const F (&frag)[QT], const typename F::KF (&kf)[BT],
+                                          f32x4 (&s)[QT][BT]) {
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int t = 0; t < BT; ++t) s[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < F::NI; ++i)
+#pragma unroll
+    for (int t = 0; t < BT; ++t)
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) s[qt][t] = frag[qt].step(kf[t], i, s[qt][t]);
+}
 
 // Cooperative copy of `rows` rows of a [*, D] matrix into LDS with row stride
 // LDK, zero-filling rows [rows, rows_pad). 16-byte vectors; every thread of

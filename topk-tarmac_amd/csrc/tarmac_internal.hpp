@@ -9,7 +9,8 @@ namespace tarmac {
 
 enum Dtype : int { kF32 = 0, kBf16 = 1 };
 
-constexpr int kTopkSmallMax = 8;  // k handled by the register-list kernel
+constexpr int kTopkSmallMax = 8;    // k handled by the register-list kernel
+constexpr int kTopkQueryTiles = 2;  // 16-query tiles per wavefront
 
 inline int next_pow2(int x) {
   int p = 1;
@@ -80,7 +81,7 @@ hipError_t run_morton_window(const MortonArgs& a);
 hipError_t run_zorder(const ZorderArgs& a);
 hipError_t run_noop(float* out, void* stream);
 
-int topk_lds_row_bytes(int dtype, int d);
+size_t topk_lds_bytes(int dtype, int d, int kc);
 size_t dense_lds_bytes(int dtype, int d, int kc);
 size_t zorder_lds_bytes(int N);
 

@@ -63,7 +63,44 @@ __device__ __forceinline__ void topk_insert_lex(float (&val)[K], int (&ix)[K], f
   ix[0] = c0 ? j : ix[0];
 }
 
-template <typename T, int D, int K>
+constexpr int kBlockTiles = 4;               // 16-key tiles per selection block
+constexpr int kBlockKeys = 16 * kBlockTiles;
+
+// Scale (non power-of-two 1/sqrt(d)) and mask one block's scores: the self
+// pair and keys past the chunk end. The branch is wave-uniform and taken only
+// for the block holding this wave's diagonal and for a ragged last block.
+template <int QT, int BT, bool POW2>
+__device__ __forceinline__ void prepare_block(f32x4 (&s)[QT][BT], float scale,
+                                              const int (&self)[QT], int q0, int kabs, int kend,
+                                              int grp) {
+  if constexpr (!POW2) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int t = 0; t < BT; ++t) s[qt][t] *= scale;
+  }
+  if ((q0 < kabs + 16 * BT && kabs < q0 + 16 * QT) || kabs + 16 * BT > kend) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int t = 0; t < BT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = kabs + 16 * t + 4 * grp + r;
+          if (key >= kend || key == self[qt]) s[qt][t][r] = -INFINITY;
+        }
+  }
+}
+
+template <int QT, int K>
+__device__ __forceinline__ void rebase_list(int (&ix)[QT][K], int delta) {
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int m = 0; m < K; ++m) ix[qt][m] -= delta;
+}
+
+template <typename T, int D, int K, int QT>
 __global__ void __launch_bounds__(256)
 topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
                   T* __restrict__ O, int32_t* __restrict__ Idx, int N, int n_qblk, int kc,
@@ -71,95 +108,113 @@ topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __
   using F = Frag<T, D>;
   constexpr int LDK = F::LDK;
   constexpr int EO = D / 4;  // output channels per lane
+  constexpr int BT = kBlockTiles;
+  constexpr bool POW2 = pow2_scale<D>();
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T* Ks = reinterpret_cast<T*>(smem_raw);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int blk = xcd_logical_block(blockIdx.x, nblocks);
   const int b = blk / n_qblk, qblk = blk - b * n_qblk;
-  const int q0 = qblk * (16 * nw) + wave * 16;
+  const int q0 = (qblk * nw + wave) * 16 * QT;  // first query of this wave
   const int col = lane & 15, grp = lane >> 4;
-  const int qi = q0 + col;
   const size_t boff = static_cast<size_t>(b) * N * D;
-  const bool pow2 = is_pow2_scale(scale);
 
-  F frag;
-  frag.load_q(Q + boff + static_cast<size_t>(min(qi, N - 1)) * D, grp, pow2 ? scale : 1.f);
-
-  float val[K];
-  int ix[K];
+  F frag[QT];
 #pragma unroll
-  for (int m = 0; m < K; ++m) { val[m] = -INFINITY; ix[m] = kIdxSentinel; }
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qi = q0 + 16 * qt + col;
+    frag[qt].load_q(Q + boff + static_cast<size_t>(min(qi, N - 1)) * D, grp,
+                    POW2 ? scale : 1.f);
+  }
+
+  float val[QT][K];
+  int ix[QT][K];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int m = 0; m < K; ++m) { val[qt][m] = -INFINITY; ix[qt][m] = kIdxSentinel; }
+
+  int self[QT];  // this lane's query index per query tile
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) self[qt] = q0 + 16 * qt + col;
+  // Stored indices are kept relative to the base of the block being
+  // selected, so a new candidate's index is the inline constant 16t+r; the
+  // lane-group offset 4*(l/16) is added at the end.
+  int base = 0;
 
   for (int c0 = 0; c0 < N; c0 += kc) {
     const int cn = min(kc, N - c0);
-    const int cn16 = (cn + 15) & ~15;
+    const int cnb = (cn + kBlockKeys - 1) / kBlockKeys * kBlockKeys;
     __syncthreads();
-    stage_rows<T, D, LDK>(Ks, Kx + boff + static_cast<size_t>(c0) * D, cn, cn16);
+    stage_rows<T, D, LDK>(Ks, Kx + boff + static_cast<size_t>(c0) * D, cn, cnb);
     __syncthreads();
-    if (q0 < N) {
-      for (int kb = 0; kb < cn16; kb += 16) {
-        f32x4 s = frag.score(Ks + (kb + col) * LDK, grp);
-        if (!pow2) {
+    if (q0 >= N) continue;
+    const int kend = c0 + cn;  // rows past the chunk end are zero padding
+    for (int kb0 = 0; kb0 < cnb; kb0 += kBlockKeys) {
+      const int kabs = c0 + kb0;
+      f32x4 s[QT][BT];
+      block_scores<F, QT, BT>(frag, Ks, kb0, LDK, lane, s);
+      prepare_block<QT, BT, POW2>(s, scale, self, q0, kabs, kend, grp);
+      rebase_list<QT, K>(ix, kabs - base);
+      base = kabs;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) s[r] *= scale;
-        }
-        const int kabs = c0 + kb;
-        const int kend = c0 + cn;  // rows past the chunk end are zero padding
-        if (kabs == q0 || kabs + 16 > kend) {  // wave-uniform: diagonal or ragged tile
+      for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int key = kabs + 4 * grp + r;
-            if (key >= kend || key == qi) s[r] = -INFINITY;
-          }
-        }
-        // index recorded without the lane-group offset (uniform), added after
+        for (int t = 0; t < BT; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) topk_insert<K>(val, ix, s[r], kabs + r);
-      }
+          for (int r = 0; r < 4; ++r) topk_insert<K>(val[qt], ix[qt], s[qt][t][r], 16 * t + r);
     }
   }
+  rebase_list<QT, K>(ix, -base);  // back to absolute key indices
   if (q0 >= N) return;
 
 #pragma unroll
-  for (int m = 0; m < K; ++m) ix[m] += 4 * grp;
+  for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+    for (int m = 0; m < K; ++m) ix[qt][m] += 4 * grp;
+#pragma unroll
+    for (int step = 16; step <= 32; step <<= 1) {
+      float pv[K];
+      int pi[K];
+#pragma unroll
+      for (int m = 0; m < K; ++m) {
+        pv[m] = __shfl_xor(val[qt][m], step);
+        pi[m] = __shfl_xor(ix[qt][m], step);
+      }
+#pragma unroll
+      for (int m = 0; m < K; ++m) topk_insert_lex<K>(val[qt], ix[qt], pv[m], pi[m]);
+    }
+  }
 
 #pragma unroll
-  for (int step = 16; step <= 32; step <<= 1) {
-    float pv[K];
-    int pi[K];
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qi = q0 + 16 * qt + col;
+    if (qi >= N) continue;
+    const float mx = val[qt][0];
+    float acc[EO];
+#pragma unroll
+    for (int c = 0; c < EO; ++c) acc[c] = 0.f;
+    float den = 0.f;
 #pragma unroll
     for (int m = 0; m < K; ++m) {
-      pv[m] = __shfl_xor(val[m], step);
-      pi[m] = __shfl_xor(ix[m], step);
+      const float w = fast_exp2((val[qt][m] - mx) * kLog2eF);
+      den += w;
+      const int row = min(max(ix[qt][m], 0), N - 1);
+      float vr[EO];
+      ld_row<T, EO>(vr, V + boff + static_cast<size_t>(row) * D + grp * EO);
+#pragma unroll
+      for (int c = 0; c < EO; ++c) acc[c] = fmaf(w, vr[c], acc[c]);
     }
+    const float inv = 1.f / den;
 #pragma unroll
-    for (int m = 0; m < K; ++m) topk_insert_lex<K>(val, ix, pv[m], pi[m]);
-  }
-
-  if (qi >= N) return;
-  const float mx = val[0];
-  float acc[EO];
+    for (int c = 0; c < EO; ++c) acc[c] *= inv;
+    st_row<T, EO>(O + boff + static_cast<size_t>(qi) * D + grp * EO, acc);
+    if (Idx != nullptr && grp == 0) {
+      int32_t* dst = Idx + (static_cast<size_t>(b) * N + qi) * K;
 #pragma unroll
-  for (int c = 0; c < EO; ++c) acc[c] = 0.f;
-  float den = 0.f;
-#pragma unroll
-  for (int m = 0; m < K; ++m) {
-    const float w = expf(val[m] - mx);
-    den += w;
-    const int row = min(max(ix[m], 0), N - 1);
-    float vr[EO];
-    ld_row<T, EO>(vr, V + boff + static_cast<size_t>(row) * D + grp * EO);
-#pragma unroll
-    for (int c = 0; c < EO; ++c) acc[c] = fmaf(w, vr[c], acc[c]);
-  }
-#pragma unroll
-  for (int c = 0; c < EO; ++c) acc[c] = acc[c] / den;
-  st_row<T, EO>(O + boff + static_cast<size_t>(qi) * D + grp * EO, acc);
-  if (Idx != nullptr && grp == 0) {
-    int32_t* dst = Idx + (static_cast<size_t>(b) * N + qi) * K;
-#pragma unroll
-    for (int m = 0; m < K; ++m) dst[m] = ix[m];
+      for (int m = 0; m < K; ++m) dst[m] = ix[qt][m];
+    }
   }
 }
 
@@ -294,11 +349,14 @@ topk_wide_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __r
 
 template <typename T, int D>
 static hipError_t launch_small(const TopkArgs& a, int kc) {
-  const int nw = a.N >= 64 ? 4 : (a.N + 15) / 16;
-  const int qb = 16 * nw;
+  constexpr int QT = kTopkQueryTiles;
+  const int per_wave = 16 * QT;
+  const int waves = (a.N + per_wave - 1) / per_wave;
+  const int nw = waves >= 4 ? 4 : waves;
+  const int qb = per_wave * nw;
   const int n_qblk = (a.N + qb - 1) / qb;
   const int nblocks = a.B * n_qblk;
-  const size_t lds = static_cast<size_t>(kc) * Frag<T, D>::LDK * sizeof(T);
+  const size_t lds = topk_lds_bytes(a.dtype, a.d, kc);
   const T* q = static_cast<const T*>(a.q);
   const T* k = static_cast<const T*>(a.k);
   const T* v = static_cast<const T*>(a.v);
@@ -306,7 +364,7 @@ static hipError_t launch_small(const TopkArgs& a, int kc) {
   hipStream_t st = static_cast<hipStream_t>(a.stream);
 #define TARMAC_TOPK_CASE(KK)                                                                   \
   case KK:                                                                                     \
-    hipLaunchKernelGGL((topk_small_kernel<T, D, KK>), dim3(nblocks), dim3(64 * nw), lds, st, \
+    hipLaunchKernelGGL((topk_small_kernel<T, D, KK, QT>), dim3(nblocks), dim3(64 * nw), lds, st, \
                        q, k, v, o, a.idx, a.N, n_qblk, kc, a.scale, nblocks);                 \
     break;
   switch (a.topk) {
@@ -364,9 +422,10 @@ hipError_t run_topk(const TopkArgs& a) {
   return hipErrorInvalidValue;
 }
 
-int topk_lds_row_bytes(int dtype, int d) {
-  if (dtype == kF32) return (d + 4) * 4;
-  return (d + 8) * 2;
+size_t topk_lds_bytes(int dtype, int d, int kc) {
+  const int row = dtype == kF32 ? (d + 4) * 4 : (d + 8) * 2;
+  const int kcb = (kc + kBlockKeys - 1) / kBlockKeys * kBlockKeys;
+  return static_cast<size_t>(kcb) * row;
 }
 
 }  // namespace tarmac
