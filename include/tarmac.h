@@ -105,6 +105,16 @@ int tarmac_zorder_fwd(const void* q, const void* k, const void* v, const float* 
                       int32_t* idx_out, int B, int N, int d, int topk, int bits, int dtype,
                       void* stream);
 
+/*
+ * fp32 top-k (d = 16, 32, 64; topk <= 8) scores all pairs on split-bf16 MFMA,
+ * rescores the k candidates in the canonical fp32 order and proves they are
+ * the exact top k (wavefronts where the proof fails recompute in fp32). The
+ * result is identical either way; this switch (default on, process-wide)
+ * selects the plain fp32 path for timing comparisons. Returns the previous
+ * setting. No counterpart in the reference (its kernels have one path).
+ */
+int tarmac_set_topk_filter(int enabled);
+
 /* Writes 1.0f to *out: the launch-floor probe of scripts/launch_overhead.py:28-30. */
 int tarmac_noop(float* out, void* stream);
 

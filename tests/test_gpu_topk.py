@@ -164,3 +164,40 @@ def test_topk_bf16(N, d, kk):
     ref = O.prescore_attention(qb.astype(np.float64), kb.astype(np.float64),
                                vb.astype(np.float64), idx.astype(np.int64))
     assert np.abs(out - ref).max() <= BF16_TOL * np.abs(ref).max()
+
+
+def _set_filter(on: bool) -> int:
+    from tarmac import _lib
+    return _lib.LIB.tarmac_set_topk_filter(1 if on else 0)
+
+
+@pytest.mark.parametrize("N,d,kk,chunk", [(256, 16, 1, None), (256, 16, 2, None), (384, 32, 4, None),
+                                          (512, 64, 8, None), (100, 16, 3, None),
+                                          (1024, 16, 2, 256), (700, 32, 5, 128)])
+def test_filter_path_matches_plain_fp32_path_bitwise(N, d, kk, chunk):
+    """The split-bf16 filter with exact verification returns exactly what the
+    plain fp32 scoring pass returns (and both equal the canonical oracle)."""
+    B = 6
+    q, k, v = qkv(17 * N + kk, B, N, d)
+    prev = _set_filter(False)
+    try:
+        out_p, idx_p = run_topk(q, k, v, kk, chunk=chunk)
+    finally:
+        _set_filter(bool(prev))
+    out_f, idx_f = run_topk(q, k, v, kk, chunk=chunk)
+    assert np.array_equal(idx_f, idx_p)
+    assert np.array_equal(out_f, out_p)
+    check_f32(q, k, v, kk, out_f, idx_f)
+
+
+def test_filter_fallback_on_ties():
+    """Duplicated keys and constant queries defeat the filter's proof; the
+    fallback must still return the canonical answer."""
+    B, N, d = 4, 256, 16
+    q, k, v = qkv(23, B, N, d)
+    k[:, 1::2] = k[:, 0::2]
+    q[:, :40] = 0.0
+    q[:, 40:80] = q[:, 40:41]
+    for kk in (1, 2, 4):
+        out, idx = run_topk(q, k, v, kk)
+        check_f32(q, k, v, kk, out, idx)

@@ -189,6 +189,12 @@ int tarmac_zorder_fwd(const void* q, const void* k, const void* v, const float* 
   return hip_status(tarmac::run_zorder(a), fn);
 }
 
+int tarmac_set_topk_filter(int enabled) {
+  const int prev = tarmac::g_topk_filter_enabled;
+  tarmac::g_topk_filter_enabled = enabled ? 1 : 0;
+  return prev;
+}
+
 int tarmac_noop(float* out, void* stream) {
   if (!out) return fail(TARMAC_ERR_INVALID, "tarmac_noop: null out");
   return hip_status(tarmac::run_noop(out, stream), "tarmac_noop");

@@ -1,0 +1,141 @@
+// Register top-k lists and block masking shared by the top-k kernels.
+//
+// A lane keeps its best K candidates as a list sorted by (score desc, index
+// asc). Keys reach a lane in ascending index order, so a strict '>' insertion
+// keeps the lower index ahead on equal scores; lists built from disjoint key
+// sets are merged with a lexicographic comparison.
+#pragma once
+
+#include "frag.hpp"
+
+namespace tarmac {
+
+constexpr int kIdxSentinel = 0x3fffffff;
+
+// max(a, b) on the median unit: v_med3_f32 needs no NaN canonicalisation of
+// its operands, unlike fmaxf (inputs here are never NaN).
+__device__ __forceinline__ float vmax(float a, float b) {
+  return __builtin_amdgcn_fmed3f(a, b, INFINITY);
+}
+
+template <int K>
+__device__ __forceinline__ void topk_insert(float (&val)[K], int (&ix)[K], float s, int j) {
+  // New keys arrive in ascending index order, so a strict '>' keeps the
+  // earlier (lower-index) entry ahead on equal scores. Values move through
+  // max / med3 (list order v[m-1] >= v[m]), indices through the compares.
+  bool c[K];
+#pragma unroll
+  for (int m = 0; m < K; ++m) c[m] = s > val[m];
+#pragma unroll
+  for (int m = K - 1; m > 0; --m) {
+    val[m] = __builtin_amdgcn_fmed3f(val[m - 1], val[m], s);
+    ix[m] = c[m - 1] ? ix[m - 1] : (c[m] ? j : ix[m]);
+  }
+  val[0] = vmax(val[0], s);
+  ix[0] = c[0] ? j : ix[0];
+}
+
+template <int K>
+__device__ __forceinline__ void topk_insert_lex(float (&val)[K], int (&ix)[K], float s, int j) {
+#pragma unroll
+  for (int m = K - 1; m > 0; --m) {
+    const bool cm = ranks_before(s, j, val[m], ix[m]);
+    const bool cp = ranks_before(s, j, val[m - 1], ix[m - 1]);
+    const float vm = val[m - 1];
+    const int im = ix[m - 1];
+    val[m] = cp ? vm : (cm ? s : val[m]);
+    ix[m] = cp ? im : (cm ? j : ix[m]);
+  }
+  const bool c0 = ranks_before(s, j, val[0], ix[0]);
+  val[0] = c0 ? s : val[0];
+  ix[0] = c0 ? j : ix[0];
+}
+
+constexpr int kBlockTiles = 4;               // 16-key tiles per selection block
+constexpr int kBlockKeys = 16 * kBlockTiles;
+
+// Scale (non power-of-two 1/sqrt(d)) and mask one block's scores: the self
+// pair and keys past the chunk end. Branches are wave-uniform. In the 16-key
+// tile holding a query tile's diagonal, lane l's element r is the self pair
+// exactly when 4*(l/16) + r == l % 16 (the loop-invariant lane predicate
+// self_r[r]), so the self mask is one select per element of that block.
+template <int QT, int BT, bool POW2>
+__device__ __forceinline__ void prepare_block(f32x4 (&s)[QT][BT], float scale,
+                                              const bool (&self_r)[4], int q0, int kabs, int kend,
+                                              int grp) {
+  if constexpr (!POW2) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int t = 0; t < BT; ++t) s[qt][t] *= scale;
+  }
+  if (q0 < kabs + 16 * BT && kabs < q0 + 16 * QT) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int t = 0; t < BT; ++t) {
+        const bool diag_tile = (q0 + 16 * qt == kabs + 16 * t);  // uniform
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          s[qt][t][r] = (diag_tile && self_r[r]) ? -INFINITY : s[qt][t][r];
+      }
+  }
+  if (kabs + 16 * BT > kend) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int t = 0; t < BT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (kabs + 16 * t + 4 * grp + r >= kend) s[qt][t][r] = -INFINITY;
+  }
+}
+
+template <int QT, int K>
+__device__ __forceinline__ void rebase_list(int (&ix)[QT][K], int delta) {
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int m = 0; m < K; ++m) ix[qt][m] -= delta;
+}
+
+
+// As topk_insert, plus the value (no index) of the (K+1)-th best in val[K]:
+// values move through max / med3, indices through the compares.
+template <int K>
+__device__ __forceinline__ void topk_insert_x(float (&val)[K + 1], int (&ix)[K], float s, int j) {
+  bool c[K];
+#pragma unroll
+  for (int m = 0; m < K; ++m) c[m] = s > val[m];
+  val[K] = __builtin_amdgcn_fmed3f(val[K - 1], val[K], s);
+#pragma unroll
+  for (int m = K - 1; m > 0; --m) {
+    val[m] = __builtin_amdgcn_fmed3f(val[m - 1], val[m], s);
+    ix[m] = c[m - 1] ? ix[m - 1] : (c[m] ? j : ix[m]);
+  }
+  val[0] = vmax(val[0], s);
+  ix[0] = c[0] ? j : ix[0];
+}
+
+// Lexicographic insertion into a (K+1)-list whose last slot carries only a
+// value. Entries with index kIdxSentinel lose every tie.
+template <int K>
+__device__ __forceinline__ void topk_insert_lex_x(float (&val)[K + 1], int (&ix)[K], float s, int j) {
+  // slot K (value only): the (K+1)-th best of the union
+  const bool ck = ranks_before(s, j, val[K - 1], ix[K - 1]);
+  val[K] = ck ? val[K - 1] : vmax(val[K], s);
+#pragma unroll
+  for (int m = K - 1; m > 0; --m) {
+    const bool cm = ranks_before(s, j, val[m], ix[m]);
+    const bool cp = ranks_before(s, j, val[m - 1], ix[m - 1]);
+    const float vm = val[m - 1];
+    const int im = ix[m - 1];
+    val[m] = cp ? vm : (cm ? s : val[m]);
+    ix[m] = cp ? im : (cm ? j : ix[m]);
+  }
+  const bool c0 = ranks_before(s, j, val[0], ix[0]);
+  val[0] = c0 ? s : val[0];
+  ix[0] = c0 ? j : ix[0];
+}
+
+}  // namespace tarmac

@@ -75,6 +75,9 @@ struct ZorderArgs {
 };
 
 hipError_t run_topk(const TopkArgs& a);
+hipError_t run_topk_filter(const TopkArgs& a);
+bool topk_filter_supported(int dtype, int d, int topk);
+extern int g_topk_filter_enabled;
 hipError_t run_dense(const DenseArgs& a);
 hipError_t run_fixedset(const FixedsetArgs& a);
 hipError_t run_morton_window(const MortonArgs& a);
@@ -82,6 +85,7 @@ hipError_t run_zorder(const ZorderArgs& a);
 hipError_t run_noop(float* out, void* stream);
 
 size_t topk_lds_bytes(int dtype, int d, int kc);
+size_t topk_filter_lds_bytes(int d, int kc);
 size_t dense_lds_bytes(int dtype, int d, int kc);
 size_t zorder_lds_bytes(int N);
 

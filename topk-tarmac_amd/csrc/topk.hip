@@ -25,80 +25,10 @@
 // found by bisection on the order-preserving integer key, ties at the
 // threshold resolved to the lowest indices.
 #include "frag.hpp"
+#include "select.hpp"
 #include "tarmac_internal.hpp"
 
 namespace tarmac {
-
-constexpr int kIdxSentinel = 0x3fffffff;
-
-template <int K>
-__device__ __forceinline__ void topk_insert(float (&val)[K], int (&ix)[K], float s, int j) {
-  // New keys arrive in ascending index order, so a strict '>' keeps the
-  // earlier (lower-index) entry ahead on equal scores.
-#pragma unroll
-  for (int m = K - 1; m > 0; --m) {
-    const bool cm = s > val[m];
-    const bool cp = s > val[m - 1];
-    val[m] = cp ? val[m - 1] : (cm ? s : val[m]);
-    ix[m] = cp ? ix[m - 1] : (cm ? j : ix[m]);
-  }
-  const bool c0 = s > val[0];
-  val[0] = c0 ? s : val[0];
-  ix[0] = c0 ? j : ix[0];
-}
-
-template <int K>
-__device__ __forceinline__ void topk_insert_lex(float (&val)[K], int (&ix)[K], float s, int j) {
-#pragma unroll
-  for (int m = K - 1; m > 0; --m) {
-    const bool cm = ranks_before(s, j, val[m], ix[m]);
-    const bool cp = ranks_before(s, j, val[m - 1], ix[m - 1]);
-    const float vm = val[m - 1];
-    const int im = ix[m - 1];
-    val[m] = cp ? vm : (cm ? s : val[m]);
-    ix[m] = cp ? im : (cm ? j : ix[m]);
-  }
-  const bool c0 = ranks_before(s, j, val[0], ix[0]);
-  val[0] = c0 ? s : val[0];
-  ix[0] = c0 ? j : ix[0];
-}
-
-constexpr int kBlockTiles = 4;               // 16-key tiles per selection block
-constexpr int kBlockKeys = 16 * kBlockTiles;
-
-// Scale (non power-of-two 1/sqrt(d)) and mask one block's scores: the self
-// pair and keys past the chunk end. The branch is wave-uniform and taken only
-// for the block holding this wave's diagonal and for a ragged last block.
-template <int QT, int BT, bool POW2>
-__device__ __forceinline__ void prepare_block(f32x4 (&s)[QT][BT], float scale,
-                                              const int (&self)[QT], int q0, int kabs, int kend,
-                                              int grp) {
-  if constexpr (!POW2) {
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int t = 0; t < BT; ++t) s[qt][t] *= scale;
-  }
-  if ((q0 < kabs + 16 * BT && kabs < q0 + 16 * QT) || kabs + 16 * BT > kend) {
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int t = 0; t < BT; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = kabs + 16 * t + 4 * grp + r;
-          if (key >= kend || key == self[qt]) s[qt][t][r] = -INFINITY;
-        }
-  }
-}
-
-template <int QT, int K>
-__device__ __forceinline__ void rebase_list(int (&ix)[QT][K], int delta) {
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-    for (int m = 0; m < K; ++m) ix[qt][m] -= delta;
-}
 
 template <typename T, int D, int K, int QT>
 __global__ void __launch_bounds__(256)
@@ -135,9 +65,9 @@ topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __
 #pragma unroll
     for (int m = 0; m < K; ++m) { val[qt][m] = -INFINITY; ix[qt][m] = kIdxSentinel; }
 
-  int self[QT];  // this lane's query index per query tile
+  bool self_r[4];  // element r of a diagonal tile is this lane's self pair
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) self[qt] = q0 + 16 * qt + col;
+  for (int r = 0; r < 4; ++r) self_r[r] = (4 * grp + r == col);
   // Stored indices are kept relative to the base of the block being
   // selected, so a new candidate's index is the inline constant 16t+r; the
   // lane-group offset 4*(l/16) is added at the end.
@@ -155,7 +85,7 @@ topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __
       const int kabs = c0 + kb0;
       f32x4 s[QT][BT];
       block_scores<F, QT, BT>(frag, Ks, kb0, LDK, lane, s);
-      prepare_block<QT, BT, POW2>(s, scale, self, q0, kabs, kend, grp);
+      prepare_block<QT, BT, POW2>(s, scale, self_r, q0, kabs, kend, grp);
       rebase_list<QT, K>(ix, kabs - base);
       base = kabs;
 #pragma unroll
@@ -404,7 +334,10 @@ static hipError_t dispatch_topk(const TopkArgs& a) {
   return launch_small<T, D>(a, a.key_chunk);
 }
 
+int g_topk_filter_enabled = 1;
+
 hipError_t run_topk(const TopkArgs& a) {
+  if (g_topk_filter_enabled && topk_filter_supported(a.dtype, a.d, a.topk)) return run_topk_filter(a);
   if (a.dtype == kF32) {
     switch (a.d) {
       case 8: return dispatch_topk<float, 8>(a);
@@ -425,7 +358,10 @@ hipError_t run_topk(const TopkArgs& a) {
 size_t topk_lds_bytes(int dtype, int d, int kc) {
   const int row = dtype == kF32 ? (d + 4) * 4 : (d + 8) * 2;
   const int kcb = (kc + kBlockKeys - 1) / kBlockKeys * kBlockKeys;
-  return static_cast<size_t>(kcb) * row;
+  const size_t plain = static_cast<size_t>(kcb) * row;
+  if (dtype != kF32 || d == 8) return plain;
+  const size_t filt = topk_filter_lds_bytes(d, kc);
+  return plain > filt ? plain : filt;
 }
 
 }  // namespace tarmac
