@@ -106,14 +106,19 @@ int tarmac_zorder_fwd(const void* q, const void* k, const void* v, const float* 
                       void* stream);
 
 /*
- * fp32 top-k (d = 16, 32, 64; topk <= 8) scores all pairs on split-bf16 MFMA,
- * rescores the k candidates in the canonical fp32 order and proves they are
- * the exact top k (wavefronts where the proof fails recompute in fp32). The
- * result is identical either way; this switch (default on, process-wide)
- * selects the plain fp32 path for timing comparisons. Returns the previous
- * setting. No counterpart in the reference (its kernels have one path).
+ * fp32 top-k (d = 16, 32, 64; topk <= 8) can score all pairs on split-bf16
+ * MFMA, rescore k+1 candidates in the canonical fp32 order and prove the
+ * result is the exact top k (16-query tiles where the proof fails recompute
+ * in fp32). The result is identical either way; only the time differs.
+ * mode: 0 = never, 1 = where it is faster (default; N >= 512), 2 = always.
+ * Process-wide. Returns the previous mode, or -1 (and sets the last error)
+ * for an invalid mode. No counterpart in the reference (its kernels have one
+ * path).
  */
-int tarmac_set_topk_filter(int enabled);
+#define TARMAC_FILTER_OFF 0
+#define TARMAC_FILTER_AUTO 1
+#define TARMAC_FILTER_ALWAYS 2
+int tarmac_set_topk_filter(int mode);
 
 /* Writes 1.0f to *out: the launch-floor probe of scripts/launch_overhead.py:28-30. */
 int tarmac_noop(float* out, void* stream);

@@ -55,6 +55,20 @@ def check_f32(q, k, v, kk, out, idx, exact_order=True):
         assert np.abs(out - out_r)[same].max() <= F32_TOL * max(np.abs(out_r).max(), 1e-30)
 
 
+def _set_filter(mode: int) -> int:
+    """0 = plain fp32 pass, 1 = automatic, 2 = filter-and-verify wherever supported."""
+    from tarmac import _lib
+    return _lib.LIB.tarmac_set_topk_filter(mode)
+
+
+@pytest.fixture
+def filter_always():
+    prev = _set_filter(2)
+    yield
+    _set_filter(prev)
+
+
+
 CASES = [
     (6, 16, 2), (6, 16, 1), (6, 8, 5), (2, 16, 1), (17, 16, 3), (32, 16, 1), (32, 16, 4),
     (64, 8, 2), (64, 32, 2), (100, 16, 2), (128, 64, 1), (256, 16, 1), (256, 16, 2),
@@ -63,11 +77,16 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("mode", [0, 2], ids=["plain", "filter"])
 @pytest.mark.parametrize("N,d,kk", CASES)
-def test_fused_topk_f32_parity(N, d, kk):
+def test_fused_topk_f32_parity(N, d, kk, mode):
     B = max(2, min(16, 4096 // N))
     q, k, v = qkv(N * 131 + d * 17 + kk, B, N, d)
-    out, idx = run_topk(q, k, v, kk)
+    prev = _set_filter(mode)
+    try:
+        out, idx = run_topk(q, k, v, kk)
+    finally:
+        _set_filter(prev)
     check_f32(q, k, v, kk, out, idx)
 
 
@@ -166,38 +185,49 @@ def test_topk_bf16(N, d, kk):
     assert np.abs(out - ref).max() <= BF16_TOL * np.abs(ref).max()
 
 
-def _set_filter(on: bool) -> int:
-    from tarmac import _lib
-    return _lib.LIB.tarmac_set_topk_filter(1 if on else 0)
-
-
 @pytest.mark.parametrize("N,d,kk,chunk", [(256, 16, 1, None), (256, 16, 2, None), (384, 32, 4, None),
                                           (512, 64, 8, None), (100, 16, 3, None),
                                           (1024, 16, 2, 256), (700, 32, 5, 128)])
-def test_filter_path_matches_plain_fp32_path_bitwise(N, d, kk, chunk):
+def test_filter_path_matches_plain_fp32_path_bitwise(N, d, kk, chunk, filter_always):
     """The split-bf16 filter with exact verification returns exactly what the
     plain fp32 scoring pass returns (and both equal the canonical oracle)."""
     B = 6
     q, k, v = qkv(17 * N + kk, B, N, d)
-    prev = _set_filter(False)
+    _set_filter(0)
     try:
         out_p, idx_p = run_topk(q, k, v, kk, chunk=chunk)
     finally:
-        _set_filter(bool(prev))
+        _set_filter(2)
     out_f, idx_f = run_topk(q, k, v, kk, chunk=chunk)
     assert np.array_equal(idx_f, idx_p)
     assert np.array_equal(out_f, out_p)
     check_f32(q, k, v, kk, out_f, idx_f)
 
 
-def test_filter_fallback_on_ties():
+@pytest.mark.parametrize("N,chunk", [(256, None), (700, 128), (2048, None)])
+def test_filter_fallback_on_ties(N, chunk, filter_always):
     """Duplicated keys and constant queries defeat the filter's proof; the
-    fallback must still return the canonical answer."""
-    B, N, d = 4, 256, 16
-    q, k, v = qkv(23, B, N, d)
+    fallback must still return the canonical answer (single-segment lists,
+    chunked lists and lists spanning several 1024-key segments)."""
+    B, d = 3, 16
+    q, k, v = qkv(23 + N, B, N, d)
     k[:, 1::2] = k[:, 0::2]
     q[:, :40] = 0.0
     q[:, 40:80] = q[:, 40:41]
-    for kk in (1, 2, 4):
-        out, idx = run_topk(q, k, v, kk)
+    for kk in (1, 2, 4, 8):
+        out, idx = run_topk(q, k, v, kk, chunk=chunk)
         check_f32(q, k, v, kk, out, idx)
+
+
+@pytest.mark.parametrize("N,kk,chunk", [(256, 2, None), (512, 8, None), (1500, 3, 256)])
+def test_filter_near_ties(N, kk, chunk, filter_always):
+    """Clusters of keys whose scores agree to ~1e-6 relative: candidates that
+    share their truncated filter score, lists that must be re-sorted after
+    repacking, and proofs that fail on purpose."""
+    B, d = 3, 16
+    q, k, v = qkv(91 + N + kk, B, N, d)
+    rng = np.random.default_rng(N)
+    for c0 in range(0, N - 40, 97):
+        k[:, c0 + 1:c0 + 40] = k[:, c0:c0 + 1] * 3.0 + 1e-6 * rng.standard_normal((B, 39, d))
+    out, idx = run_topk(q, k, v, kk, chunk=chunk)
+    check_f32(q, k, v, kk, out, idx)

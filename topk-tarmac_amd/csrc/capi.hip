@@ -189,9 +189,13 @@ int tarmac_zorder_fwd(const void* q, const void* k, const void* v, const float* 
   return hip_status(tarmac::run_zorder(a), fn);
 }
 
-int tarmac_set_topk_filter(int enabled) {
-  const int prev = tarmac::g_topk_filter_enabled;
-  tarmac::g_topk_filter_enabled = enabled ? 1 : 0;
+int tarmac_set_topk_filter(int mode) {
+  if (mode < tarmac::kFilterOff || mode > tarmac::kFilterAlways) {
+    fail(TARMAC_ERR_INVALID, "tarmac_set_topk_filter: mode must be 0, 1 or 2 (got %d)", mode);
+    return -1;
+  }
+  const int prev = tarmac::g_topk_filter_mode;
+  tarmac::g_topk_filter_mode = mode;
   return prev;
 }
 

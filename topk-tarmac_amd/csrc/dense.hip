@@ -77,19 +77,26 @@ template <typename T, int D, int CP>
 __device__ __forceinline__ void stage_vt(T* Vt, int ldv, const T* src, int rows, int rows_pad) {
   constexpr int VE = 16 / sizeof(T);
   constexpr int VPR = D / VE;
+  constexpr int U = kStageBatch;
   const int total = rows_pad * VPR;
-  for (int v = threadIdx.x; v < total; v += blockDim.x) {
-    const int row = v / VPR, cv = v - row * VPR;
-    T x[VE];
-    if (row < rows) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(src + static_cast<size_t>(row) * D + cv * VE);
-      __builtin_memcpy(x, &raw, 16);
-    } else {
+  for (int v0 = threadIdx.x; v0 < total; v0 += U * blockDim.x) {
+    uint4 raw[U];
 #pragma unroll
-      for (int e = 0; e < VE; ++e) x[e] = T(0);
+    for (int u = 0; u < U; ++u) {
+      const int v = v0 + u * blockDim.x, row = v / VPR, cv = v - row * VPR;
+      raw[u] = make_uint4(0u, 0u, 0u, 0u);
+      if (v < total && row < rows)
+        raw[u] = *reinterpret_cast<const uint4*>(src + static_cast<size_t>(row) * D + cv * VE);
     }
 #pragma unroll
-    for (int e = 0; e < VE; ++e) Vt[(cv * VE + e) * ldv + row] = x[e];
+    for (int u = 0; u < U; ++u) {
+      const int v = v0 + u * blockDim.x, row = v / VPR, cv = v - row * VPR;
+      if (v >= total) break;
+      T x[VE];
+      __builtin_memcpy(x, &raw[u], 16);
+#pragma unroll
+      for (int e = 0; e < VE; ++e) Vt[(cv * VE + e) * ldv + row] = x[e];
+    }
   }
   if constexpr (CP > D) {
     const int pad = (CP - D) * rows_pad;

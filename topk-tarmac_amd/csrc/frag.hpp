@@ -256,17 +256,31 @@ __device__ __forceinline__ void mma_block(const F (&frag)[QT], const typename F:
 // Cooperative copy of `rows` rows of a [*, D] matrix into LDS with row stride
 // LDK, zero-filling rows [rows, rows_pad). 16-byte vectors; every thread of
 // the workgroup participates.
+// Loads in flight per thread while staging: a chunk costs one memory round
+// trip per kStageBatch * blockDim vectors instead of one per vector.
+constexpr int kStageBatch = 4;
+
 template <typename T, int D, int LDK>
 __device__ __forceinline__ void stage_rows(T* lds, const T* src, int rows, int rows_pad) {
   constexpr int VE = 16 / sizeof(T);
   constexpr int VPR = D / VE;
+  constexpr int U = kStageBatch;
   static_assert(D % VE == 0 && (LDK * sizeof(T)) % 16 == 0, "16-byte staging");
   const int total = rows_pad * VPR;
-  for (int v = threadIdx.x; v < total; v += blockDim.x) {
-    const int row = v / VPR, cv = v - row * VPR;
-    uint4 x = make_uint4(0u, 0u, 0u, 0u);
-    if (row < rows) x = *reinterpret_cast<const uint4*>(src + static_cast<size_t>(row) * D + cv * VE);
-    *reinterpret_cast<uint4*>(lds + row * LDK + cv * VE) = x;
+  for (int v0 = threadIdx.x; v0 < total; v0 += U * blockDim.x) {
+    uint4 x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int v = v0 + u * blockDim.x, row = v / VPR, cv = v - row * VPR;
+      x[u] = make_uint4(0u, 0u, 0u, 0u);
+      if (v < total && row < rows)
+        x[u] = *reinterpret_cast<const uint4*>(src + static_cast<size_t>(row) * D + cv * VE);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int v = v0 + u * blockDim.x, row = v / VPR, cv = v - row * VPR;
+      if (v < total) *reinterpret_cast<uint4*>(lds + row * LDK + cv * VE) = x[u];
+    }
   }
 }
 

@@ -12,10 +12,19 @@ namespace tarmac {
 
 constexpr int kIdxSentinel = 0x3fffffff;
 
-// max(a, b) on the median unit: v_med3_f32 needs no NaN canonicalisation of
-// its operands, unlike fmaxf (inputs here are never NaN).
+// +inf in an SGPR, from an instruction the compiler cannot fold.
+__device__ __forceinline__ float opaque_inf() {
+  float r;
+  asm("s_mov_b32 %0, 0x7f800000" : "=s"(r));
+  return r;
+}
+
+// max(a, b) as one v_med3_f32. The compiler's maxnum (fmaxf, or fmed3
+// against a literal +inf, which it folds to maxnum) first canonicalises every
+// operand it cannot prove canonical: one extra instruction per score here.
+// Inputs are never NaN.
 __device__ __forceinline__ float vmax(float a, float b) {
-  return __builtin_amdgcn_fmed3f(a, b, INFINITY);
+  return __builtin_amdgcn_fmed3f(a, b, opaque_inf());
 }
 
 template <int K>
@@ -54,6 +63,44 @@ __device__ __forceinline__ void topk_insert_lex(float (&val)[K], int (&ix)[K], f
 constexpr int kBlockTiles = 4;               // 16-key tiles per selection block
 constexpr int kBlockKeys = 16 * kBlockTiles;
 
+// Set the self pair and keys at or past kend to `masked`. q0 and kabs are
+// wave-uniform, so both tests are scalar branches and only the diagonal and
+// ragged blocks pay for the per-element selects. In the 16-key tile holding
+// a query tile's diagonal, lane l's element r is the self pair exactly when
+// 4*(l/16) + r == l % 16 (the loop-invariant lane predicate self_r[r]).
+template <int QT, int BT>
+__device__ __forceinline__ void mask_block(f32x4 (&s)[QT][BT], const bool (&self_r)[4], int q0,
+                                           int kabs, int kend, int grp, float masked) {
+  if (q0 < kabs + 16 * BT && kabs < q0 + 16 * QT) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int t = 0; t < BT; ++t) {
+        const bool diag_tile = (q0 + 16 * qt == kabs + 16 * t);  // uniform
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          s[qt][t][r] = (diag_tile && self_r[r]) ? masked : s[qt][t][r];
+      }
+  }
+  if (kabs + 16 * BT > kend) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int t = 0; t < BT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (kabs + 16 * t + 4 * grp + r >= kend) s[qt][t][r] = masked;
+  }
+}
+
+// Value-only insertion into a descending list: L max/med3 operations.
+template <int L>
+__device__ __forceinline__ void vinsert(float (&v)[L], float s) {
+#pragma unroll
+  for (int m = L - 1; m > 0; --m) v[m] = __builtin_amdgcn_fmed3f(v[m - 1], v[m], s);
+  v[0] = vmax(v[0], s);
+}
+
 // Scale (non power-of-two 1/sqrt(d)) and mask one block's scores: the self
 // pair and keys past the chunk end. Branches are wave-uniform. In the 16-key
 // tile holding a query tile's diagonal, lane l's element r is the self pair
@@ -69,26 +116,7 @@ __device__ __forceinline__ void prepare_block(f32x4 (&s)[QT][BT], float scale,
 #pragma unroll
       for (int t = 0; t < BT; ++t) s[qt][t] *= scale;
   }
-  if (q0 < kabs + 16 * BT && kabs < q0 + 16 * QT) {
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int t = 0; t < BT; ++t) {
-        const bool diag_tile = (q0 + 16 * qt == kabs + 16 * t);  // uniform
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          s[qt][t][r] = (diag_tile && self_r[r]) ? -INFINITY : s[qt][t][r];
-      }
-  }
-  if (kabs + 16 * BT > kend) {
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int t = 0; t < BT; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (kabs + 16 * t + 4 * grp + r >= kend) s[qt][t][r] = -INFINITY;
-  }
+  mask_block<QT, BT>(s, self_r, q0, kabs, kend, grp, -INFINITY);
 }
 
 template <int QT, int K>

@@ -77,7 +77,9 @@ struct ZorderArgs {
 hipError_t run_topk(const TopkArgs& a);
 hipError_t run_topk_filter(const TopkArgs& a);
 bool topk_filter_supported(int dtype, int d, int topk);
-extern int g_topk_filter_enabled;
+// tarmac_set_topk_filter modes
+constexpr int kFilterOff = 0, kFilterAuto = 1, kFilterAlways = 2;
+extern int g_topk_filter_mode;
 hipError_t run_dense(const DenseArgs& a);
 hipError_t run_fixedset(const FixedsetArgs& a);
 hipError_t run_morton_window(const MortonArgs& a);

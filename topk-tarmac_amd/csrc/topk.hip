@@ -334,10 +334,17 @@ static hipError_t dispatch_topk(const TopkArgs& a) {
   return launch_small<T, D>(a, a.key_chunk);
 }
 
-int g_topk_filter_enabled = 1;
+int g_topk_filter_mode = kFilterAuto;
+
+// Where the filter-and-verify kernel beats the plain fp32 pass (measured on
+// MI355X): its fixed per-query cost (split staging, merge, rescoring) pays
+// off once each query scans at least 512 keys.
+static bool filter_pays(const TopkArgs& a) { return a.N >= 512; }
 
 hipError_t run_topk(const TopkArgs& a) {
-  if (g_topk_filter_enabled && topk_filter_supported(a.dtype, a.d, a.topk)) return run_topk_filter(a);
+  if (g_topk_filter_mode != kFilterOff && topk_filter_supported(a.dtype, a.d, a.topk) &&
+      (g_topk_filter_mode == kFilterAlways || filter_pays(a)))
+    return run_topk_filter(a);
   if (a.dtype == kF32) {
     switch (a.d) {
       case 8: return dispatch_topk<float, 8>(a);

@@ -9,18 +9,23 @@
 //     >= 2^-16, which approximates the fp32 dot to
 //     |a - q.k| <= 2^-21 sum_c |q_c k_c| (representation 2^-22, bf16 MFMA
 //     accumulation measured <= 2^-21.9 of the term magnitudes); the canonical
-//     fp32 dot is within 2^-20 of q.k. Each lane keeps its best k candidates
-//     plus the value of the (k+1)-th, as in the exact kernel.
-//  2. verify: the k candidates are rescored in the canonical fp32 order. If
-//     the (k+1)-th filtered score plus eps = 2^-18 |q| max_j |k_j| (>= the
-//     bounds above, with margin) is strictly below every rescored candidate,
-//     no other key can reach the top k, so the candidates ARE the exact top k.
-//     Equal filtered scores anywhere in the merged list also fail the proof,
-//     which keeps the four lanes of a query on identical candidate lists.
-//  3. fallback: a wavefront with any unproven query recomputes its queries
-//     exactly (fp32 MFMA over all keys), so the result never depends on the
-//     filter -- only the time does (near-ties at the k-th score, e.g.
-//     duplicated keys, take the fallback).
+//     fp32 dot is within 2^-20 of q.k. Selection runs on packed values (the
+//     filter score with the key's position in its low mantissa bits, see
+//     pack8): each lane keeps its k+2 largest with max / med3 only, and the
+//     four lane lists of a query merge into k+1 candidates plus the (k+2)-th
+//     entry, identically on the four lanes.
+//  2. verify: the k+1 candidates are rescored in the canonical fp32 order and
+//     their exact top k taken. Every other key's filter score is at most C,
+//     the largest value that truncates like the (k+2)-th entry. If C plus
+//     eps = 2^-18 |q| max_j |k_j| (>= the bounds above, with margin), scaled,
+//     is strictly below the k-th exact score, no other key can reach the top
+//     k, so the result IS the exact top k. Rescoring one spare candidate
+//     settles near-ties between the k-th and (k+1)-th scores (duplicated keys
+//     included) without the fallback.
+//  3. fallback: a 16-query tile with any unproven query recomputes exactly
+//     (fp32 MFMA over all keys, rebuilt from the LDS copy when that holds
+//     them all), so the result never depends on the filter -- only the time
+//     does.
 //
 // Reference behaviour: src/kernels/fused_topk_attention.py:211-333 and
 // src/kernels/streaming_topk_attention.py:66-258 (including the retained
@@ -156,6 +161,18 @@ struct SplitFrag<32> : SplitFragWide<32> {};
 template <>
 struct SplitFrag<64> : SplitFragWide<64> {};
 
+// The fp32 value of a split element: (hi + mid + lo), both sums in fp32.
+__device__ __forceinline__ float rebuild(uint32_t hi, uint32_t mid, uint32_t lo, int half) {
+  const uint32_t m = half ? 0xffff0000u : 0x0000ffffu;
+  const int sh = half ? 0 : 16;
+  return (__uint_as_float((hi & m) << sh) + __uint_as_float((mid & m) << sh)) +
+         __uint_as_float((lo & m) << sh);
+}
+
+__device__ __forceinline__ bool rebuilds(float x0, float x1, uint32_t hi, uint32_t mid, uint32_t lo) {
+  return rebuild(hi, mid, lo, 0) == x0 && rebuild(hi, mid, lo, 1) == x1;
+}
+
 __device__ __forceinline__ uint2 pack_bf16x4(const __bf16 (&v)[4]) {
   uint2 p;
   p.x = __builtin_bit_cast(uint16_t, v[0]) | (uint32_t(__builtin_bit_cast(uint16_t, v[1])) << 16);
@@ -164,84 +181,105 @@ __device__ __forceinline__ uint2 pack_bf16x4(const __bf16 (&v)[4]) {
 }
 
 // Stage `rows` fp32 key rows as split bf16 rows (zero rows up to rows_pad) and
-// return this thread's max squared row norm.
+// return this thread's max squared row norm. exact is cleared if some element
+// is not rebuilt bit for bit by (hi + mid + lo) in fp32 (only for values near
+// the ends of the fp32 range, or NaN).
 template <int D>
-__device__ __forceinline__ float stage_split(bf16* lds, const float* src, int rows, int rows_pad) {
+__device__ __forceinline__ float stage_split(bf16* lds, const float* src, int rows, int rows_pad,
+                                         bool& exact) {
   constexpr int VPR = D / 4;  // float4 per row; VPR consecutive threads share a row
   constexpr int LDK = SplitFrag<D>::LDK;
+  constexpr int U = kStageBatch;
   float mx = 0.f;
-  const int total = rows_pad * VPR;
-  for (int v = threadIdx.x; v < total; v += blockDim.x) {
-    const int row = v / VPR, cv = v - row * VPR;
-    f32x4 x = {0.f, 0.f, 0.f, 0.f};
-    if (row < rows) x = *reinterpret_cast<const f32x4*>(src + static_cast<size_t>(row) * D + 4 * cv);
-    uint2 hi, mid, lo;
-    split3_pair(x[0], x[1], hi.x, mid.x, lo.x);
-    split3_pair(x[2], x[3], hi.y, mid.y, lo.y);
-    bf16* dst = lds + row * LDK + 4 * cv;
-    *reinterpret_cast<uint2*>(dst) = hi;
-    *reinterpret_cast<uint2*>(dst + D) = mid;
-    *reinterpret_cast<uint2*>(dst + 2 * D) = lo;
-    float n2 = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+  const int total = rows_pad * VPR;  // a multiple of 64: whole wavefronts agree on v < total
+  for (int v0 = threadIdx.x; v0 < total; v0 += U * blockDim.x) {
+    f32x4 x[U];
 #pragma unroll
-    for (int o = 1; o < VPR; o <<= 1) n2 += __shfl_xor(n2, o);
-    mx = fmaxf(mx, n2);
+    for (int u = 0; u < U; ++u) {
+      const int v = v0 + u * blockDim.x, row = v / VPR, cv = v - row * VPR;
+      x[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (v < total && row < rows)
+        x[u] = *reinterpret_cast<const f32x4*>(src + static_cast<size_t>(row) * D + 4 * cv);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int v = v0 + u * blockDim.x, row = v / VPR, cv = v - row * VPR;
+      if (v >= total) break;
+      uint2 hi, mid, lo;
+      split3_pair(x[u][0], x[u][1], hi.x, mid.x, lo.x);
+      split3_pair(x[u][2], x[u][3], hi.y, mid.y, lo.y);
+      bf16* dst = lds + row * LDK + 4 * cv;
+      *reinterpret_cast<uint2*>(dst) = hi;
+      *reinterpret_cast<uint2*>(dst + D) = mid;
+      *reinterpret_cast<uint2*>(dst + 2 * D) = lo;
+      exact = exact && rebuilds(x[u][0], x[u][1], hi.x, mid.x, lo.x) &&
+              rebuilds(x[u][2], x[u][3], hi.y, mid.y, lo.y);
+      float n2 = x[u][0] * x[u][0] + x[u][1] * x[u][1] + x[u][2] * x[u][2] + x[u][3] * x[u][3];
+#pragma unroll
+      for (int o = 1; o < VPR; o <<= 1) n2 += __shfl_xor(n2, o);
+      mx = fmaxf(mx, n2);
+    }
   }
   return mx;
 }
 
 // ---------------------------------------------------------------------------
-// exact fp32 pass for one wavefront (fallback): keys straight from HBM/L2
+// exact fp32 pass for one query tile (fallback)
 // ---------------------------------------------------------------------------
 
-template <int D, int K, int QT>
-__device__ __forceinline__ void exact_wave(const float* __restrict__ Qb, const float* __restrict__ Kb,
-                                        int N, int q0, float scale, int lane,
-                                        float (&val)[QT][K], int (&ix)[QT][K]) {
+// The tile's exact top-k lists (merged over the four lanes of each query), in
+// the canonical fp32 order. from_lds (wave-uniform): key rows are rebuilt from
+// the split rows resident in LDS (all N keys, each rebuilt exactly);
+// otherwise they come from global memory.
+template <int D, int K>
+__device__ __forceinline__ void exact_tile(const float* __restrict__ Qb,
+                                           const float* __restrict__ Kb, const bf16* Ks,
+                                           bool from_lds, int N, int qbase, float scale, int lane,
+                                           float (&val)[K], int (&ix)[K]) {
   using F = Frag<float, D>;
   constexpr bool POW2 = pow2_scale<D>();
+  constexpr int E = F::E;
+  constexpr int LDK = SplitFrag<D>::LDK;
   const int col = lane & 15, grp = lane >> 4;
-  F frag[QT];
-  int self[QT];
+  const int self = qbase + col;
+  F frag;
+  frag.load_q(Qb + static_cast<size_t>(min(self, N - 1)) * D, grp, POW2 ? scale : 1.f);
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    self[qt] = q0 + 16 * qt + col;
-    frag[qt].load_q(Qb + static_cast<size_t>(min(self[qt], N - 1)) * D, grp, POW2 ? scale : 1.f);
-#pragma unroll
-    for (int m = 0; m < K; ++m) { val[qt][m] = -INFINITY; ix[qt][m] = kIdxSentinel; }
-  }
+  for (int m = 0; m < K; ++m) { val[m] = -INFINITY; ix[m] = kIdxSentinel; }
   for (int kb = 0; kb < N; kb += 16) {
     typename F::KF kf;
-    const int row = min(kb + col, N - 1);
-    ld_f32<F::E>(kf.v, Kb + static_cast<size_t>(row) * D + grp * F::E);
+    if (from_lds) {
+      // rows [N, 16 * ceil(N / 16)) are staged zero rows
+      const bf16* r = Ks + (kb + col) * LDK + grp * E;
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      f32x4 s = {0.f, 0.f, 0.f, 0.f};
+      for (int e = 0; e < E; ++e)
+        kf.v[e] = (bf16_to_f32(r[e]) + bf16_to_f32(r[D + e])) + bf16_to_f32(r[2 * D + e]);
+    } else {
+      ld_f32<E>(kf.v, Kb + static_cast<size_t>(min(kb + col, N - 1)) * D + grp * E);
+    }
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < F::NI; ++i) s = frag[qt].step(kf, i, s);
+    for (int i = 0; i < F::NI; ++i) s = frag.step(kf, i, s);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = kb + 4 * grp + r;
-        float v = POW2 ? s[r] : s[r] * scale;
-        if (key >= N || key == self[qt]) v = -INFINITY;
-        topk_insert<K>(val[qt], ix[qt], v, key);
-      }
+    for (int r = 0; r < 4; ++r) {
+      const int key = kb + 4 * grp + r;
+      float v = POW2 ? s[r] : s[r] * scale;
+      if (key >= N || key == self) v = -INFINITY;
+      topk_insert<K>(val, ix, v, key);
     }
   }
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt)
+  for (int step = 16; step <= 32; step <<= 1) {
+    float pv[K];
+    int pi[K];
 #pragma unroll
-    for (int step = 16; step <= 32; step <<= 1) {
-      float pv[K];
-      int pi[K];
-#pragma unroll
-      for (int m = 0; m < K; ++m) {
-        pv[m] = __shfl_xor(val[qt][m], step);
-        pi[m] = __shfl_xor(ix[qt][m], step);
-      }
-#pragma unroll
-      for (int m = 0; m < K; ++m) topk_insert_lex<K>(val[qt], ix[qt], pv[m], pi[m]);
+    for (int m = 0; m < K; ++m) {
+      pv[m] = __shfl_xor(val[m], step);
+      pi[m] = __shfl_xor(ix[m], step);
     }
+#pragma unroll
+    for (int m = 0; m < K; ++m) topk_insert_lex<K>(val, ix, pv[m], pi[m]);
+  }
 }
 
 // Canonical fp32 score of one (query row, key row) pair: fmaf chain with
@@ -268,8 +306,60 @@ __device__ __forceinline__ float canon_pair(const float* qrow, const float* krow
 
 constexpr float kFilterEps = 1.0f / 262144.0f;  // 2^-18
 
-template <int D, int K, int QT>
-__global__ void __launch_bounds__(256)
+// Waves per workgroup: every wave of a workgroup shares one staged key chunk,
+// so larger groups stage each batch row's keys fewer times and amortise the
+// LDS copy over more queries.
+constexpr int kFilterMaxWaves = 8;
+
+// Packed candidates. During the scan a lane's filter score keeps its top 24
+// bits and carries, in the low 8 mantissa bits, the key's position
+// u = 4 * tile + r within the current 1024-key segment (the lane sees keys
+// seg + 16 * tile + 4 * grp + r, tile < 64, r < 4). Clearing low bits rounds
+// toward zero, a monotone map, so packed order refines the order of the
+// truncated scores and distinct keys give distinct packed values: the scan
+// keeps values only (max / med3) and the key comes back from the bits.
+constexpr int kSegKeys = 1024;
+constexpr uint32_t kLow8 = 0xffu, kLow10 = 0x3ffu;
+constexpr float kMasked = -3.40282347e38f;   // -FLT_MAX: stays finite when packed
+constexpr float kMaskedBelow = -1.0e38f;     // list entries below this are masked keys
+constexpr float kNormLimit = 1.329228e36f;   // 2^120: |q| max|k| at or above fails the proof
+
+// Bits 8..31 from s, bits 0..7 from u (< 256): one v_perm_b32 (the compiler
+// turns the and/or form into two instructions).
+__device__ __forceinline__ float pack8(float s, uint32_t u) {
+  return __uint_as_float(__builtin_amdgcn_perm(__float_as_uint(s), u, 0x07060500u));
+}
+
+// Largest value whose truncation (bits `mask` cleared) is at most trunc(t).
+__device__ __forceinline__ float trunc_ceiling(float t, uint32_t mask) {
+  const uint32_t b = __float_as_uint(t) & ~mask;
+  return __uint_as_float((b & 0x80000000u) ? b : (b | mask));
+}
+
+// Decode a lane's packed segment list into (truncated score, key) pairs, fold
+// them into its running list and restart the segment list. lane_base is the
+// segment's first key plus 4 * grp. The running list stays in (score desc,
+// key asc) order, so the four lanes of a query merge to identical lists even
+// where truncated scores tie.
+template <int QT, int L>
+__device__ __forceinline__ void flush_segment(float (&pv)[QT][L], float (&rv)[QT][L],
+                                              int (&ri)[QT][L], int lane_base) {
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int m = 0; m < L; ++m) {
+      const uint32_t bits = __float_as_uint(pv[qt][m]);
+      const int u = static_cast<int>(bits & kLow8);
+      topk_insert_lex<L>(rv[qt], ri[qt], __uint_as_float(bits & ~kLow8),
+                         lane_base + 16 * (u >> 2) + (u & 3));
+      pv[qt][m] = kMasked;
+    }
+}
+
+// ONESEG: one chunk of at most one segment holds every key (kc >= N, N <= 1024),
+// so the lists stay packed until the merge.
+template <int D, int K, int QT, bool ONESEG>
+__global__ void __launch_bounds__(kFilterMaxWaves * 64, 5)
 topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
                    const float* __restrict__ V, float* __restrict__ O, int32_t* __restrict__ Idx,
                    int N, int n_qblk, int kc, float scale, int nblocks) {
@@ -277,15 +367,19 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   constexpr int LDK = SF::LDK;
   constexpr int EO = D / 4;
   constexpr int BT = kBlockTiles;
+  constexpr int C = K + 1;  // candidates rescored exactly
+  constexpr int L = K + 2;  // list length: the candidates and the (k+2)-th
   constexpr bool POW2 = pow2_scale<D>();
   extern __shared__ __align__(16) unsigned char smem_raw[];
   bf16* Ks = reinterpret_cast<bf16*>(smem_raw + 16);
-  unsigned* kmax_slot = reinterpret_cast<unsigned*>(smem_raw);
+  unsigned* kmax_slot = reinterpret_cast<unsigned*>(smem_raw);      // max |k|^2 of the chunk
+  unsigned* inexact_slot = kmax_slot + 1;  // some staged element is not rebuilt exactly
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int blk = xcd_logical_block(blockIdx.x, nblocks);
   const int b = blk / n_qblk, qblk = blk - b * n_qblk;
-  const int q0 = (qblk * nw + wave) * 16 * QT;
+  const int q0 = (qblk * nw + wave) * 16 * QT;  // wave-uniform
   const int col = lane & 15, grp = lane >> 4;
   const size_t boff = static_cast<size_t>(b) * N * D;
   const float* Qb = Q + boff;
@@ -302,24 +396,30 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
 #pragma unroll
   for (int r = 0; r < 4; ++r) self_r[r] = (4 * grp + r == col);
 
-  float val[QT][K + 1];
-  int ix[QT][K];
+  float pv[QT][L];  // packed scores of the current segment
+  float rv[QT][L];  // finished segments: truncated scores ...
+  int ri[QT][L];    // ... and their keys
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
+  for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-    for (int m = 0; m <= K; ++m) val[qt][m] = -INFINITY;
-#pragma unroll
-    for (int m = 0; m < K; ++m) ix[qt][m] = kIdxSentinel;
-  }
-  int base = 0;
+    for (int m = 0; m < L; ++m) {
+      pv[qt][m] = kMasked;
+      rv[qt][m] = kMasked;
+      ri[qt][m] = kIdxSentinel;
+    }
   float kmax2 = 0.f;
 
   for (int c0 = 0; c0 < N; c0 += kc) {
     const int cn = min(kc, N - c0);
     const int cnb = (cn + kBlockKeys - 1) / kBlockKeys * kBlockKeys;
     __syncthreads();
-    if (threadIdx.x == 0) *kmax_slot = 0u;
-    const float mine = stage_split<D>(Ks, Kb + static_cast<size_t>(c0) * D, cn, cnb);
+    if (threadIdx.x == 0) {
+      *kmax_slot = 0u;
+      *inexact_slot = 0u;
+    }
+    bool exact = true;
+    const float mine = stage_split<D>(Ks, Kb + static_cast<size_t>(c0) * D, cn, cnb, exact);
+    if (!exact) atomicOr(inexact_slot, 1u);
     __syncthreads();
     atomicMax(kmax_slot, __float_as_uint(mine));  // non-negative: bit order is value order
     if (q0 < N) {
@@ -338,62 +438,109 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
             for (int qt = 0; qt < QT; ++qt) s[qt][t] = frag[qt].step(kf, i, s[qt][t]);
         }
         // raw (unscaled) filter scores: scaling does not change the order
-        prepare_block<QT, BT, true>(s, 1.f, self_r, q0, kabs, kend, grp);
-        rebase_list<QT, K>(ix, kabs - base);
-        base = kabs;
+        const uint32_t u0 = static_cast<uint32_t>(kb0 & (kSegKeys - 1)) >> 2;
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
           for (int t = 0; t < BT; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              topk_insert_x<K>(val[qt], ix[qt], s[qt][t][r], 16 * t + r);
+            for (int r = 0; r < 4; ++r) s[qt][t][r] = pack8(s[qt][t][r], u0 + 4 * t + r);
+        mask_block<QT, BT>(s, self_r, q0, kabs, kend, grp, kMasked);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+          for (int t = 0; t < BT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) vinsert<L>(pv[qt], s[qt][t][r]);
+        const int next = kb0 + kBlockKeys;
+        if (!ONESEG && ((next & (kSegKeys - 1)) == 0 || next >= cnb))
+          flush_segment<QT, L>(pv, rv, ri, c0 + (kb0 & ~(kSegKeys - 1)) + 4 * grp);
       }
     }
     __syncthreads();
     kmax2 = fmaxf(kmax2, __uint_as_float(*kmax_slot));
   }
   if (q0 >= N) return;
-  rebase_list<QT, K>(ix, -base);
+  // the exact fallback may rebuild keys from LDS: one chunk holds them all
+  const bool lds_exact = ONESEG && *inexact_slot == 0u;
 
-  // ---- merge the four lane lists of each query --------------------------
+  // ---- merge the four lane lists of each query ---------------------------
+  // cand: the k+1 candidates (identical on the four lanes of a query;
+  // -1 for a masked entry); ceil_f: no other key's filter score exceeds it.
+  int cand[QT][C];
+  float ceil_f[QT];
+  if constexpr (ONESEG) {
+    const uint32_t mmask = N <= 256 ? kLow8 : kLow10;
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
+      // repack with the lane group (low bits = 4 * u + grp; u < 64 fits 8 bits
+      // when N <= 256) and re-sort: entries equal above those bits may change order
+      float p[L];
 #pragma unroll
-    for (int m = 0; m < K; ++m) ix[qt][m] += 4 * grp;
+      for (int m = 0; m < L; ++m) p[m] = kMasked;
 #pragma unroll
-    for (int step = 16; step <= 32; step <<= 1) {
-      float pv[K + 1];
-      int pi[K];
+      for (int m = 0; m < L; ++m) {
+        const uint32_t bits = __float_as_uint(pv[qt][m]);
+        vinsert<L>(p, __uint_as_float((bits & ~mmask) | ((bits & kLow8) << 2) |
+                                      static_cast<uint32_t>(grp)));
+      }
 #pragma unroll
-      for (int m = 0; m <= K; ++m) pv[m] = __shfl_xor(val[qt][m], step);
+      for (int step = 16; step <= 32; step <<= 1) {
+        float o[L];
 #pragma unroll
-      for (int m = 0; m < K; ++m) pi[m] = __shfl_xor(ix[qt][m], step);
+        for (int m = 0; m < L; ++m) o[m] = __shfl_xor(p[m], step);
 #pragma unroll
-      for (int m = 0; m < K; ++m) topk_insert_x<K>(val[qt], ix[qt], pv[m], pi[m]);
-      topk_insert_x<K>(val[qt], ix[qt], pv[K], kIdxSentinel);
+        for (int m = 0; m < L; ++m) vinsert<L>(p, o[m]);
+      }
+#pragma unroll
+      for (int m = 0; m < C; ++m) {
+        const int w = static_cast<int>(__float_as_uint(p[m]) & mmask), u = w >> 2;
+        cand[qt][m] = p[m] < kMaskedBelow ? -1 : 16 * (u >> 2) + 4 * (w & 3) + (u & 3);
+      }
+      ceil_f[qt] = trunc_ceiling(p[C], mmask);
+    }
+  } else {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+      for (int step = 16; step <= 32; step <<= 1) {
+        float ov[L];
+        int oi[L];
+#pragma unroll
+        for (int m = 0; m < L; ++m) {
+          ov[m] = __shfl_xor(rv[qt][m], step);
+          oi[m] = __shfl_xor(ri[qt][m], step);
+        }
+#pragma unroll
+        for (int m = 0; m < L; ++m) topk_insert_lex<L>(rv[qt], ri[qt], ov[m], oi[m]);
+      }
+#pragma unroll
+      for (int m = 0; m < C; ++m) cand[qt][m] = rv[qt][m] < kMaskedBelow ? -1 : ri[qt][m];
+      ceil_f[qt] = trunc_ceiling(rv[qt][C], kLow8);
     }
   }
 
   // ---- verify: rescore the candidates exactly ---------------------------
   const float kmax = sqrtf(kmax2);
-  float ex[QT][K];
-  bool ok = true;
+  float val[QT][K];
+  int ix[QT][K];
+  bool ok[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int qi = min(self[qt], N - 1);
     const float* qrow = Qb + static_cast<size_t>(qi) * D;
     // lane group g rescores candidates g, g+4, ...
-    float mine[(K + 3) / 4];
+    float mine[(C + 3) / 4];
 #pragma unroll
-    for (int u = 0; u < (K + 3) / 4; ++u) {
+    for (int u = 0; u < (C + 3) / 4; ++u) {
       const int m = 4 * u + grp;
-      int cand = kIdxSentinel;
+      int c = -1;
 #pragma unroll
-      for (int mm = 0; mm < K; ++mm)
-        if (mm == m) cand = ix[qt][mm];
-      const int row = min(max(cand, 0), N - 1);
-      mine[u] = canon_pair<D, POW2>(qrow, Kb + static_cast<size_t>(row) * D, scale);
+      for (int mm = 0; mm < C; ++mm)
+        if (mm == m) c = cand[qt][mm];
+      const int row = min(max(c, 0), N - 1);
+      const float e = canon_pair<D, POW2>(qrow, Kb + static_cast<size_t>(row) * D, scale);
+      mine[u] = c < 0 ? -INFINITY : e;
     }
     float qn2 = 0.f;
     {
@@ -402,40 +549,21 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
 #pragma unroll
       for (int c = 0; c < D; ++c) qn2 = fmaf(qf[c], qf[c], qn2);
     }
-    float worst = INFINITY;
+    // the exact top k of the candidates, in (score desc, index asc) order
 #pragma unroll
-    for (int m = 0; m < K; ++m) {
-      ex[qt][m] = __shfl(mine[m / 4], col + 16 * (m % 4));
-      worst = fminf(worst, ex[qt][m]);
-    }
-    const float bound = (val[qt][K] + kFilterEps * sqrtf(qn2) * kmax) * scale;
-    bool distinct = true;  // strictly decreasing filtered values: the lane lists agree
+    for (int m = 0; m < K; ++m) { val[qt][m] = -INFINITY; ix[qt][m] = kIdxSentinel; }
 #pragma unroll
-    for (int m = 0; m < K; ++m) distinct = distinct && val[qt][m] > val[qt][m + 1];
-    ok = ok && (self[qt] >= N || (distinct && bound < worst));
+    for (int m = 0; m < C; ++m)
+      topk_insert_lex<K>(val[qt], ix[qt], __shfl(mine[m / 4], col + 16 * (m % 4)), cand[qt][m]);
+    const float nprod = sqrtf(qn2) * kmax;
+    const float bound = (ceil_f[qt] + kFilterEps * nprod) * scale;
+    ok[qt] = self[qt] >= N || (nprod < kNormLimit && bound < val[qt][K - 1]);
   }
 
-  if (__all(ok)) {
-    // the candidates are the exact top k: order them by exact score
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      float sv[K];
-      int si[K];
-#pragma unroll
-      for (int m = 0; m < K; ++m) { sv[m] = -INFINITY; si[m] = kIdxSentinel; }
-#pragma unroll
-      for (int m = 0; m < K; ++m) topk_insert_lex<K>(sv, si, ex[qt][m], ix[qt][m]);
-#pragma unroll
-      for (int m = 0; m < K; ++m) { val[qt][m] = sv[m]; ix[qt][m] = si[m]; }
-    }
-  } else {
-    float ev[QT][K];
-    int ei[QT][K];
-    exact_wave<D, K, QT>(Qb, Kb, N, q0, scale, lane, ev, ei);
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int m = 0; m < K; ++m) { val[qt][m] = ev[qt][m]; ix[qt][m] = ei[qt][m]; }
+  for (int qt = 0; qt < QT; ++qt) {
+    if (!__all(ok[qt]))
+      exact_tile<D, K>(Qb, Kb, Ks, lds_exact, N, q0 + 16 * qt, scale, lane, val[qt], ix[qt]);
   }
 
   // ---- k-softmax and gathered aggregation --------------------------------
@@ -480,7 +608,7 @@ static hipError_t launch_filter(const TopkArgs& a, int kc) {
   constexpr int QT = kTopkQueryTiles;
   const int per_wave = 16 * QT;
   const int waves = (a.N + per_wave - 1) / per_wave;
-  const int nw = waves >= 4 ? 4 : waves;
+  const int nw = waves >= kFilterMaxWaves ? kFilterMaxWaves : waves;
   const int qb = per_wave * nw;
   const int n_qblk = (a.N + qb - 1) / qb;
   const int nblocks = a.B * n_qblk;
@@ -490,10 +618,15 @@ static hipError_t launch_filter(const TopkArgs& a, int kc) {
   const float* v = static_cast<const float*>(a.v);
   float* o = static_cast<float*>(a.out);
   hipStream_t st = static_cast<hipStream_t>(a.stream);
-#define TARMAC_FILTER_CASE(KK)                                                                  \
-  case KK:                                                                                      \
-    hipLaunchKernelGGL((topk_filter_kernel<D, KK, QT>), dim3(nblocks), dim3(64 * nw), lds, st, \
-                       q, k, v, o, a.idx, a.N, n_qblk, kc, a.scale, nblocks);                  \
+  const bool oneseg = kc >= a.N && a.N <= kSegKeys;
+#define TARMAC_FILTER_CASE(KK)                                                                 \
+  case KK:                                                                                     \
+    if (oneseg)                                                                                \
+      hipLaunchKernelGGL((topk_filter_kernel<D, KK, QT, true>), dim3(nblocks), dim3(64 * nw), \
+                         lds, st, q, k, v, o, a.idx, a.N, n_qblk, kc, a.scale, nblocks);      \
+    else                                                                                       \
+      hipLaunchKernelGGL((topk_filter_kernel<D, KK, QT, false>), dim3(nblocks), dim3(64 * nw), \
+                         lds, st, q, k, v, o, a.idx, a.N, n_qblk, kc, a.scale, nblocks);      \
     break;
   switch (a.topk) {
     TARMAC_FILTER_CASE(1)
