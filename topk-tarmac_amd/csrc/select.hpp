@@ -60,6 +60,24 @@ __device__ __forceinline__ void topk_insert_lex(float (&val)[K], int (&ix)[K], f
   ix[0] = c0 ? j : ix[0];
 }
 
+// Sort n (value, index) pairs by (value desc, index asc): odd-even
+// transposition network, n rounds of compare-exchange.
+template <int n>
+__device__ __forceinline__ void sort_lex(float (&v)[n], int (&ix)[n]) {
+#pragma unroll
+  for (int round = 0; round < n; ++round)
+#pragma unroll
+    for (int a = round & 1; a + 1 < n; a += 2) {
+      const bool sw = ranks_before(v[a + 1], ix[a + 1], v[a], ix[a]);
+      const float va = v[a];
+      const int ia = ix[a];
+      v[a] = sw ? v[a + 1] : va;
+      ix[a] = sw ? ix[a + 1] : ia;
+      v[a + 1] = sw ? va : v[a + 1];
+      ix[a + 1] = sw ? ia : ix[a + 1];
+    }
+}
+
 constexpr int kBlockTiles = 4;               // 16-key tiles per selection block
 constexpr int kBlockKeys = 16 * kBlockTiles;
 

@@ -337,9 +337,10 @@ static hipError_t dispatch_topk(const TopkArgs& a) {
 int g_topk_filter_mode = kFilterAuto;
 
 // Where the filter-and-verify kernel beats the plain fp32 pass (measured on
-// MI355X): its fixed per-query cost (split staging, merge, rescoring) pays
-// off once each query scans at least 512 keys.
-static bool filter_pays(const TopkArgs& a) { return a.N >= 512; }
+// MI355X, d = 16): its fixed per-query cost (split staging, merge, exact
+// rescoring) pays off once each query scans 512 keys, or 256 keys when the
+// plain pass's per-score selection cost grows with k >= 3.
+static bool filter_pays(const TopkArgs& a) { return a.N >= 512 || (a.N >= 256 && a.topk >= 3); }
 
 hipError_t run_topk(const TopkArgs& a) {
   if (g_topk_filter_mode != kFilterOff && topk_filter_supported(a.dtype, a.d, a.topk) &&

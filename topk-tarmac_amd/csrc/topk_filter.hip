@@ -51,9 +51,12 @@ __device__ __forceinline__ void split3_bf16(float x, __bf16& hi, __bf16& mid, __
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // Two elements at a time: one packed conversion per part (v_cvt_pk_bf16_f32),
-// results already packed as bf16 pairs.
+// results already packed as bf16 pairs. exact: both elements satisfy
+// x == hi + mid + lo exactly (the last residual is representable in bf16;
+// then the fp32 sums (hi + mid) + lo rebuild x bit for bit). It fails only
+// near the ends of the fp32 range, or for NaN.
 __device__ __forceinline__ void split3_pair(float x0, float x1, uint32_t& hi, uint32_t& mid,
-                                            uint32_t& lo) {
+                                            uint32_t& lo, bool& exact) {
   bf16x2_t h = {static_cast<__bf16>(x0), static_cast<__bf16>(x1)};
   hi = __builtin_bit_cast(uint32_t, h);
   const float r0 = x0 - __uint_as_float(hi << 16), r1 = x1 - __uint_as_float(hi & 0xffff0000u);
@@ -62,6 +65,13 @@ __device__ __forceinline__ void split3_pair(float x0, float x1, uint32_t& hi, ui
   const float s0 = r0 - __uint_as_float(mid << 16), s1 = r1 - __uint_as_float(mid & 0xffff0000u);
   bf16x2_t l = {static_cast<__bf16>(s0), static_cast<__bf16>(s1)};
   lo = __builtin_bit_cast(uint32_t, l);
+  exact = __uint_as_float(lo << 16) == s0 && __uint_as_float(lo & 0xffff0000u) == s1;
+}
+
+__device__ __forceinline__ void split3_pair(float x0, float x1, uint32_t& hi, uint32_t& mid,
+                                            uint32_t& lo) {
+  bool unused;
+  split3_pair(x0, x1, hi, mid, lo, unused);
 }
 
 // The six products whose size is >= 2^-16 of q.k are formed:
@@ -70,44 +80,51 @@ __device__ __forceinline__ void split3_pair(float x0, float x1, uint32_t& hi, ui
 template <int D>
 struct SplitFrag;
 
-// d = 16: three 16x16x32 steps, each contraction = two 16-wide products:
-//   step 0: A = [k_hi  | k_hi ], B = [q_hi  | q_mid]
-//   step 1: A = [k_mid | k_lo ], B = [q_hi  | q_hi ]
-//   step 2: A = [k_mid | k_hi ], B = [q_mid | q_lo ]
+// d = 16: three 16x16x32 steps over two distinct key operands, from rows
+// stored as lo[16] hi[16] mid[16] pad[8] (two 16-byte LDS reads per tile):
+//   A1 = [k_hi | k_mid] (halves 16..47), A2 = [k_lo | k_hi] (halves 0..31)
+//   step 0: A1 x [q_hi  | q_hi ] = hi.hi + mid.hi
+//   step 1: A1 x [q_mid | q_mid] = hi.mid + mid.mid
+//   step 2: A2 x [q_hi  | q_lo ] = lo.hi + hi.lo
 template <>
 struct SplitFrag<16> {
-  static constexpr int LDK = 3 * 16 + 8;  // bf16 per LDS row: hi[16] mid[16] lo[16] pad
+  static constexpr int LDK = 3 * 16 + 8;
+  static constexpr int OFF_L = 0, OFF_H = 16, OFF_M = 32;  // part offsets in a row
   static constexpr int NI = 3;
   bf16x8 q[3];
-  __device__ __forceinline__ void load_q(const float* qrow, int grp) {
+  // Returns the sum of squares of the 8 elements this lane loaded; lane
+  // groups g and g ^ 1 together hold the whole row.
+  __device__ __forceinline__ float load_q(const float* qrow, int grp) {
     float x[8];
     ld_f32<8>(x, qrow + 8 * (grp & 1));
     const bool lower = grp < 2;
     uint32_t h[4], m[4], l[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) split3_pair(x[2 * e], x[2 * e + 1], h[e], m[e], l[e]);
-    uint32_t w0[4], w2[4];
+    uint32_t w2[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      w0[e] = lower ? h[e] : m[e];
-      w2[e] = lower ? m[e] : l[e];
-    }
-    q[0] = __builtin_bit_cast(bf16x8, w0);
-    q[1] = __builtin_bit_cast(bf16x8, h);
+    for (int e = 0; e < 4; ++e) w2[e] = lower ? h[e] : l[e];
+    q[0] = __builtin_bit_cast(bf16x8, h);
+    q[1] = __builtin_bit_cast(bf16x8, m);
     q[2] = __builtin_bit_cast(bf16x8, w2);
+    float n2 = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) n2 = fmaf(x[e], x[e], n2);
+    return n2;
   }
-  struct KF { bf16x8 a[3]; };
+  // |q|^2 from the per-lane sums of load_q
+  __device__ __forceinline__ static float row_norm2(float part) {
+    return part + __shfl_xor(part, 16);
+  }
+  struct KF { bf16x8 a[2]; };
   __device__ __forceinline__ static KF load_k(const bf16* krow, int grp) {
-    const int off = 8 * (grp & 1);
-    const bool lower = grp < 2;
     KF f;
-    f.a[0] = *reinterpret_cast<const bf16x8*>(krow + off);                         // hi
-    f.a[1] = *reinterpret_cast<const bf16x8*>(krow + (lower ? 16 : 32) + off);    // mid | lo
-    f.a[2] = *reinterpret_cast<const bf16x8*>(krow + (lower ? 16 : 0) + off);     // mid | hi
+    f.a[0] = *reinterpret_cast<const bf16x8*>(krow + OFF_H + 8 * grp);  // [hi | mid]
+    f.a[1] = *reinterpret_cast<const bf16x8*>(krow + OFF_L + 8 * grp);  // [lo | hi]
     return f;
   }
   __device__ __forceinline__ f32x4 step(const KF& kf, int i, f32x4 acc) const {
-    return mfma_bf16_16x16x32(kf.a[i], q[i], acc);
+    return mfma_bf16_16x16x32(kf.a[i == 2 ? 1 : 0], q[i], acc);
   }
 };
 
@@ -117,13 +134,19 @@ struct SplitFragWide {
   static_assert(D == 32 || D == 64, "split fragment width");
   static constexpr int NH = D / 32;
   static constexpr int LDK = 3 * D + 8;  // hi[D] mid[D] lo[D] pad
+  static constexpr int OFF_H = 0, OFF_M = D, OFF_L = 2 * D;  // part offsets in a row
   static constexpr int NI = 6 * NH;
   bf16x8 qh[NH], qm[NH], ql[NH];
-  __device__ __forceinline__ void load_q(const float* qrow, int grp) {
+  // Returns the sum of squares of the elements this lane loaded; the four
+  // lane groups together hold the whole row.
+  __device__ __forceinline__ float load_q(const float* qrow, int grp) {
+    float n2 = 0.f;
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
       float x[8];
       ld_f32<8>(x, qrow + 32 * h + 8 * grp);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) n2 = fmaf(x[e], x[e], n2);
       uint32_t a[4], b[4], c[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) split3_pair(x[2 * e], x[2 * e + 1], a[e], b[e], c[e]);
@@ -131,6 +154,11 @@ struct SplitFragWide {
       qm[h] = __builtin_bit_cast(bf16x8, b);
       ql[h] = __builtin_bit_cast(bf16x8, c);
     }
+    return n2;
+  }
+  __device__ __forceinline__ static float row_norm2(float part) {
+    part += __shfl_xor(part, 16);
+    return part + __shfl_xor(part, 32);
   }
   struct KF { bf16x8 hi[NH], mid[NH], lo[NH]; };
   __device__ __forceinline__ static KF load_k(const bf16* krow, int grp) {
@@ -160,18 +188,6 @@ template <>
 struct SplitFrag<32> : SplitFragWide<32> {};
 template <>
 struct SplitFrag<64> : SplitFragWide<64> {};
-
-// The fp32 value of a split element: (hi + mid + lo), both sums in fp32.
-__device__ __forceinline__ float rebuild(uint32_t hi, uint32_t mid, uint32_t lo, int half) {
-  const uint32_t m = half ? 0xffff0000u : 0x0000ffffu;
-  const int sh = half ? 0 : 16;
-  return (__uint_as_float((hi & m) << sh) + __uint_as_float((mid & m) << sh)) +
-         __uint_as_float((lo & m) << sh);
-}
-
-__device__ __forceinline__ bool rebuilds(float x0, float x1, uint32_t hi, uint32_t mid, uint32_t lo) {
-  return rebuild(hi, mid, lo, 0) == x0 && rebuild(hi, mid, lo, 1) == x1;
-}
 
 __device__ __forceinline__ uint2 pack_bf16x4(const __bf16 (&v)[4]) {
   uint2 p;
@@ -206,14 +222,14 @@ __device__ __forceinline__ float stage_split(bf16* lds, const float* src, int ro
       const int v = v0 + u * blockDim.x, row = v / VPR, cv = v - row * VPR;
       if (v >= total) break;
       uint2 hi, mid, lo;
-      split3_pair(x[u][0], x[u][1], hi.x, mid.x, lo.x);
-      split3_pair(x[u][2], x[u][3], hi.y, mid.y, lo.y);
+      bool e0, e1;
+      split3_pair(x[u][0], x[u][1], hi.x, mid.x, lo.x, e0);
+      split3_pair(x[u][2], x[u][3], hi.y, mid.y, lo.y, e1);
+      exact = exact && e0 && e1;
       bf16* dst = lds + row * LDK + 4 * cv;
-      *reinterpret_cast<uint2*>(dst) = hi;
-      *reinterpret_cast<uint2*>(dst + D) = mid;
-      *reinterpret_cast<uint2*>(dst + 2 * D) = lo;
-      exact = exact && rebuilds(x[u][0], x[u][1], hi.x, mid.x, lo.x) &&
-              rebuilds(x[u][2], x[u][3], hi.y, mid.y, lo.y);
+      *reinterpret_cast<uint2*>(dst + SplitFrag<D>::OFF_H) = hi;
+      *reinterpret_cast<uint2*>(dst + SplitFrag<D>::OFF_M) = mid;
+      *reinterpret_cast<uint2*>(dst + SplitFrag<D>::OFF_L) = lo;
       float n2 = x[u][0] * x[u][0] + x[u][1] * x[u][1] + x[u][2] * x[u][2] + x[u][3] * x[u][3];
 #pragma unroll
       for (int o = 1; o < VPR; o <<= 1) n2 += __shfl_xor(n2, o);
@@ -253,7 +269,8 @@ __device__ __forceinline__ void exact_tile(const float* __restrict__ Qb,
       const bf16* r = Ks + (kb + col) * LDK + grp * E;
 #pragma unroll
       for (int e = 0; e < E; ++e)
-        kf.v[e] = (bf16_to_f32(r[e]) + bf16_to_f32(r[D + e])) + bf16_to_f32(r[2 * D + e]);
+        kf.v[e] = (bf16_to_f32(r[SplitFrag<D>::OFF_H + e]) + bf16_to_f32(r[SplitFrag<D>::OFF_M + e])) +
+                  bf16_to_f32(r[SplitFrag<D>::OFF_L + e]);
     } else {
       ld_f32<E>(kf.v, Kb + static_cast<size_t>(min(kb + col, N - 1)) * D + grp * E);
     }
@@ -310,6 +327,8 @@ constexpr float kFilterEps = 1.0f / 262144.0f;  // 2^-18
 // so larger groups stage each batch row's keys fewer times and amortise the
 // LDS copy over more queries.
 constexpr int kFilterMaxWaves = 8;
+// 16-key tiles per selection block (the unit of masking and packing)
+constexpr int kFilterBlockTiles = 4;
 
 // Packed candidates. During the scan a lane's filter score keeps its top 24
 // bits and carries, in the low 8 mantissa bits, the key's position
@@ -366,7 +385,7 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   using SF = SplitFrag<D>;
   constexpr int LDK = SF::LDK;
   constexpr int EO = D / 4;
-  constexpr int BT = kBlockTiles;
+  constexpr int BT = kFilterBlockTiles;
   constexpr int C = K + 1;  // candidates rescored exactly
   constexpr int L = K + 2;  // list length: the candidates and the (k+2)-th
   constexpr bool POW2 = pow2_scale<D>();
@@ -387,10 +406,11 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
 
   SF frag[QT];
   int self[QT];
+  float qn2[QT];  // |q|^2 of this lane's query
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     self[qt] = q0 + 16 * qt + col;
-    frag[qt].load_q(Qb + static_cast<size_t>(min(self[qt], N - 1)) * D, grp);
+    qn2[qt] = SF::row_norm2(frag[qt].load_q(Qb + static_cast<size_t>(min(self[qt], N - 1)) * D, grp));
   }
   bool self_r[4];  // element r of a diagonal tile is this lane's self pair
 #pragma unroll
@@ -424,7 +444,7 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
     atomicMax(kmax_slot, __float_as_uint(mine));  // non-negative: bit order is value order
     if (q0 < N) {
       const int kend = c0 + cn;
-      for (int kb0 = 0; kb0 < cnb; kb0 += kBlockKeys) {
+      for (int kb0 = 0; kb0 < cnb; kb0 += 16 * BT) {
         const int kabs = c0 + kb0;
         f32x4 s[QT][BT];
 #pragma unroll
@@ -452,7 +472,7 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
           for (int t = 0; t < BT; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) vinsert<L>(pv[qt], s[qt][t][r]);
-        const int next = kb0 + kBlockKeys;
+        const int next = kb0 + 16 * BT;
         if (!ONESEG && ((next & (kSegKeys - 1)) == 0 || next >= cnb))
           flush_segment<QT, L>(pv, rv, ri, c0 + (kb0 & ~(kSegKeys - 1)) + 4 * grp);
       }
@@ -542,20 +562,14 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
       const float e = canon_pair<D, POW2>(qrow, Kb + static_cast<size_t>(row) * D, scale);
       mine[u] = c < 0 ? -INFINITY : e;
     }
-    float qn2 = 0.f;
-    {
-      float qf[D];
-      ld_f32<D>(qf, qrow);
-#pragma unroll
-      for (int c = 0; c < D; ++c) qn2 = fmaf(qf[c], qf[c], qn2);
-    }
     // the exact top k of the candidates, in (score desc, index asc) order
+    float cv[C];
 #pragma unroll
-    for (int m = 0; m < K; ++m) { val[qt][m] = -INFINITY; ix[qt][m] = kIdxSentinel; }
+    for (int m = 0; m < C; ++m) cv[m] = __shfl(mine[m / 4], col + 16 * (m % 4));
+    sort_lex<C>(cv, cand[qt]);
 #pragma unroll
-    for (int m = 0; m < C; ++m)
-      topk_insert_lex<K>(val[qt], ix[qt], __shfl(mine[m / 4], col + 16 * (m % 4)), cand[qt][m]);
-    const float nprod = sqrtf(qn2) * kmax;
+    for (int m = 0; m < K; ++m) { val[qt][m] = cv[m]; ix[qt][m] = cand[qt][m]; }
+    const float nprod = sqrtf(qn2[qt]) * kmax;
     const float bound = (ceil_f[qt] + kFilterEps * nprod) * scale;
     ok[qt] = self[qt] >= N || (nprod < kNormLimit && bound < val[qt][K - 1]);
   }
@@ -608,7 +622,10 @@ static hipError_t launch_filter(const TopkArgs& a, int kc) {
   constexpr int QT = kTopkQueryTiles;
   const int per_wave = 16 * QT;
   const int waves = (a.N + per_wave - 1) / per_wave;
-  const int nw = waves >= kFilterMaxWaves ? kFilterMaxWaves : waves;
+  // up to N = 256 the 28 KiB key copy is small: four-wave groups keep five
+  // groups (20 waves) resident per CU; larger rows share one copy among eight
+  const int maxw = a.N <= 256 ? 4 : kFilterMaxWaves;
+  const int nw = waves >= maxw ? maxw : waves;
   const int qb = per_wave * nw;
   const int n_qblk = (a.N + qb - 1) / qb;
   const int nblocks = a.B * n_qblk;
