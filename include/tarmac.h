@@ -75,6 +75,27 @@ int tarmac_topk_stream_fwd(const void* q, const void* k, const void* v, void* ou
                            int key_chunk, void* stream);
 
 /*
+ * The reference's two other resident selection rules (one wavefront per query
+ * row, the score row in LDS; N + kept <= 16384):
+ *   TARMAC_VARIANT_MASKED: every peer whose score key is >= the threshold
+ *     left by `bisect` halvings of the integer bisection -- exact top-k plus
+ *     every peer tied at the k-th score when bisect >= 32.
+ *     Replaces src/kernels/fused_topk_attention.py:127-208,358-387
+ *     (_fused_topk_masked_kernel, fused_topk_attention_masked). idx_out must
+ *     be NULL (the kept count varies).
+ *   TARMAC_VARIANT_SORT: exactly topk, ties at the k-th score keep the higher
+ *     indices. Replaces src/kernels/fused_topk_attention.py:405-540
+ *     (_fused_topk_sort_kernel, fused_topk_attention_sort). idx_out
+ *     (nullable) in ascending index order.
+ * bisect is ignored for the sort variant.
+ */
+#define TARMAC_VARIANT_MASKED 1
+#define TARMAC_VARIANT_SORT 2
+int tarmac_topk_variant_fwd(const void* q, const void* k, const void* v, void* out,
+                            int32_t* idx_out, int B, int N, int d, int topk, int variant, int bisect,
+                            int dtype, void* stream);
+
+/*
  * Attention over a given peer set idx [B, N, kk] (int32 or int64).
  * Replaces src/kernels/fused_prescore_attention.py:88-114
  * (fused_prescore_attention) and src/kernels/prescore_selection.py:184-195

@@ -34,6 +34,14 @@ morton_code                 bit-by-bit interleave loop; golden vectors written
 select_morton_window        golden vectors from the reference; k distinct
                             peers, never self; curve-neighbour sets
 prescore_attention          dense softmax restricted to the selected set
+ordered_key                 exhaustive order check on special values and
+                            random fp32 pairs (a < b iff key(a) < key(b))
+masked_threshold_keep       bisect >= 32: exactly {j : s_j >= k-th largest}
+                            (closed form, ties included); bisect = 0 keeps
+                            every valid peer; monotone in bisect
+sort_select                 brute force: k largest by (score, index) desc
+weights_attention           equals topk_gather when the kept set is the
+                            top-k set
 canon_topk (C)              numpy oracle: same sets off near-ties, outputs to
                             1e-6; brute force of the fmaf chain in Python
 canon_morton_window (C)     numpy oracle bit-exact (codes and indices)
@@ -143,6 +151,53 @@ def topk_masked(q, k, v, topk):
 #: ``src/kernels/prescore_selection.py:51-52``.
 _SPREAD = ((16, 0x0000FFFF), (8, 0x00FF00FF), (4, 0x0F0F0F0F),
            (2, 0x33333333), (1, 0x55555555))
+
+
+def ordered_key(s: np.ndarray) -> np.ndarray:
+    """Monotone fp32 -> int32 key ``i ^ ((i >> 31) & 0x7FFFFFFF)`` --
+    ``src/kernels/fused_topk_attention.py:113-124``."""
+    i = np.ascontiguousarray(s, np.float32).view(np.int32)
+    return i ^ ((i >> 31) & np.int32(0x7FFFFFFF))
+
+
+def masked_threshold_keep(s: np.ndarray, topk: int, bisect: int = 34) -> np.ndarray:
+    """Kept-peer mask of the threshold-bisection kernel, step for step --
+    ``src/kernels/fused_topk_attention.py:172-186``: int64 keys of the fp32
+    scores ``s`` ([..., N, N], -inf on the self pair); ``lo`` starts at the
+    smallest valid key, ``hi`` at the row maximum; ``bisect`` halvings keep
+    "at least topk keys >= lo"; the kept peers are the keys >= lo."""
+    keys = ordered_key(s).astype(np.int64)
+    n = s.shape[-1]
+    valid = ~np.eye(n, dtype=bool)
+    big = np.int64(np.iinfo(np.int64).max)
+    lo = np.where(valid, keys, big).min(-1)
+    hi = keys.max(-1)
+    for _ in range(bisect):
+        mid = lo + (hi - lo + 1) // 2
+        cnt = (keys >= mid[..., None]).sum(-1)
+        take = cnt >= topk
+        lo = np.where(take, mid, lo)
+        hi = np.where(take, hi, mid - 1)
+    return keys >= lo[..., None]
+
+
+def sort_select(s: np.ndarray, topk: int) -> np.ndarray:
+    """Indices kept by the sort kernel -- ``fused_topk_attention.py:470-480``:
+    a descending sort of ``key << 32 | index``, the first ``topk`` entries
+    (ties at equal score keep the higher index)."""
+    n = s.shape[-1]
+    packed = (ordered_key(s).astype(np.int64) << 32) | np.arange(n, dtype=np.int64)
+    top = np.flip(np.sort(packed, -1), -1)[..., :topk]
+    return top & np.int64(0xFFFFFFFF)
+
+
+def weights_attention(s: np.ndarray, keep: np.ndarray, v: np.ndarray) -> np.ndarray:
+    """Softmax of ``s`` over the kept peers, then ``sum_j w_j v_j`` --
+    ``fused_topk_attention.py:188-208`` (masked) and ``:482-504`` (sort)."""
+    s64 = np.where(keep, s.astype(np.float64), -np.inf)
+    m = s64.max(-1, keepdims=True)
+    w = np.where(keep, np.exp(s64 - m), 0.0)
+    return np.matmul(w, v.astype(np.float64)) / w.sum(-1, keepdims=True)
 
 
 def spread_bits(x: np.ndarray) -> np.ndarray:

@@ -231,3 +231,81 @@ def test_filter_near_ties(N, kk, chunk, filter_always):
         k[:, c0 + 1:c0 + 40] = k[:, c0:c0 + 1] * 3.0 + 1e-6 * rng.standard_normal((B, 39, d))
     out, idx = run_topk(q, k, v, kk, chunk=chunk)
     check_f32(q, k, v, kk, out, idx)
+
+
+# ---------------------------------------------------------------------------
+# the reference's other resident selection rules (masked bisection, sort)
+# ---------------------------------------------------------------------------
+
+def _variant_inputs(seed, B, N, d, ties):
+    q, k, v = qkv(seed, B, N, d)
+    if ties:
+        k[:, 1::2] = k[:, 0:2 * (N // 2):2]  # every score tied in pairs
+        q[:, :N // 4] = 0.0              # and whole rows of +0 scores
+    return q, k, v
+
+
+@pytest.mark.parametrize("N,d,kk,ties", [(6, 16, 2, False), (24, 16, 3, True), (100, 32, 4, False),
+                                         (256, 16, 2, True), (256, 64, 8, False), (513, 16, 5, True)])
+@pytest.mark.parametrize("bisect", [34, 32, 20, 5, 0])
+def test_masked_variant_matches_bisection_oracle(N, d, kk, ties, bisect):
+    """fused_topk_attention_masked: the kept set is the reference's bisection
+    step for step (on the canonical fp32 scores), so outputs match the float64
+    softmax over exactly that set."""
+    from tarmac.kernels import fused_topk_attention_masked
+    B = 3
+    q, k, v = _variant_inputs(N + kk + bisect, B, N, d, ties)
+    qd, kd, vd = dev(q, k, v)
+    out = fused_topk_attention_masked(qd, kd, vd, kk, bisect=bisect)
+    torch.cuda.synchronize()
+    s = O.canon_scores(q, k)
+    keep = O.masked_threshold_keep(s, kk, bisect)
+    ref = O.weights_attention(s, keep, v)
+    assert np.abs(out.cpu().numpy() - ref).max() <= F32_TOL * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("N,d,kk,ties", [(6, 16, 2, True), (24, 8, 5, True), (100, 32, 4, False),
+                                         (256, 16, 2, True), (256, 64, 8, True), (300, 16, 12, True)])
+def test_sort_variant_keeps_higher_index_on_ties(N, d, kk, ties):
+    from tarmac.kernels import fused_topk_attention_sort, topk_variant_attention
+    from tarmac import _lib
+    B = 3
+    q, k, v = _variant_inputs(7 * N + kk, B, N, d, ties)
+    qd, kd, vd = dev(q, k, v)
+    out, idx = topk_variant_attention(qd, kd, vd, kk, _lib.VARIANT_SORT, return_indices=True)
+    out2 = fused_topk_attention_sort(qd, kd, vd, kk)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+    s = O.canon_scores(q, k)
+    want = O.sort_select(s, kk)
+    assert np.array_equal(idx.cpu().numpy(), np.sort(want, -1))
+    keep = np.zeros_like(s, dtype=bool)
+    np.put_along_axis(keep, want, True, -1)
+    ref = O.weights_attention(s, keep, v)
+    assert np.abs(out.cpu().numpy() - ref).max() <= F32_TOL * np.abs(ref).max()
+    if ties:  # the tie rule is visible: rows of +0 scores keep the top indices
+        assert np.all(idx.cpu().numpy()[:, 0] == np.arange(N - kk, N))
+
+
+def test_variants_equal_topk_without_ties():
+    from tarmac.kernels import (fused_topk_attention, fused_topk_attention_masked,
+                                fused_topk_attention_sort)
+    q, k, v = qkv(4321, 4, 128, 16)
+    qd, kd, vd = dev(q, k, v)
+    for kk in (1, 2, 4):
+        a = fused_topk_attention(qd, kd, vd, kk)
+        b = fused_topk_attention_masked(qd, kd, vd, kk)
+        c = fused_topk_attention_sort(qd, kd, vd, kk)
+        assert (a - b).abs().max().item() <= 1e-6 and (a - c).abs().max().item() <= 1e-6
+
+
+def test_variant_argument_errors():
+    from tarmac.kernels import topk_variant_attention
+    from tarmac import _lib
+    q, k, v = dev(*qkv(1, 2, 16, 16))
+    with pytest.raises(ValueError, match="idx_out must be NULL"):
+        topk_variant_attention(q, k, v, 2, _lib.VARIANT_MASKED, return_indices=True)
+    with pytest.raises(ValueError, match="variant"):
+        topk_variant_attention(q, k, v, 2, 7)
+    with pytest.raises(ValueError, match="bisect"):
+        topk_variant_attention(q, k, v, 2, _lib.VARIANT_MASKED, bisect=-1)

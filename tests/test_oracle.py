@@ -127,9 +127,86 @@ def pin_morton(code_fn, golden) -> bool:
     return bool(ok)
 
 
+def _tie_rows(seed, B, N):
+    """fp32 score rows with exact ties: values on a coarse grid, -inf self pair."""
+    rng = np.random.default_rng(seed)
+    s = rng.integers(-3, 4, size=(B, N, N)).astype(np.float32) * np.float32(0.5)
+    s[:, np.arange(N), np.arange(N)] = -np.inf
+    return s
+
+
+def pin_ordered_key(key_fn) -> bool:
+    specials = np.array([-np.inf, -3e38, -1.0, -1e-40, -0.0, 0.0, 1e-40, 1.0, 3e38, np.inf],
+                        np.float32)
+    rng = np.random.default_rng(11)
+    rand = (rng.standard_normal(2000) * np.exp(rng.uniform(-20, 20, 2000))).astype(np.float32)
+    vals = np.concatenate([specials, rand])
+    keys = key_fn(vals).astype(np.int64)
+    a, b = vals[:, None], vals[None, :]
+    ka, kb = keys[:, None], keys[None, :]
+    # strict order agrees wherever the floats are ordered (-0 == +0 is a tie
+    # for floats, ordered by sign for keys)
+    ok = np.all((a < b) <= (ka < kb)) and np.all((a > b) <= (ka > kb))
+    return bool(ok and key_fn(np.float32([-0.0]))[0] < key_fn(np.float32([0.0]))[0])
+
+
+def pin_masked_keep(keep_fn) -> bool:
+    ok = True
+    for seed, (B, N) in enumerate([(3, 7), (2, 12), (2, 33)]):
+        for s in (_tie_rows(seed, B, N), O.scores(*qkv(seed, B, N, 16, np.float32)[:2]).astype(np.float32)):
+            for kk in (1, 2, N // 2, N - 1):
+                # closed form at full precision: every peer at or above the k-th score
+                kth = -np.sort(-s, -1)[..., kk - 1:kk]
+                ok &= np.array_equal(keep_fn(s, kk, 34), s >= kth)
+                ok &= np.array_equal(keep_fn(s, kk, 32), s >= kth)
+                # no halving keeps every valid peer; fewer halvings keep a superset
+                ok &= np.array_equal(keep_fn(s, kk, 0), ~np.eye(N, dtype=bool)[None].repeat(B, 0))
+                for b in (3, 10, 20):
+                    ok &= bool(np.all(keep_fn(s, kk, b) >= (s >= kth)))
+                    ok &= bool(np.all(keep_fn(s, kk, b) >= keep_fn(s, kk, b + 1)))
+    return bool(ok)
+
+
+def pin_sort_select(sel_fn) -> bool:
+    ok = True
+    for seed, (B, N) in enumerate([(2, 6), (3, 9)]):
+        s = _tie_rows(seed, B, N)
+        for kk in (1, 2, 3, N - 1):
+            got = sel_fn(s, kk)
+            for b in range(B):
+                for i in range(N):
+                    # brute force: sort (score, index) pairs, both descending
+                    pairs = sorted(((float(s[b, i, j]), j) for j in range(N)), reverse=True)
+                    ok &= sorted(int(x) for x in got[b, i]) == sorted(j for _, j in pairs[:kk])
+    return bool(ok)
+
+
 # ---------------------------------------------------------------------------
 # the pins, applied to the oracle
 # ---------------------------------------------------------------------------
+
+def test_ordered_key_pinned():
+    assert pin_ordered_key(O.ordered_key)
+
+
+def test_masked_threshold_pinned():
+    assert pin_masked_keep(O.masked_threshold_keep)
+
+
+def test_sort_select_pinned():
+    assert pin_sort_select(O.sort_select)
+
+
+def test_weights_attention_is_topk_gather_on_the_topk_set():
+    q, k, v = qkv(8, 3, 10, 16, F64)
+    s = O.scores(q, k)
+    for kk in (1, 3, 9):
+        idx = O.topk_indices(s, kk)
+        keep = np.zeros_like(s, dtype=bool)
+        np.put_along_axis(keep, idx, True, -1)
+        assert np.allclose(O.weights_attention(s, keep, v), O.topk_gather(q, k, v, kk)[0],
+                           rtol=1e-12, atol=1e-12)
+
 
 def test_scores_pinned():
     assert pin_scores(O.scores)
@@ -363,3 +440,33 @@ def test_pins_reject_planted_mistakes(golden):
 
     assert not pin_morton(morton_swapped_axes, golden)
     assert not pin_morton(morton_rounding, golden)
+
+    # ordered key without the sign fix-up, or with the wrong mask
+    assert not pin_ordered_key(lambda x: np.ascontiguousarray(x, np.float32).view(np.int32))
+    assert not pin_ordered_key(
+        lambda x: (lambda i: i ^ ((i >> 31) & np.int32(0x7FFFFF)))(
+            np.ascontiguousarray(x, np.float32).view(np.int32)))
+
+    def masked_strict(s, topk, bisect=34):         # keys > lo drops the k-th itself
+        keys = O.ordered_key(s).astype(np.int64)
+        return keys > np.where(O.masked_threshold_keep(s, topk, bisect),
+                               keys, np.iinfo(np.int64).max).min(-1, keepdims=True)
+
+    def masked_counts_above(s, topk, bisect=34):  # off by one: needs more than topk
+        keys = O.ordered_key(s).astype(np.int64)
+        n = s.shape[-1]
+        lo = np.where(~np.eye(n, dtype=bool), keys, np.iinfo(np.int64).max).min(-1)
+        hi = keys.max(-1)
+        for _ in range(bisect):
+            mid = lo + (hi - lo + 1) // 2
+            take = (keys >= mid[..., None]).sum(-1) > topk
+            lo, hi = np.where(take, mid, lo), np.where(take, hi, mid - 1)
+        return keys >= lo[..., None]
+
+    assert not pin_masked_keep(masked_strict)
+    assert not pin_masked_keep(masked_counts_above)
+
+    def sort_low_index(s, topk):                   # ties keep the lower index
+        return O.topk_indices(s, topk)
+
+    assert not pin_sort_select(sort_low_index)

@@ -133,6 +133,30 @@ int tarmac_topk_stream_fwd(const void* q, const void* k, const void* v, void* ou
   return topk_common(q, k, v, out, idx_out, B, N, d, topk, dtype, key_chunk, stream, fn);
 }
 
+int tarmac_topk_variant_fwd(const void* q, const void* k, const void* v, void* out,
+                            int32_t* idx_out, int B, int N, int d, int topk, int variant, int bisect,
+                            int dtype, void* stream) {
+  const char* fn = "tarmac_topk_variant_fwd";
+  int rc = check_core(q, k, v, out, B, N, d, dtype, fn);
+  if (rc) return rc;
+  if (variant != TARMAC_VARIANT_MASKED && variant != TARMAC_VARIANT_SORT)
+    return fail(TARMAC_ERR_INVALID, "%s: variant must be %d (masked) or %d (sort) (got %d)", fn,
+                TARMAC_VARIANT_MASKED, TARMAC_VARIANT_SORT, variant);
+  if (topk < 1 || topk > N - 1)
+    return fail(TARMAC_ERR_INVALID, "%s: need 1 <= topk <= N-1 (got topk=%d, N=%d)", fn, topk, N);
+  if (bisect < 0) return fail(TARMAC_ERR_INVALID, "%s: bisect must be >= 0 (got %d)", fn, bisect);
+  if (variant == TARMAC_VARIANT_MASKED && idx_out)
+    return fail(TARMAC_ERR_INVALID, "%s: the masked variant keeps a variable number of peers; "
+                "idx_out must be NULL", fn);
+  if (idx_out && !aligned(idx_out, 4)) return fail(TARMAC_ERR_INVALID, "%s: idx_out misaligned", fn);
+  tarmac::TopkArgs a{q, k, v, out, idx_out, B, N, d, topk, dtype, 0, inv_sqrt(d), stream};
+  a.select = variant == TARMAC_VARIANT_MASKED ? tarmac::kSelMasked : tarmac::kSelSort;
+  a.bisect = bisect;
+  if (static_cast<long>(N + tarmac::wide_cap(a)) * 4 > kLdsBudget)
+    return fail(TARMAC_ERR_UNSUPPORTED, "%s: N=%d too large for one score row in LDS", fn, N);
+  return hip_status(tarmac::run_topk(a), fn);
+}
+
 int tarmac_fixedset_fwd(const void* q, const void* k, const void* v, const void* idx,
                         int idx_dtype, int kk, void* out, int B, int N, int d, int dtype,
                         void* stream) {

@@ -28,7 +28,13 @@ struct TopkArgs {
   int key_chunk;    // keys per LDS chunk (multiple of 16)
   float scale;      // fp32(1/sqrt(d))
   void* stream;
+  int select = 0;   // kSelTopk / kSelMasked / kSelSort
+  int bisect = 0;   // kSelMasked: bisection halvings
 };
+
+// Selection rules (TARMAC_VARIANT_* in include/tarmac.h).
+constexpr int kSelTopk = 0, kSelMasked = 1, kSelSort = 2;
+int wide_cap(const TopkArgs& a);
 
 struct DenseArgs {
   const void* q;

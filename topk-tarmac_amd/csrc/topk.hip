@@ -183,18 +183,41 @@ __device__ __forceinline__ float canon_score(const float (&q)[D], const T* krow)
   return acc;
 }
 
-// mode 0: ties at the threshold keep the lowest indices (exact top-k).
+__device__ __forceinline__ int wave_min_int(int x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = min(x, __shfl_xor(x, o));
+  return x;
+}
+
+__device__ __forceinline__ int wave_max_int(int x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = max(x, __shfl_xor(x, o));
+  return x;
+}
+
+// Selection rules of the wide kernel:
+//   kSelTopk   exactly k, ties at the k-th score keep the lowest indices
+//              (the standard rule, src/kernels/streaming_topk_attention.py:37-44);
+//   kSelMasked every peer whose key is >= the threshold left by `bisect`
+//              halvings of the reference's integer bisection
+//              (src/kernels/fused_topk_attention.py:127-208): exact top-k plus
+//              every peer tied at the k-th score once bisect >= 32;
+//   kSelSort   exactly k, ties at the k-th score keep the highest indices (the
+//              descending sort of key << 32 | index, :405-504).
+// One wave per query row; the score row and the selected indices live in LDS
+// (the selected list holds up to `cap` entries: k, or N for kSelMasked).
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
 topk_wide_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
-                 T* __restrict__ O, int32_t* __restrict__ Idx, int B, int N, int topk, float scale) {
+                 T* __restrict__ O, int32_t* __restrict__ Idx, int B, int N, int topk, float scale,
+                 int mode, int bisect, int cap) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const long row_raw = static_cast<long>(blockIdx.x) * nw + wave;  // (b, i) flattened
   const bool live = row_raw < static_cast<long>(B) * N;  // wave-uniform
   const long row = live ? row_raw : 0;
   const int b = static_cast<int>(row / N), i = static_cast<int>(row - static_cast<long>(b) * N);
-  float* S = reinterpret_cast<float*>(smem_raw) + static_cast<size_t>(wave) * (N + topk);
+  float* S = reinterpret_cast<float*>(smem_raw) + static_cast<size_t>(wave) * (N + cap);
   int* sel = reinterpret_cast<int*>(S + N);
   const size_t boff = static_cast<size_t>(b) * N * D;
   const bool pow2 = is_pow2_scale(scale);
@@ -212,20 +235,49 @@ topk_wide_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __r
   }
   __syncthreads();
 
-  // Largest t with count(key >= t) >= topk.
-  long lo = -2147483648L, hi = 2147483647L;
-  while (lo < hi) {
-    const long mid = lo + (hi - lo + 1) / 2;
-    int cnt = 0;
-    for (int j = lane; j < N; j += kWave) cnt += (ordered_key(S[j]) >= mid) ? 1 : 0;
-    cnt = wave_sum(cnt);
-    if (cnt >= topk) lo = mid; else hi = mid - 1;
+  int thr;
+  if (mode == kSelMasked) {
+    // the reference's bisection, step for step: lo starts at the smallest
+    // valid key, hi at the row maximum; bisect halvings
+    int kmin = 2147483647, kmx = -2147483647 - 1;
+    for (int j = lane; j < N; j += kWave) {
+      const int key = ordered_key(S[j]);
+      kmx = max(kmx, key);
+      if (j != i) kmin = min(kmin, key);
+    }
+    long lo = wave_min_int(kmin), hi = wave_max_int(kmx);
+    for (int it = 0; it < bisect; ++it) {
+      const long mid = lo + (hi - lo + 1) / 2;
+      int cnt = 0;
+      for (int j = lane; j < N; j += kWave) cnt += (ordered_key(S[j]) >= mid) ? 1 : 0;
+      cnt = wave_sum(cnt);
+      if (cnt >= topk) lo = mid; else hi = mid - 1;
+    }
+    thr = static_cast<int>(lo);
+  } else {
+    // largest t with count(key >= t) >= topk: the k-th largest key
+    long lo = -2147483648L, hi = 2147483647L;
+    while (lo < hi) {
+      const long mid = lo + (hi - lo + 1) / 2;
+      int cnt = 0;
+      for (int j = lane; j < N; j += kWave) cnt += (ordered_key(S[j]) >= mid) ? 1 : 0;
+      cnt = wave_sum(cnt);
+      if (cnt >= topk) lo = mid; else hi = mid - 1;
+    }
+    thr = static_cast<int>(lo);
   }
-  const int thr = static_cast<int>(lo);
-  int gt = 0;
-  for (int j = lane; j < N; j += kWave) gt += (ordered_key(S[j]) > thr) ? 1 : 0;
+  int gt = 0, eq = 0;
+  for (int j = lane; j < N; j += kWave) {
+    const int key = ordered_key(S[j]);
+    gt += key > thr ? 1 : 0;
+    eq += key == thr ? 1 : 0;
+  }
   gt = wave_sum(gt);
-  const int need_ties = topk - gt;
+  eq = wave_sum(eq);
+  // ties at thr taken: all (masked), the first need_ties in index order
+  // (topk) or the last need_ties (sort)
+  const int need_ties = mode == kSelMasked ? eq : topk - gt;
+  const int skip_ties = mode == kSelSort ? eq - need_ties : 0;
 
   // Compact the selected indices in ascending index order.
   int taken = 0, ties = 0;
@@ -236,7 +288,8 @@ topk_wide_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __r
     const bool is_tie = (j < N) && key == thr;
     const unsigned long long tie_mask = __ballot(is_tie);
     const int tie_rank = ties + __popcll(tie_mask & ((1ull << lane) - 1ull));
-    const bool pick = (j < N) && (key > thr || (is_tie && tie_rank < need_ties));
+    const bool pick = (j < N) && (key > thr || (is_tie && tie_rank >= skip_ties &&
+                                                 tie_rank < skip_ties + need_ties));
     const unsigned long long pick_mask = __ballot(pick);
     if (pick) {
       sel[taken + __popcll(pick_mask & ((1ull << lane) - 1ull))] = j;
@@ -252,7 +305,7 @@ topk_wide_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __r
   // Lane c < D accumulates channel c over the selected rows.
   if (lane < D) {
     float acc = 0.f, den = 0.f;
-    for (int m = 0; m < topk; ++m) {
+    for (int m = 0; m < taken; ++m) {
       const int j = sel[m];
       const float w = expf(S[j] - mx);
       den += w;
@@ -267,7 +320,7 @@ topk_wide_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __r
     if constexpr (sizeof(T) == 4) *reinterpret_cast<float*>(dst) = o;
     else *reinterpret_cast<bf16*>(dst) = f32_to_bf16(o);
   }
-  if (Idx != nullptr) {
+  if (Idx != nullptr) {  // never for kSelMasked (the set size varies)
     int32_t* dst = Idx + (static_cast<size_t>(b) * N + i) * topk;
     for (int m = lane; m < topk; m += kWave) dst[m] = sel[m];
   }
@@ -313,24 +366,27 @@ static hipError_t launch_small(const TopkArgs& a, int kc) {
   return hipGetLastError();
 }
 
+int wide_cap(const TopkArgs& a) { return a.select == kSelMasked ? a.N : a.topk; }
+
 template <typename T, int D>
 static hipError_t launch_wide(const TopkArgs& a) {
-  // nw waves per workgroup, each holding N + topk words of LDS (<= 64 KiB total)
-  int nw = 16384 / (a.N + a.topk);
+  // nw waves per workgroup, each holding N + cap words of LDS (<= 64 KiB total)
+  const int cap = wide_cap(a);
+  int nw = 16384 / (a.N + cap);
   nw = nw < 1 ? 1 : (nw > 4 ? 4 : nw);
   const long rows = static_cast<long>(a.B) * a.N;
   const int grid = static_cast<int>((rows + nw - 1) / nw);
-  const size_t lds = static_cast<size_t>(nw) * (a.N + a.topk) * sizeof(float);
+  const size_t lds = static_cast<size_t>(nw) * (a.N + cap) * sizeof(float);
   hipLaunchKernelGGL((topk_wide_kernel<T, D>), dim3(grid), dim3(64 * nw), lds,
                      static_cast<hipStream_t>(a.stream), static_cast<const T*>(a.q),
                      static_cast<const T*>(a.k), static_cast<const T*>(a.v), static_cast<T*>(a.out),
-                     a.idx, a.B, a.N, a.topk, a.scale);
+                     a.idx, a.B, a.N, a.topk, a.scale, a.select, a.bisect, cap);
   return hipGetLastError();
 }
 
 template <typename T, int D>
 static hipError_t dispatch_topk(const TopkArgs& a) {
-  if (a.topk > kTopkSmallMax) return launch_wide<T, D>(a);
+  if (a.topk > kTopkSmallMax || a.select != kSelTopk) return launch_wide<T, D>(a);
   return launch_small<T, D>(a, a.key_chunk);
 }
 
@@ -343,7 +399,8 @@ int g_topk_filter_mode = kFilterAuto;
 static bool filter_pays(const TopkArgs& a) { return a.N >= 512 || (a.N >= 256 && a.topk >= 3); }
 
 hipError_t run_topk(const TopkArgs& a) {
-  if (g_topk_filter_mode != kFilterOff && topk_filter_supported(a.dtype, a.d, a.topk) &&
+  if (a.select == kSelTopk && g_topk_filter_mode != kFilterOff &&
+      topk_filter_supported(a.dtype, a.d, a.topk) &&
       (g_topk_filter_mode == kFilterAlways || filter_pays(a)))
     return run_topk_filter(a);
   if (a.dtype == kF32) {

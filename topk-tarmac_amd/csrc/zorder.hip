@@ -8,8 +8,9 @@
 //   src/agents/mappo.py:265-292                     zorder_k (selector + attend)
 //
 // Fixed-set attention: a quad of lanes owns one query; lane (l % 4) holds d/4
-// channels. For each retained peer the quad forms the dot with two xor
-// shuffles, runs an online softmax, and accumulates its V slice.
+// channels. Peers are taken in batches whose index, K and V loads are all in
+// flight together; the quad forms each dot with two xor shuffles and folds the
+// batch into an online softmax (one rescale per batch) and its V slice.
 //
 // Morton window, one workgroup per batch row:
 //   1. per-axis min/max over the agents (workgroup reduction);
@@ -28,6 +29,9 @@
 
 namespace tarmac {
 
+// One workgroup per batch row for the selector.
+constexpr int kZorderThreads = 256;
+
 // ---------------------------------------------------------------------------
 // fixed-set attention for one query (a quad of lanes)
 // ---------------------------------------------------------------------------
@@ -39,6 +43,8 @@ __device__ __forceinline__ void quad_fixedset_row(const T* __restrict__ qrow,
                                                   int N, int kk, float scale, int sub,
                                                   IdxFn peer) {
   constexpr int E = D / 4;
+  // peers per batch: all their index, K and V loads are in flight together
+  constexpr int U = E <= 4 ? 4 : (E <= 8 ? 2 : 1);
   float q[E];
   ld_row<T, E>(q, qrow + sub * E);
   float acc[E];
@@ -46,30 +52,56 @@ __device__ __forceinline__ void quad_fixedset_row(const T* __restrict__ qrow,
   for (int c = 0; c < E; ++c) acc[c] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
   bool bad = false;
-  for (int j = 0; j < kk; ++j) {
-    int p = peer(j);
-    bad |= (p < 0) | (p >= N);
-    p = min(max(p, 0), N - 1);
-    float kr[E], vr[E];
-    ld_row<T, E>(kr, Kb + static_cast<size_t>(p) * D + sub * E);
-    ld_row<T, E>(vr, Vb + static_cast<size_t>(p) * D + sub * E);
-    float s = 0.f;
+  for (int j0 = 0; j0 < kk; j0 += U) {
+    int p[U];
 #pragma unroll
-    for (int c = 0; c < E; ++c) s = fmaf(q[c], kr[c], s);
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s *= scale;
-    const float m_new = fmaxf(m_run, s);
-    const float alpha = (m_run == -INFINITY) ? 0.f : expf(m_run - m_new);
-    const float w = expf(s - m_new);
-    l_run = l_run * alpha + w;
+    for (int u = 0; u < U; ++u) {
+      const bool live = j0 + u < kk;
+      p[u] = live ? peer(j0 + u) : 0;
+      bad |= live && ((p[u] < 0) | (p[u] >= N));
+      p[u] = min(max(p[u], 0), N - 1);
+    }
+    float kr[U][E], vr[U][E];
 #pragma unroll
-    for (int c = 0; c < E; ++c) acc[c] = fmaf(w, vr[c], acc[c] * alpha);
-    m_run = m_new;
+    for (int u = 0; u < U; ++u) {
+      if (j0 + u < kk) {
+        ld_row<T, E>(kr[u], Kb + static_cast<size_t>(p[u]) * D + sub * E);
+        ld_row<T, E>(vr[u], Vb + static_cast<size_t>(p[u]) * D + sub * E);
+      } else {
+#pragma unroll
+        for (int c = 0; c < E; ++c) kr[u][c] = vr[u][c] = 0.f;
+      }
+    }
+    // scores of the batch (log2 domain), then one rescale of the running sums
+    float s[U];
+    float m_b = m_run;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float t = 0.f;
+#pragma unroll
+      for (int c = 0; c < E; ++c) t = fmaf(q[c], kr[u][c], t);
+      t += __shfl_xor(t, 1);
+      t += __shfl_xor(t, 2);
+      s[u] = j0 + u < kk ? t * scale * kLog2eF : -INFINITY;
+      m_b = fmaxf(m_b, s[u]);
+    }
+    const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_b);
+    l_run *= alpha;
+#pragma unroll
+    for (int c = 0; c < E; ++c) acc[c] *= alpha;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float w = s[u] == -INFINITY ? 0.f : fast_exp2(s[u] - m_b);
+      l_run += w;
+#pragma unroll
+      for (int c = 0; c < E; ++c) acc[c] = fmaf(w, vr[u][c], acc[c]);
+    }
+    m_run = m_b;
   }
+  const float inv = 1.f / l_run;
   float o[E];
 #pragma unroll
-  for (int c = 0; c < E; ++c) o[c] = bad ? __int_as_float(0x7fc00000) : acc[c] / l_run;
+  for (int c = 0; c < E; ++c) o[c] = bad ? __int_as_float(0x7fc00000) : acc[c] * inv;
   if constexpr (E % 4 == 0) {
     st_row<T, E>(orow + sub * E, o);
   } else {
@@ -207,7 +239,7 @@ __device__ __forceinline__ ZorderSmem zorder_smem(unsigned char* raw, int N, int
 }
 
 template <typename I>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kZorderThreads)
 morton_window_kernel(const float* __restrict__ pos, I* __restrict__ idx, int64_t* __restrict__ codes,
                      int N, int P, int k, int bits) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -229,7 +261,7 @@ morton_window_kernel(const float* __restrict__ pos, I* __restrict__ idx, int64_t
 }
 
 template <typename T, int D>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kZorderThreads)
 zorder_attn_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
                    const float* __restrict__ pos, T* __restrict__ O, int32_t* __restrict__ idx_out,
                    int N, int P, int k, int bits, float scale) {
@@ -257,7 +289,7 @@ zorder_attn_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
 
 size_t zorder_lds_bytes(int N) {
   const int P = next_pow2(N);
-  return static_cast<size_t>(P) * 8 + static_cast<size_t>(N) * 8 + 4 * 4 * 4;
+  return static_cast<size_t>(P) * 8 + static_cast<size_t>(N) * 8 + 4 * 4 * (kZorderThreads / 64);
 }
 
 template <typename T, int D>
@@ -302,10 +334,10 @@ hipError_t run_morton_window(const MortonArgs& a) {
   const size_t lds = zorder_lds_bytes(a.N);
   hipStream_t st = static_cast<hipStream_t>(a.stream);
   if (a.idx_is_i64) {
-    hipLaunchKernelGGL((morton_window_kernel<int64_t>), dim3(a.B), dim3(256), lds, st, a.pos,
+    hipLaunchKernelGGL((morton_window_kernel<int64_t>), dim3(a.B), dim3(kZorderThreads), lds, st, a.pos,
                        static_cast<int64_t*>(a.idx), a.codes, a.N, P, a.k, a.bits);
   } else {
-    hipLaunchKernelGGL((morton_window_kernel<int32_t>), dim3(a.B), dim3(256), lds, st, a.pos,
+    hipLaunchKernelGGL((morton_window_kernel<int32_t>), dim3(a.B), dim3(kZorderThreads), lds, st, a.pos,
                        static_cast<int32_t*>(a.idx), a.codes, a.N, P, a.k, a.bits);
   }
   return hipGetLastError();
@@ -315,7 +347,7 @@ template <typename T, int D>
 static hipError_t launch_zorder(const ZorderArgs& a) {
   const int P = next_pow2(a.N);
   const size_t lds = zorder_lds_bytes(a.N);
-  hipLaunchKernelGGL((zorder_attn_kernel<T, D>), dim3(a.B), dim3(256), lds,
+  hipLaunchKernelGGL((zorder_attn_kernel<T, D>), dim3(a.B), dim3(kZorderThreads), lds,
                      static_cast<hipStream_t>(a.stream), static_cast<const T*>(a.q),
                      static_cast<const T*>(a.k), static_cast<const T*>(a.v), a.pos,
                      static_cast<T*>(a.out), a.idx, a.N, P, a.topk, a.bits, a.scale);

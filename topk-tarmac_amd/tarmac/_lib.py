@@ -23,6 +23,9 @@ DTYPE_BF16 = 1
 IDX_I32 = 0
 IDX_I64 = 1
 
+VARIANT_MASKED = 1
+VARIANT_SORT = 2
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 
@@ -33,6 +36,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tarmac_dense_fwd": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
     "tarmac_topk_fused_fwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
     "tarmac_topk_stream_fwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "tarmac_topk_variant_fwd": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tarmac_fixedset_fwd": ([_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P], _I),
     "tarmac_morton_window": ([_P, _P, _I, _P, _I, _I, _I, _I, _P], _I),
     "tarmac_zorder_fwd": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),

@@ -4,7 +4,8 @@ from .fused_dense_attention import fused_dense_attention
 from .fused_prescore_attention import fused_prescore_attention
 from .fused_topk_attention import (fused_topk_attention, fused_topk_attention_masked,
                                    fused_topk_attention_sort, fused_topk_attention_tiled,
-                                   reference_topk_attention, topk_attention)
+                                   reference_topk_attention, topk_attention,
+                                   topk_variant_attention)
 from .prescore_selection import (_morton_code, prescore_attention, select_morton_window,
                                  zorder_attention)
 from .streaming_topk_attention import streaming_topk_attention
@@ -12,6 +13,7 @@ from .streaming_topk_attention import streaming_topk_attention
 __all__ = [
     "fused_dense_attention", "fused_prescore_attention", "fused_topk_attention",
     "fused_topk_attention_masked", "fused_topk_attention_sort", "fused_topk_attention_tiled",
-    "reference_topk_attention", "topk_attention", "prescore_attention", "select_morton_window",
+    "reference_topk_attention", "topk_attention", "topk_variant_attention",
+    "prescore_attention", "select_morton_window",
     "zorder_attention", "streaming_topk_attention", "_morton_code",
 ]

@@ -8,11 +8,12 @@ score row, index tensor or gathered tensor written to HBM.
 * ``fused_topk_attention`` / ``fused_topk_attention_tiled``
   (``fused_topk_attention.py:296-355``): both are this kernel; the reference's
   two differ only in Triton tiling.
-* ``fused_topk_attention_masked`` (``:358-387``): the threshold-bisection
-  kernel. Its retained set is "every peer at or above the k-th score", which
+* ``fused_topk_attention_masked`` (``:127-208,358-387``): the
+  threshold-bisection kernel, emulated step for step on the integer score
+  keys. Its retained set is "every peer at or above the threshold", which
   equals exact top-k except on an exact tie at the k-th score, where it keeps
-  k+1 peers.
-* ``fused_topk_attention_sort`` (``:507-540``): sort-based selection whose
+  every tied peer (or a superset when ``bisect`` < 32).
+* ``fused_topk_attention_sort`` (``:405-540``): sort-based selection whose
   tie rule keeps the higher index.
 * ``reference_topk_attention`` (``:390-402``): the composed PyTorch gather
   path, kept as the baseline it is in the reference.
@@ -82,37 +83,46 @@ def fused_topk_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return topk_attention(q, k, v, topk)
 
 
+def topk_variant_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, topk: int,
+                           variant: int, bisect: int = 34,
+                           return_indices: bool = False):
+    """The reference's other two resident selection rules (one HIP launch):
+    ``_lib.VARIANT_MASKED`` (threshold bisection) or ``_lib.VARIANT_SORT``
+    (ties keep the higher index). ``topk`` is clamped to [1, N-1]."""
+    q, k, v = _launch.core(q, k, v)
+    B, N, d = q.shape
+    kk = max(1, min(int(topk), N - 1))
+    out = torch.empty_like(q)
+    idx = torch.empty(B, N, kk, device=q.device, dtype=torch.int32) if return_indices else None
+    with torch.cuda.device(q.device):
+        rc = _lib.LIB.tarmac_topk_variant_fwd(
+            _launch.ptr(q), _launch.ptr(k), _launch.ptr(v), _launch.ptr(out), _launch.ptr(idx),
+            B, N, d, kk, int(variant), int(bisect), _launch.dtype_code(q), _launch.stream(q))
+        _lib.check(rc)
+    return (out, idx) if return_indices else out
+
+
 def fused_topk_attention_masked(q: torch.Tensor, k: torch.Tensor,
                                 v: torch.Tensor, topk: int,
                                 bisect: int = 34) -> torch.Tensor:
-    """Threshold top-k: every peer whose score is >= the k-th largest.
-
-    Identical to exact top-k unless the k-th score is tied, where the
-    threshold keeps every tied peer (k+1 or more), as the reference's
-    bisection kernel does. ``bisect`` is accepted for signature compatibility.
-    """
+    """Threshold top-k: every peer whose score key is at or above the
+    threshold left by ``bisect`` halvings of the integer bisection -- exact
+    top-k plus every peer tied at the k-th score once ``bisect`` >= 32, a
+    superset for fewer halvings, as the reference's kernel computes it."""
     B, N, d = q.shape
     assert N <= 1024
-    kk = max(1, min(int(topk), N - 1))
-    out, idx = topk_attention(q, k, v, kk, return_indices=True)
-    return _widen_on_ties(q, k, v, out, idx, kk, keep="all")
+    return topk_variant_attention(q, k, v, topk, _lib.VARIANT_MASKED, bisect)
 
 
 def fused_topk_attention_sort(q: torch.Tensor, k: torch.Tensor,
                               v: torch.Tensor, topk: int,
                               block_m: int | None = None) -> torch.Tensor:
     """Sort-based selection; an exact tie at the k-th score keeps the higher
-    index, as the reference's descending sort of (key << 32 | index) does."""
+    index, as the reference's descending sort of (key << 32 | index) does.
+    ``block_m`` is a Triton tiling knob, accepted for signature compatibility."""
     B, N, d = q.shape
     assert N <= 1024
-    kk = max(1, min(int(topk), N - 1))
-    out, idx = topk_attention(q, k, v, kk, return_indices=True)
-    return _widen_on_ties(q, k, v, out, idx, kk, keep="high")
-
-
-def _widen_on_ties(q, k, v, out, idx, kk, keep):
-    raise NotImplementedError(
-        "tie-rule variants (masked / sort) are not built as HIP kernels yet")
+    return topk_variant_attention(q, k, v, topk, _lib.VARIANT_SORT)
 
 
 def reference_topk_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
