@@ -322,6 +322,58 @@ def main() -> int:
         harness.analytic_bytes("dense", B, N, D, itemsize=2) / (td * 1e-6)
         / harness.PEAK_HBM_BYTES_PER_S, 4)
 
+    # ---- the whole AttentionComm forward (qkv Linear, core, gelu, proj) ---
+    # the reference's module microbenchmark cell (scripts/microbenchmark_comm.py:
+    # batch 256, in_dim 64, msg_dim 16, k = max(1, floor(0.25 (N-1)))); the
+    # torch arm composes the reference's topk_gather core from torch ops on
+    # the same GPU and weights
+    import torch.nn.functional as F
+    from tarmac.agents.mappo import AttentionComm, MAPPOConfig
+    from tarmac.kernels import reference_topk_attention
+    mod_rows = {}
+    for n in (6, 96, 384):
+        kk = max(1, int(0.25 * (n - 1)))
+        gx = np.random.default_rng(900 + n)
+        x = torch.from_numpy(gx.standard_normal((256, n, 64)).astype(np.float32)).to(dev)
+        fm = {}
+        for mode in ("dense", "topk_gather"):
+            cfg = MAPPOConfig(obs_dim=18, n_actions=5, n_agents=n, hidden=64, use_comm=True,
+                              msg_dim=16, attn_mode=mode, topk=kk)
+            m = AttentionComm(cfg, in_dim=64).to(dev).eval()
+            m.collect_info = False
+            fm[f"hip_{mode}"] = (lambda m=m, x=x: m(x)[0])
+            if mode == "topk_gather":
+                def torch_arm(m=m, x=x, kk=kk):
+                    qkv_ = m.qkv(x)
+                    q_, k_, v_ = (t.contiguous() for t in qkv_.chunk(3, dim=-1))
+                    return m.proj(F.gelu(reference_topk_attention(q_, k_, v_, kk)))
+                fm["torch_topk_gather"] = torch_arm
+        se = {nm: harness.stats(sm)["min_us"] for nm, sm in
+              harness.time_interleaved(fm, args.reps, 5, 2).items()}
+        sg = {nm: harness.stats(sm)["min_us"] for nm, sm in
+              harness.time_interleaved(harness.as_graphs(fm), args.reps, 5, 2).items()}
+        mod_rows[f"N{n}_k{kk}"] = {"eager_us": {k_: round(v_, 3) for k_, v_ in se.items()},
+                                   "graph_us": {k_: round(v_, 3) for k_, v_ in sg.items()}}
+    detail["module_forward_B256_in64_msg16"] = mod_rows
+
+    # ---- small-N, launch-bound regime (B=1024, d=16, k=2): eager vs graph --
+    small = {}
+    for n in (12, 24, 48, 96):
+        gs = np.random.default_rng(1234 + 7 * n + D)
+        qs, ks, vs = (torch.from_numpy(gs.standard_normal((B, n, D)).astype(np.float32)).to(dev)
+                      for _ in range(3))
+        fs = {"dense": bound.dense(qs, ks, vs), "topk_k2": bound.topk(qs, ks, vs, 2)}
+        fg = {"dense": lambda: fused_dense_attention(qs, ks, vs),
+              "topk_k2": lambda: topk_attention(qs, ks, vs, 2)}
+        se = {nm: harness.stats(sm)["min_us"] for nm, sm in
+              harness.time_interleaved(fs, args.reps, 5, 2).items()}
+        sg = {nm: harness.stats(sm)["min_us"] for nm, sm in
+              harness.time_interleaved(harness.as_graphs(fg), args.reps, 5, 2).items()}
+        small[f"N{n}"] = {"eager_us": {k_: round(v_, 3) for k_, v_ in se.items()},
+                          "graph_us": {k_: round(v_, 3) for k_, v_ in sg.items()},
+                          "launches_per_call": 1}
+    detail["small_n_B1024_d16"] = small
+
     line["detail"] = detail
     line["device"] = torch.cuda.get_device_name(dev)
     line["host"] = {"cpu": platform.processor() or platform.machine(),

@@ -209,15 +209,18 @@ __device__ __forceinline__ int wave_max_int(int x) {
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
 topk_wide_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
-                 T* __restrict__ O, int32_t* __restrict__ Idx, int B, int N, int topk, float scale,
-                 int mode, int bisect, int cap) {
+                 T* __restrict__ O, int32_t* __restrict__ Idx, int N, int n_qblk, int topk,
+                 float scale, int mode, int bisect, int cap, int k_in_lds) {
+  constexpr int KST = D + 16 / static_cast<int>(sizeof(T));  // padded LDS key row
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  const long row_raw = static_cast<long>(blockIdx.x) * nw + wave;  // (b, i) flattened
-  const bool live = row_raw < static_cast<long>(B) * N;  // wave-uniform
-  const long row = live ? row_raw : 0;
-  const int b = static_cast<int>(row / N), i = static_cast<int>(row - static_cast<long>(b) * N);
-  float* S = reinterpret_cast<float*>(smem_raw) + static_cast<size_t>(wave) * (N + cap);
+  const int b = blockIdx.x / n_qblk, qb = blockIdx.x - b * n_qblk;
+  const int i_raw = qb * nw + wave;
+  const bool live = i_raw < N;  // wave-uniform
+  const int i = live ? i_raw : N - 1;
+  T* Ks = reinterpret_cast<T*>(smem_raw);
+  const size_t kbytes = k_in_lds ? static_cast<size_t>(N) * KST * sizeof(T) : 0;
+  float* S = reinterpret_cast<float*>(smem_raw + kbytes) + static_cast<size_t>(wave) * (N + cap);
   int* sel = reinterpret_cast<int*>(S + N);
   const size_t boff = static_cast<size_t>(b) * N * D;
   const bool pow2 = is_pow2_scale(scale);
@@ -228,8 +231,14 @@ topk_wide_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __r
 #pragma unroll
     for (int c = 0; c < D; ++c) q[c] *= scale;
   }
+  if (k_in_lds) {  // uniform: the workgroup's queries share one copy of the batch row's keys
+    stage_rows<T, D, KST>(Ks, Kx + boff, N, N);
+    __syncthreads();
+  }
   for (int j = lane; j < N; j += kWave) {
-    float s = canon_score<T, D>(q, Kx + boff + static_cast<size_t>(j) * D);
+    // separate calls keep LDS reads as ds_read (a merged pointer would be generic)
+    float s = k_in_lds ? canon_score<T, D>(q, Ks + j * KST)
+                       : canon_score<T, D>(q, Kx + boff + static_cast<size_t>(j) * D);
     if (!pow2) s *= scale;
     S[j] = (j == i) ? -INFINITY : s;
   }
@@ -255,7 +264,8 @@ topk_wide_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __r
     }
     thr = static_cast<int>(lo);
   } else {
-    // largest t with count(key >= t) >= topk: the k-th largest key
+    // largest t with count(key >= t) >= topk: the k-th largest key (or any t
+    // with exactly topk keys at or above it, which selects the same set)
     long lo = -2147483648L, hi = 2147483647L;
     while (lo < hi) {
       const long mid = lo + (hi - lo + 1) / 2;
@@ -263,6 +273,7 @@ topk_wide_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __r
       for (int j = lane; j < N; j += kWave) cnt += (ordered_key(S[j]) >= mid) ? 1 : 0;
       cnt = wave_sum(cnt);
       if (cnt >= topk) lo = mid; else hi = mid - 1;
+      if (cnt == topk) break;
     }
     thr = static_cast<int>(lo);
   }
@@ -302,27 +313,231 @@ topk_wide_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __r
   __syncthreads();
   if (!live) return;
 
-  // Lane c < D accumulates channel c over the selected rows.
-  if (lane < D) {
-    float acc = 0.f, den = 0.f;
-    for (int m = 0; m < taken; ++m) {
-      const int j = sel[m];
-      const float w = expf(S[j] - mx);
-      den += w;
-      const T* vr = V + boff + static_cast<size_t>(j) * D + lane;
-      float x;
-      if constexpr (sizeof(T) == 4) x = *reinterpret_cast<const float*>(vr);
-      else x = bf16_to_f32(*reinterpret_cast<const bf16*>(vr));
-      acc = fmaf(w, x, acc);
+  // Aggregation over the selected rows, all lanes at once: lane = 4 * slot + g
+  // takes rows m = slot, slot + 16, ... and channels g*E .. g*E+E-1; the 16
+  // slots are then summed with xor shuffles.
+  constexpr int E = D / 4;
+  const int slot = lane >> 2, g = lane & 3;
+  float acc[E];
+#pragma unroll
+  for (int c = 0; c < E; ++c) acc[c] = 0.f;
+  float den = 0.f;
+  for (int m = slot; m < taken; m += 16) {
+    const int j = sel[m];
+    const float w = expf(S[j] - mx);
+    den += w;
+    float vr[E];
+    ld_row<T, E>(vr, V + boff + static_cast<size_t>(j) * D + g * E);
+#pragma unroll
+    for (int c = 0; c < E; ++c) acc[c] = fmaf(w, vr[c], acc[c]);
+  }
+#pragma unroll
+  for (int o = 4; o < kWave; o <<= 1) {
+    den += __shfl_xor(den, o);
+#pragma unroll
+    for (int c = 0; c < E; ++c) acc[c] += __shfl_xor(acc[c], o);
+  }
+  if (slot == 0) {
+    const float inv = 1.f / den;
+    T* dst = O + boff + static_cast<size_t>(i) * D + g * E;
+#pragma unroll
+    for (int c = 0; c < E; ++c) {
+      const float o = acc[c] * inv;
+      if constexpr (sizeof(T) == 4) dst[c] = o;
+      else dst[c] = f32_to_bf16(o);
     }
-    const float o = acc / den;
-    T* dst = O + boff + static_cast<size_t>(i) * D + lane;
-    if constexpr (sizeof(T) == 4) *reinterpret_cast<float*>(dst) = o;
-    else *reinterpret_cast<bf16*>(dst) = f32_to_bf16(o);
   }
   if (Idx != nullptr) {  // never for kSelMasked (the set size varies)
     int32_t* dst = Idx + (static_cast<size_t>(b) * N + i) * topk;
     for (int m = lane; m < topk; m += kWave) dst[m] = sel[m];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// large k, N <= 16 * NS: sixteen lanes per query, keys in registers
+// ---------------------------------------------------------------------------
+
+// Same function as topk_wide_kernel (all three selection rules), four
+// queries per wavefront and sixteen per workgroup. Lane (16 q + s) holds the
+// integer keys of its query's peers j = s + 16 t, t < NS, so every count of
+// the bisection is NS compares and a four-step xor reduction over the
+// query's sixteen lanes. The selected (index, score) pairs are compacted into
+// LDS in ascending index order; four slots x four channel groups then gather
+// the value rows.
+template <typename T, int D, int NS>
+__global__ void __launch_bounds__(256)
+topk_wide16_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
+                   T* __restrict__ O, int32_t* __restrict__ Idx, int N, int n_qblk, int topk,
+                   float scale, int mode, int bisect, int cap, int k_in_lds) {
+  constexpr int KST = D + 16 / static_cast<int>(sizeof(T));  // padded LDS key row
+  constexpr int kNone = -2147483647 - 1;                       // no peer in this slot
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int qs = lane >> 4, sub = lane & 15;
+  const int b = blockIdx.x / n_qblk, qb = blockIdx.x - b * n_qblk;
+  const int qslot = 4 * wave + qs;                 // query slot in the workgroup
+  const int i_raw = 16 * qb + qslot;
+  const bool live = i_raw < N;                     // uniform over the 16 lanes
+  const int i = live ? i_raw : N - 1;
+  T* Ks = reinterpret_cast<T*>(smem_raw);
+  const size_t kbytes = k_in_lds ? static_cast<size_t>(N) * KST * sizeof(T) : 0;
+  int* sel = reinterpret_cast<int*>(smem_raw + kbytes) + static_cast<size_t>(qslot) * 2 * cap;
+  float* sel_s = reinterpret_cast<float*>(sel + cap);
+  const size_t boff = static_cast<size_t>(b) * N * D;
+  const bool pow2 = is_pow2_scale(scale);
+  const unsigned long long below = (1ull << sub) - 1ull;
+  auto seg = [&](unsigned long long m) { return (m >> (16 * qs)) & 0xffffull; };
+
+  float q[D];
+  ld_row<T, D>(q, Q + boff + static_cast<size_t>(i) * D);
+  if (pow2) {
+#pragma unroll
+    for (int c = 0; c < D; ++c) q[c] *= scale;
+  }
+  if (k_in_lds) {
+    stage_rows<T, D, KST>(Ks, Kx + boff, N, N);
+    __syncthreads();
+  }
+  int key[NS];
+#pragma unroll
+  for (int t = 0; t < NS; ++t) {
+    const int j = sub + 16 * t;
+    key[t] = kNone;
+    if (j < N) {
+      float sc = k_in_lds ? canon_score<T, D>(q, Ks + j * KST)
+                          : canon_score<T, D>(q, Kx + boff + static_cast<size_t>(j) * D);
+      if (!pow2) sc *= scale;
+      key[t] = ordered_key(j == i ? -INFINITY : sc);
+    }
+  }
+  auto count_ge = [&](long m) {
+    int c = 0;
+#pragma unroll
+    for (int t = 0; t < NS; ++t) c += key[t] >= m ? 1 : 0;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) c += __shfl_xor(c, o);
+    return c;
+  };
+
+  long lo, hi;
+  int iters;
+  if (mode == kSelMasked) {
+    // the reference's bisection, step for step (see topk_wide_kernel)
+    int kmin = 2147483647, kmx = kNone;
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      const int j = sub + 16 * t;
+      if (j < N) {
+        kmx = max(kmx, key[t]);
+        if (j != i) kmin = min(kmin, key[t]);
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      kmin = min(kmin, __shfl_xor(kmin, o));
+      kmx = max(kmx, __shfl_xor(kmx, o));
+    }
+    lo = kmin;
+    hi = kmx;
+    iters = bisect;
+  } else {
+    lo = -2147483648L;
+    hi = 2147483647L;
+    iters = 32;  // closes the full 32-bit range
+  }
+  // Exactly topk keys at or above lo also settles the top-k rules (every key
+  // >= lo is taken, no tie straddles lo); the masked rule runs all its
+  // halvings, as the reference does. The loop ends when the wave's four
+  // queries are all settled.
+  bool settled = false;
+  for (int it = 0; it < iters; ++it) {
+    if (__all(settled)) break;
+    const long mid = lo + (hi - lo + 1) / 2;
+    const int c = count_ge(mid);
+    const bool take = c >= topk;
+    if (!settled) {
+      lo = take ? mid : lo;
+      hi = take ? hi : mid - 1;
+    }
+    settled = settled || (mode != kSelMasked && take && c == topk);
+  }
+  const int thr = static_cast<int>(lo);
+  int gt = 0, eq = 0;
+#pragma unroll
+  for (int t = 0; t < NS; ++t) {
+    gt += key[t] > thr ? 1 : 0;
+    eq += (key[t] == thr && sub + 16 * t < N) ? 1 : 0;
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) {
+    gt += __shfl_xor(gt, o);
+    eq += __shfl_xor(eq, o);
+  }
+  const int need_ties = mode == kSelMasked ? eq : topk - gt;
+  const int skip_ties = mode == kSelSort ? eq - need_ties : 0;
+
+  // compact (index, score) in ascending index order: t-major, lane-minor
+  int taken = 0, ties = 0;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < NS; ++t) {
+    const int j = sub + 16 * t;
+    const bool is_tie = j < N && key[t] == thr;
+    const unsigned long long tmask = seg(__ballot(is_tie));
+    const int tie_rank = ties + __popcll(tmask & below);
+    const bool pick = j < N && (key[t] > thr || (is_tie && tie_rank >= skip_ties &&
+                                                  tie_rank < skip_ties + need_ties));
+    const unsigned long long pmask = seg(__ballot(pick));
+    if (pick) {
+      const int pos = taken + __popcll(pmask & below);
+      const float sc = __int_as_float(key[t] ^ ((key[t] >> 31) & 0x7fffffff));
+      sel[pos] = j;
+      sel_s[pos] = sc;
+      mx = fmaxf(mx, sc);
+    }
+    taken += __popcll(pmask);
+    ties += __popcll(tmask);
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  __syncthreads();  // the compacted lists, written by other lanes, are read below
+
+  // aggregation: lane s = 4 slot + g takes rows slot, slot + 4, ..., channels g*E..
+  constexpr int E = D / 4;
+  const int slot = sub >> 2, g = sub & 3;
+  float acc[E];
+#pragma unroll
+  for (int c = 0; c < E; ++c) acc[c] = 0.f;
+  float den = 0.f;
+  for (int m = slot; m < taken; m += 4) {
+    const int j = sel[m];
+    const float w = expf(sel_s[m] - mx);
+    den += w;
+    float vr[E];
+    ld_row<T, E>(vr, V + boff + static_cast<size_t>(j) * D + g * E);
+#pragma unroll
+    for (int c = 0; c < E; ++c) acc[c] = fmaf(w, vr[c], acc[c]);
+  }
+#pragma unroll
+  for (int o = 4; o < 16; o <<= 1) {
+    den += __shfl_xor(den, o);
+#pragma unroll
+    for (int c = 0; c < E; ++c) acc[c] += __shfl_xor(acc[c], o);
+  }
+  if (!live) return;
+  if (slot == 0) {
+    const float inv = 1.f / den;
+    T* dst = O + boff + static_cast<size_t>(i) * D + g * E;
+#pragma unroll
+    for (int c = 0; c < E; ++c) {
+      const float o = acc[c] * inv;
+      if constexpr (sizeof(T) == 4) dst[c] = o;
+      else dst[c] = f32_to_bf16(o);
+    }
+  }
+  if (Idx != nullptr) {  // never for kSelMasked
+    int32_t* dst = Idx + (static_cast<size_t>(b) * N + i) * topk;
+    for (int m = sub; m < topk; m += 16) dst[m] = sel[m];
   }
 }
 
@@ -368,19 +583,54 @@ static hipError_t launch_small(const TopkArgs& a, int kc) {
 
 int wide_cap(const TopkArgs& a) { return a.select == kSelMasked ? a.N : a.topk; }
 
-template <typename T, int D>
-static hipError_t launch_wide(const TopkArgs& a) {
-  // nw waves per workgroup, each holding N + cap words of LDS (<= 64 KiB total)
-  const int cap = wide_cap(a);
-  int nw = 16384 / (a.N + cap);
-  nw = nw < 1 ? 1 : (nw > 4 ? 4 : nw);
-  const long rows = static_cast<long>(a.B) * a.N;
-  const int grid = static_cast<int>((rows + nw - 1) / nw);
-  const size_t lds = static_cast<size_t>(nw) * (a.N + cap) * sizeof(float);
-  hipLaunchKernelGGL((topk_wide_kernel<T, D>), dim3(grid), dim3(64 * nw), lds,
+template <typename T, int D, int NS>
+static hipError_t launch_wide16(const TopkArgs& a, int cap, size_t kbytes, size_t selbytes) {
+  const int k_in_lds = kbytes + selbytes <= 65536 ? 1 : 0;
+  const int n_qblk = (a.N + 15) / 16;
+  const size_t lds = (k_in_lds ? kbytes : 0) + selbytes;
+  hipLaunchKernelGGL((topk_wide16_kernel<T, D, NS>), dim3(a.B * n_qblk), dim3(256), lds,
                      static_cast<hipStream_t>(a.stream), static_cast<const T*>(a.q),
                      static_cast<const T*>(a.k), static_cast<const T*>(a.v), static_cast<T*>(a.out),
-                     a.idx, a.B, a.N, a.topk, a.scale, a.select, a.bisect, cap);
+                     a.idx, a.N, n_qblk, a.topk, a.scale, a.select, a.bisect, cap, k_in_lds);
+  return hipGetLastError();
+}
+
+template <typename T, int D>
+static hipError_t launch_wide(const TopkArgs& a) {
+  {
+    // sixteen lanes per query while the keys fit registers and the selected
+    // lists of sixteen queries fit LDS
+    constexpr int KST = D + 16 / static_cast<int>(sizeof(T));
+    const int cap = wide_cap(a);
+    const size_t selbytes = static_cast<size_t>(16) * 2 * cap * sizeof(int);
+    const size_t kbytes = static_cast<size_t>(a.N) * KST * sizeof(T);
+    if (selbytes <= 65536) {
+      if (a.N <= 64) return launch_wide16<T, D, 4>(a, cap, kbytes, selbytes);
+      if (a.N <= 128) return launch_wide16<T, D, 8>(a, cap, kbytes, selbytes);
+      if (a.N <= 256) return launch_wide16<T, D, 16>(a, cap, kbytes, selbytes);
+      if (a.N <= 512) return launch_wide16<T, D, 32>(a, cap, kbytes, selbytes);
+    }
+  }
+  // nw waves per workgroup (one query each), each holding N + cap words of
+  // LDS; the batch row's keys join them in LDS when everything fits 64 KiB
+  constexpr size_t kBudget = 65536;
+  constexpr int KST = D + 16 / static_cast<int>(sizeof(T));
+  const int cap = wide_cap(a);
+  const size_t per_wave = static_cast<size_t>(a.N + cap) * sizeof(float);
+  const size_t kbytes = static_cast<size_t>(a.N) * KST * sizeof(T);
+  int nw = 4, k_in_lds = 1;
+  while (nw > 1 && kbytes + nw * per_wave > kBudget) --nw;
+  if (kbytes + nw * per_wave > kBudget) {
+    k_in_lds = 0;
+    nw = static_cast<int>(kBudget / per_wave);
+    nw = nw < 1 ? 1 : (nw > 4 ? 4 : nw);
+  }
+  const int n_qblk = (a.N + nw - 1) / nw;
+  const size_t lds = (k_in_lds ? kbytes : 0) + nw * per_wave;
+  hipLaunchKernelGGL((topk_wide_kernel<T, D>), dim3(a.B * n_qblk), dim3(64 * nw), lds,
+                     static_cast<hipStream_t>(a.stream), static_cast<const T*>(a.q),
+                     static_cast<const T*>(a.k), static_cast<const T*>(a.v), static_cast<T*>(a.out),
+                     a.idx, a.N, n_qblk, a.topk, a.scale, a.select, a.bisect, cap, k_in_lds);
   return hipGetLastError();
 }
 
