@@ -127,6 +127,30 @@ int tarmac_zorder_fwd(const void* q, const void* k, const void* v, const float* 
                       void* stream);
 
 /*
+ * Backward of attention over a given peer set idx [B, N, kk] (fp32): the
+ * gradients of the top-k core with the set its forward retained (gradients
+ * flow only through the retained scores and value rows, as for torch.topk's
+ * gather), of the Z-order core with its selector's set, and of prescore
+ * attention. dq is written; dk and dv are ACCUMULATED (fp32 atomic adds, zero
+ * them first). No kernel counterpart in the reference (its Triton kernels are
+ * forward-only, scripts/bench_attention_core.py:172-176); replaces autograd
+ * through src/agents/mappo.py:192-231 in src/training/train_mappo.py:366.
+ */
+int tarmac_fixedset_bwd(const float* q, const float* k, const float* v, const float* dout,
+                        const void* idx, int idx_dtype, int kk, float* dq, float* dk, float* dv,
+                        int B, int N, int d, void* stream);
+
+/*
+ * Backward of dense attention (fp32, self pair excluded): dq, dk, dv are
+ * written. stats: caller-provided workspace of 2 * B * N floats (per query
+ * logsumexp and dO.O). No kernel counterpart in the reference; replaces
+ * autograd through src/agents/mappo.py:361-372 in training.
+ */
+int tarmac_dense_bwd(const float* q, const float* k, const float* v, const float* out,
+                     const float* dout, float* dq, float* dk, float* dv, float* stats, int B, int N,
+                     int d, void* stream);
+
+/*
  * fp32 top-k (d = 16, 32, 64; topk <= 8) can score all pairs on split-bf16
  * MFMA, rescore k+1 candidates in the canonical fp32 order and prove the
  * result is the exact top k (16-query tiles where the proof fails recompute

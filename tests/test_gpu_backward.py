@@ -1,0 +1,102 @@
+"""Backward kernels against torch autograd in float64 (CPU).
+
+The reference's Triton kernels are forward-only; its training differentiates
+the PyTorch composition (src/agents/mappo.py:192-231 gather path, :361-372
+dense). Here torch autograd of that composition, in float64 on the CPU, is
+the reference gradient; the fixed-set composition uses the kernel's own
+retained sets. Bar: 1e-4 of max|ref| (normwise; dk, dv accumulate with fp32
+atomics in no fixed order).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import qkv
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _ref_set(q, k, v, idx, g):
+    t = [torch.from_numpy(np.asarray(x, np.float64)).requires_grad_(True) for x in (q, k, v)]
+    qt, kt, vt = t
+    B, N, d = qt.shape
+    ix = torch.from_numpy(idx).long()
+    kk = ix.shape[-1]
+    kg = torch.gather(kt.unsqueeze(1).expand(B, N, N, d), 2, ix.unsqueeze(-1).expand(B, N, kk, d))
+    vg = torch.gather(vt.unsqueeze(1).expand(B, N, N, d), 2, ix.unsqueeze(-1).expand(B, N, kk, d))
+    s = (qt.unsqueeze(-2) * kg).sum(-1) / d ** 0.5
+    out = (torch.softmax(s, -1).unsqueeze(-1) * vg).sum(-2)
+    (out * torch.from_numpy(g.astype(np.float64))).sum().backward()
+    return [x.grad.numpy() for x in t]
+
+
+def _ref_dense(q, k, v, g):
+    t = [torch.from_numpy(np.asarray(x, np.float64)).requires_grad_(True) for x in (q, k, v)]
+    qt, kt, vt = t
+    N, d = qt.shape[1], qt.shape[2]
+    s = (qt @ kt.transpose(-1, -2) / d ** 0.5).masked_fill(torch.eye(N, dtype=torch.bool), float("-inf"))
+    out = torch.softmax(s, -1) @ vt
+    (out * torch.from_numpy(g.astype(np.float64))).sum().backward()
+    return [x.grad.numpy() for x in t]
+
+
+def _close(got, want):
+    for a, b in zip(got, want):
+        assert np.abs(a.cpu().numpy() - b).max() <= TOL * np.abs(b).max()
+
+
+def _dev(*xs):
+    return [torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in xs]
+
+
+@pytest.mark.parametrize("N,d,kk", [(6, 16, 2), (24, 8, 5), (100, 16, 3), (256, 16, 2),
+                                    (256, 32, 4), (300, 64, 12), (512, 16, 8)])
+def test_topk_backward(N, d, kk):
+    from tarmac.kernels import fixedset_attention_backward, topk_attention
+    B = 3
+    q, k, v = qkv(31 * N + kk, B, N, d)
+    g = np.random.default_rng(N).standard_normal(q.shape).astype(np.float32)
+    qd, kd, vd, gd = _dev(q, k, v, g)
+    _, idx = topk_attention(qd, kd, vd, kk, return_indices=True)
+    got = fixedset_attention_backward(qd, kd, vd, idx, gd)
+    torch.cuda.synchronize()
+    _close(got, _ref_set(q, k, v, idx.cpu().numpy(), g))
+
+
+@pytest.mark.parametrize("idx_dtype", [torch.int32, torch.int64])
+def test_fixedset_backward_any_sets(idx_dtype):
+    """Arbitrary peer sets, repeated peers and the self pair included."""
+    from tarmac.kernels import fixedset_attention_backward
+    B, N, d, kk = 2, 40, 16, 6
+    q, k, v = qkv(9, B, N, d)
+    g = np.random.default_rng(2).standard_normal(q.shape).astype(np.float32)
+    idx = np.random.default_rng(3).integers(0, N, size=(B, N, kk))
+    qd, kd, vd, gd = _dev(q, k, v, g)
+    got = fixedset_attention_backward(qd, kd, vd, torch.from_numpy(idx).to(idx_dtype).cuda(), gd)
+    torch.cuda.synchronize()
+    _close(got, _ref_set(q, k, v, idx, g))
+
+
+@pytest.mark.parametrize("N,d", [(6, 16), (24, 8), (100, 32), (256, 16), (300, 64), (700, 16)])
+def test_dense_backward(N, d):
+    from tarmac.kernels import dense_attention_backward, fused_dense_attention
+    B = 2
+    q, k, v = qkv(5 * N + d, B, N, d)
+    g = np.random.default_rng(N + 1).standard_normal(q.shape).astype(np.float32)
+    qd, kd, vd, gd = _dev(q, k, v, g)
+    out = fused_dense_attention(qd, kd, vd)
+    got = dense_attention_backward(qd, kd, vd, out, gd)
+    torch.cuda.synchronize()
+    _close(got, _ref_dense(q, k, v, g))
+
+
+def test_backward_rejects_bf16():
+    from tarmac.kernels import dense_attention_backward
+    q, k, v = (t.to(torch.bfloat16) for t in _dev(*qkv(1, 2, 16, 16)))
+    with pytest.raises(NotImplementedError):
+        dense_attention_backward(q, k, v, q, q)

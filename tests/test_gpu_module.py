@@ -62,12 +62,58 @@ def test_module_info_and_errors(golden):
         bad(x)
 
 
-def test_module_forward_under_grad_then_backward_raises(golden):
-    tag = "comm_n6_d16"
-    x = torch.from_numpy(golden[f"{tag}_x"]).cuda()
-    mod = _module("topk_gather", 2, 6, 16, golden, tag)
+def _torch_module_ref(mod, x, pos, mode, k, idx=None):
+    """float64 CPU restatement of the module (qkv split, core, gelu, proj) in
+    torch, with the given peer sets for the set-based modes; autograd gives
+    the reference gradients."""
+    import torch.nn.functional as F
+    W = {n: p.detach().double().cpu().requires_grad_(True) for n, p in mod.named_parameters()}
+    xr = x.detach().double().cpu().requires_grad_(True)
+    qkv = xr @ W["qkv.weight"].T + W["qkv.bias"]
+    q, kk_, v = qkv.chunk(3, dim=-1)
+    B, N, d = q.shape
+    s = q @ kk_.transpose(-1, -2) / d ** 0.5
+    if mode in ("dense", "dense_sdpa"):
+        s = s.masked_fill(torch.eye(N, dtype=torch.bool), float("-inf"))
+        msg = torch.softmax(s, -1) @ v
+    else:
+        ix = torch.from_numpy(idx).long()
+        sg = torch.gather(s, -1, ix)
+        w = torch.softmax(sg, -1)
+        vg = torch.gather(v.unsqueeze(1).expand(B, N, N, d), 2, ix.unsqueeze(-1).expand(B, N, ix.shape[-1], d))
+        msg = (w.unsqueeze(-1) * vg).sum(-2)
+    out = F.gelu(msg) @ W["proj.weight"].T + W["proj.bias"]
+    return out, xr, W
+
+
+@pytest.mark.parametrize("mode,k", [("dense", 0), ("topk_gather", 2), ("topk", 3), ("zorder_k", 2)])
+def test_module_backward_matches_torch_autograd(golden, mode, k):
+    """Forward + backward of the whole module: the HIP core's gradients
+    (through the retained set for top-k / Z-order) against torch autograd of
+    the same composition in float64."""
+    tag = "comm_n24_d16"
+    mod = _module(mode, k, 24, 16, golden, tag)
     mod.collect_info = False
-    out, _ = mod(x)
-    assert out.requires_grad
-    with pytest.raises(NotImplementedError):
-        out.sum().backward()
+    x = torch.from_numpy(golden[f"{tag}_x"]).cuda().requires_grad_(True)
+    pos = torch.from_numpy(golden[f"{tag}_pos"]).cuda()
+    out, _ = mod(x, pos if mode == "zorder_k" else None)
+    g = torch.from_numpy(np.random.default_rng(5).standard_normal(out.shape).astype(np.float32)).cuda()
+    (out * g).sum().backward()
+    idx = None
+    if mode != "dense":
+        from tarmac.kernels import topk_attention, zorder_attention
+        with torch.no_grad():
+            q, kk_, v = (t.contiguous() for t in mod.qkv(x).chunk(3, dim=-1))
+            kk = min(max(k, 1), 23)
+            idx = (zorder_attention(q, kk_, v, pos, kk, 10, return_indices=True)[1]
+                   if mode == "zorder_k" else topk_attention(q, kk_, v, kk, return_indices=True)[1])
+        idx = idx.cpu().numpy()
+    ref, xr, W = _torch_module_ref(mod, x, pos, mode, k, idx)
+    assert np.abs(out.detach().cpu().numpy() - ref.detach().numpy()).max() <= 1e-5 * ref.abs().max().item()
+    (ref * g.double().cpu()).sum().backward()
+    for name, p in mod.named_parameters():
+        if name.startswith("k_gate"):
+            continue
+        got, want = p.grad.cpu().numpy(), W[name].grad.numpy()
+        assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max(), name
+    assert np.abs(x.grad.cpu().numpy() - xr.grad.numpy()).max() <= 1e-4 * xr.grad.abs().max().item()

@@ -213,6 +213,37 @@ int tarmac_zorder_fwd(const void* q, const void* k, const void* v, const float* 
   return hip_status(tarmac::run_zorder(a), fn);
 }
 
+int tarmac_fixedset_bwd(const float* q, const float* k, const float* v, const float* dout,
+                        const void* idx, int idx_dtype, int kk, float* dq, float* dk, float* dv,
+                        int B, int N, int d, void* stream) {
+  const char* fn = "tarmac_fixedset_bwd";
+  int rc = check_core(q, k, v, dout, B, N, d, TARMAC_DTYPE_F32, fn);
+  if (rc) return rc;
+  if (!idx || !dq || !dk || !dv) return fail(TARMAC_ERR_INVALID, "%s: null pointer", fn);
+  if (!aligned(dq, 16) || !aligned(dk, 16) || !aligned(dv, 16))
+    return fail(TARMAC_ERR_INVALID, "%s: gradient buffers must be 16-byte aligned", fn);
+  if (idx_dtype != TARMAC_IDX_I32 && idx_dtype != TARMAC_IDX_I64)
+    return fail(TARMAC_ERR_INVALID, "%s: idx_dtype must be TARMAC_IDX_I32 or TARMAC_IDX_I64", fn);
+  if (kk < 1) return fail(TARMAC_ERR_INVALID, "%s: kk must be >= 1 (got %d)", fn, kk);
+  tarmac::FixedsetBwdArgs a{q, k, v, dout, idx, idx_dtype == TARMAC_IDX_I64, dq, dk, dv,
+                            B, N, d, kk, inv_sqrt(d), stream};
+  return hip_status(tarmac::run_fixedset_bwd(a), fn);
+}
+
+int tarmac_dense_bwd(const float* q, const float* k, const float* v, const float* out,
+                     const float* dout, float* dq, float* dk, float* dv, float* stats, int B, int N,
+                     int d, void* stream) {
+  const char* fn = "tarmac_dense_bwd";
+  int rc = check_core(q, k, v, out, B, N, d, TARMAC_DTYPE_F32, fn);
+  if (rc) return rc;
+  if (!dout || !dq || !dk || !dv || !stats) return fail(TARMAC_ERR_INVALID, "%s: null pointer", fn);
+  if (!aligned(dout, 16) || !aligned(dq, 16) || !aligned(dk, 16) || !aligned(dv, 16) ||
+      !aligned(stats, 8))
+    return fail(TARMAC_ERR_INVALID, "%s: misaligned buffer", fn);
+  tarmac::DenseBwdArgs a{q, k, v, out, dout, dq, dk, dv, stats, B, N, d, inv_sqrt(d), stream};
+  return hip_status(tarmac::run_dense_bwd(a), fn);
+}
+
 int tarmac_set_topk_filter(int mode) {
   if (mode < tarmac::kFilterOff || mode > tarmac::kFilterAlways) {
     fail(TARMAC_ERR_INVALID, "tarmac_set_topk_filter: mode must be 0, 1 or 2 (got %d)", mode);

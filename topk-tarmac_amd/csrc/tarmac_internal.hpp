@@ -59,6 +59,36 @@ struct FixedsetArgs {
   void* stream;
 };
 
+struct FixedsetBwdArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* dout;
+  const void* idx;
+  int idx_is_i64;
+  float* dq;        // written
+  float* dk;        // accumulated (zero on entry)
+  float* dv;        // accumulated (zero on entry)
+  int B, N, d, kk;
+  float scale;
+  void* stream;
+};
+
+struct DenseBwdArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* out;
+  const float* dout;
+  float* dq;
+  float* dk;
+  float* dv;
+  float* stats;     // workspace [B, N, 2]: logsumexp and dO.O per query
+  int B, N, d;
+  float scale;
+  void* stream;
+};
+
 struct MortonArgs {
   const float* pos;
   void* idx;          // nullable
@@ -91,6 +121,8 @@ hipError_t run_fixedset(const FixedsetArgs& a);
 hipError_t run_morton_window(const MortonArgs& a);
 hipError_t run_zorder(const ZorderArgs& a);
 hipError_t run_noop(float* out, void* stream);
+hipError_t run_fixedset_bwd(const FixedsetBwdArgs& a);
+hipError_t run_dense_bwd(const DenseBwdArgs& a);
 
 size_t topk_lds_bytes(int dtype, int d, int kc);
 size_t topk_filter_lds_bytes(int d, int kc);

@@ -40,6 +40,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tarmac_fixedset_fwd": ([_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P], _I),
     "tarmac_morton_window": ([_P, _P, _I, _P, _I, _I, _I, _I, _P], _I),
     "tarmac_zorder_fwd": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "tarmac_fixedset_bwd": ([_P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I, _P], _I),
+    "tarmac_dense_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P], _I),
     "tarmac_set_topk_filter": ([_I], _I),
     "tarmac_noop": ([_P, _P], _I),
 }

@@ -22,9 +22,12 @@ zorder_k       ``tarmac_zorder_fwd`` (selector + attend in one launch)
 The training-study arms ``random_k``, ``entmax`` and ``adaptive_topk`` are
 not part of the timed core and are not provided here.
 
-The kernels are forward-only, as the reference's Triton kernels are
-(``scripts/bench_attention_core.py:172-176``): calling ``backward`` through the
-core raises ``NotImplementedError``.
+The reference's Triton kernels are forward-only
+(``scripts/bench_attention_core.py:172-176``) and its training differentiates
+the PyTorch composition; here the core's backward runs on HIP kernels too
+(:mod:`tarmac.kernels.backward`, fp32): gradients reach q, k, v through the
+retained set of the top-k and Z-order cores, and through every pair of the
+dense core.
 """
 
 from __future__ import annotations
@@ -36,6 +39,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from ..kernels.backward import dense_attention_backward, fixedset_attention_backward
 from ..kernels.fused_dense_attention import fused_dense_attention
 from ..kernels.fused_topk_attention import topk_attention
 from ..kernels.prescore_selection import zorder_attention
@@ -69,22 +73,43 @@ def _ortho_init(layer: nn.Linear, gain: float = np.sqrt(2.0)) -> None:
     nn.init.zeros_(layer.bias)
 
 
-class _Core(torch.autograd.Function):
-    """Wraps a forward-only HIP core so it can sit in a graph that tracks
-    gradients (the projections around it do); backward is not available."""
+class _DenseCore(torch.autograd.Function):
+    """Dense core with the HIP backward (fp32)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v):
+        out = fused_dense_attention(q, k, v)
+        ctx.save_for_backward(q, k, v, out)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out = ctx.saved_tensors
+        return dense_attention_backward(q, k, v, out, dout)
+
+
+class _SetCore(torch.autograd.Function):
+    """A core that attends over a peer set it chooses itself (top-k,
+    Z-order); the HIP backward treats that set as fixed, as autograd through
+    ``torch.topk``'s gather does. ``fn`` returns (out, idx)."""
 
     @staticmethod
     def forward(ctx, fn, q, k, v, *extra):
-        res = fn(q, k, v, *extra)
-        if isinstance(res, tuple):
-            ctx.mark_non_differentiable(*res[1:])
-        return res
+        out, idx = fn(q, k, v, *extra)
+        ctx.mark_non_differentiable(idx)
+        ctx.save_for_backward(q, k, v, idx)
+        ctx.n_extra = len(extra)
+        return out, idx
 
     @staticmethod
-    def backward(ctx, *grads):
-        raise NotImplementedError(
-            "the tarmac attention-core kernels are forward-only; backward kernels "
-            "are not built yet")
+    def backward(ctx, dout, _didx):
+        q, k, v, idx = ctx.saved_tensors
+        dq, dk, dv = fixedset_attention_backward(q, k, v, idx, dout)
+        return (None, dq, dk, dv) + (None,) * ctx.n_extra
+
+
+def _tracks_grad(*ts: torch.Tensor) -> bool:
+    return torch.is_grad_enabled() and any(t.requires_grad for t in ts)
 
 
 def _entropy(w: torch.Tensor) -> float:
@@ -145,29 +170,36 @@ class AttentionComm(nn.Module):
             if pos is None:
                 raise ValueError("attn_mode='zorder_k' needs agent positions")
             kk = self._k_eff(N)
-            want_idx = self.collect_info
-            res = _Core.apply(
-                lambda a, b, c, p: zorder_attention(a, b, c, p, kk, ZORDER_BITS,
-                                                    return_indices=want_idx),
-                q, k, v, pos)
-            msg, idx = res if want_idx else (res, None)
+            if _tracks_grad(q, k, v):
+                msg, idx = _SetCore.apply(
+                    lambda a, b, c, p: zorder_attention(a, b, c, p, kk, ZORDER_BITS,
+                                                        return_indices=True),
+                    q, k, v, pos)
+            else:
+                res = zorder_attention(q, k, v, pos, kk, ZORDER_BITS,
+                                       return_indices=self.collect_info)
+                msg, idx = res if self.collect_info else (res, None)
             info["effective_k"] = float(kk)
-            if want_idx:
+            if self.collect_info:
                 info["mean_attn_entropy"] = _entropy(self._set_weights(q, k, idx))
             return self.proj(F.gelu(msg)), info
 
         if mode in ("dense", "dense_sdpa"):
-            msg = _Core.apply(lambda a, b, c: fused_dense_attention(a, b, c), q, k, v)
+            msg = (_DenseCore.apply(q, k, v) if _tracks_grad(q, k, v)
+                   else fused_dense_attention(q, k, v))
             if mode == "dense" and self.collect_info:
                 info["mean_attn_entropy"] = _entropy(self._dense_weights(q, k))
             return self.proj(F.gelu(msg)), info
 
         if mode in ("topk", "topk_gather"):
             kk = self._k_eff(N)
-            want_idx = self.collect_info and mode == "topk_gather"
-            res = _Core.apply(
-                lambda a, b, c: topk_attention(a, b, c, kk, return_indices=want_idx), q, k, v)
-            msg, idx = res if want_idx else (res, None)
+            if _tracks_grad(q, k, v):
+                msg, idx = _SetCore.apply(
+                    lambda a, b, c: topk_attention(a, b, c, kk, return_indices=True), q, k, v)
+            else:
+                want_idx = self.collect_info and mode == "topk_gather"
+                res = topk_attention(q, k, v, kk, return_indices=want_idx)
+                msg, idx = res if want_idx else (res, None)
             if mode == "topk":
                 if self.collect_info:
                     info["mean_attn_entropy"] = _entropy(self._dense_weights(q, k))

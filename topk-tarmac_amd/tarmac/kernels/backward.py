@@ -1,0 +1,74 @@
+"""Backward passes of the attention core (fp32, HIP).
+
+The reference's Triton kernels are forward-only
+(``scripts/bench_attention_core.py:172-176``); in training it differentiates
+its PyTorch composition with autograd (``src/agents/mappo.py:192-231`` gather
+path, ``:361-372`` dense path). These wrappers compute the same gradients on
+the GPU:
+
+* ``fixedset_attention_backward`` -- attention over a given peer set: the
+  top-k core with the set its forward retained (gradients flow only through
+  the retained scores and value rows, as for ``torch.topk``'s gather), the
+  Z-order core with its selector's set, and prescore attention.
+* ``dense_attention_backward`` -- the dense core (self pair excluded).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _launch, _lib
+
+
+def _f32(*ts):
+    for t in ts:
+        if t.dtype != torch.float32:
+            raise NotImplementedError("the backward kernels take fp32 tensors")
+
+
+def fixedset_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                                idx: torch.Tensor, dout: torch.Tensor):
+    """Gradients (dq, dk, dv) of ``softmax(q k_S^T / sqrt(d)) v_S`` over the
+    peer sets ``idx`` ([B, N, kk], int32 or int64)."""
+    q, k, v = _launch.core(q, k, v)
+    _f32(q, dout)
+    dout = dout.contiguous()
+    if dout.shape != q.shape:
+        raise ValueError(f"dout shape {tuple(dout.shape)} != {tuple(q.shape)}")
+    idx = idx.contiguous()
+    B, N, d = q.shape
+    if idx.dim() != 3 or idx.shape[:2] != (B, N):
+        raise ValueError(f"idx must be [B, N, kk], got {tuple(idx.shape)}")
+    if idx.dtype not in (torch.int32, torch.int64):
+        raise ValueError("idx must be int32 or int64")
+    dq = torch.empty_like(q)
+    dk = torch.zeros_like(k)
+    dv = torch.zeros_like(v)
+    with torch.cuda.device(q.device):
+        rc = _lib.LIB.tarmac_fixedset_bwd(
+            _launch.ptr(q), _launch.ptr(k), _launch.ptr(v), _launch.ptr(dout), _launch.ptr(idx),
+            _lib.IDX_I64 if idx.dtype == torch.int64 else _lib.IDX_I32, idx.shape[-1],
+            _launch.ptr(dq), _launch.ptr(dk), _launch.ptr(dv), B, N, d, _launch.stream(q))
+        _lib.check(rc)
+    return dq, dk, dv
+
+
+def dense_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                             out: torch.Tensor, dout: torch.Tensor):
+    """Gradients (dq, dk, dv) of dense attention with the self pair excluded,
+    given its forward output ``out``."""
+    q, k, v = _launch.core(q, k, v)
+    _f32(q, out, dout)
+    out, dout = out.contiguous(), dout.contiguous()
+    if out.shape != q.shape or dout.shape != q.shape:
+        raise ValueError("out and dout must match q's shape")
+    B, N, d = q.shape
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    stats = torch.empty(B, N, 2, device=q.device, dtype=torch.float32)
+    with torch.cuda.device(q.device):
+        rc = _lib.LIB.tarmac_dense_bwd(
+            _launch.ptr(q), _launch.ptr(k), _launch.ptr(v), _launch.ptr(out), _launch.ptr(dout),
+            _launch.ptr(dq), _launch.ptr(dk), _launch.ptr(dv), _launch.ptr(stats), B, N, d,
+            _launch.stream(q))
+        _lib.check(rc)
+    return dq, dk, dv
