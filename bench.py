@@ -356,6 +356,58 @@ def main() -> int:
                                    "graph_us": {k_: round(v_, 3) for k_, v_ in sg.items()}}
     detail["module_forward_B256_in64_msg16"] = mod_rows
 
+    # ---- forward + backward (the reference's module benchmark times both,
+    # scripts/microbenchmark_comm.py:401): HIP backward kernels vs torch
+    # autograd of the composed reference arm, eager, same weights
+    def fwd_bwd_time(fn, reps):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            e1.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e3)
+        return round(best, 3)
+
+    fb_rows = {}
+    for n in (6, 96, 384):
+        kk = max(1, int(0.25 * (n - 1)))
+        gx = np.random.default_rng(900 + n)
+        x = torch.from_numpy(gx.standard_normal((256, n, 64)).astype(np.float32)).to(dev)
+        x.requires_grad_(True)
+        gout = torch.from_numpy(gx.standard_normal((256, n, 16)).astype(np.float32)).to(dev)
+        row = {}
+        for mode in ("dense", "topk_gather"):
+            cfg = MAPPOConfig(obs_dim=18, n_actions=5, n_agents=n, hidden=64, use_comm=True,
+                              msg_dim=16, attn_mode=mode, topk=kk)
+            m = AttentionComm(cfg, in_dim=64).to(dev)
+            m.collect_info = False
+            row[f"hip_{mode}"] = fwd_bwd_time(lambda m=m: (m(x)[0] * gout).sum().backward(),
+                                              args.reps)
+            if mode == "topk_gather":
+                def torch_fb(m=m, kk=kk):
+                    q_, k_, v_ = (t.contiguous() for t in m.qkv(x).chunk(3, dim=-1))
+                    out_ = m.proj(F.gelu(reference_topk_attention(q_, k_, v_, kk)))
+                    (out_ * gout).sum().backward()
+                row["torch_topk_gather"] = fwd_bwd_time(torch_fb, args.reps)
+        fb_rows[f"N{n}_k{kk}"] = row
+    detail["module_fwd_bwd_B256_in64_msg16_us"] = fb_rows
+
+    # ---- core backward kernels at the metric point (B=1024, N=256, d=16) ---
+    from tarmac.kernels import dense_attention_backward, fixedset_attention_backward
+    gq = torch.from_numpy(rng.standard_normal((B, N, D)).astype(np.float32)).to(dev)
+    out_d = fused_dense_attention(q, k, v)
+    fbk = {"dense_bwd": lambda: dense_attention_backward(q, k, v, out_d, gq)}
+    for kk in (1, 2, 4):
+        fbk[f"topk_k{kk}_bwd"] = (lambda kk=kk: fixedset_attention_backward(q, k, v, idx[kk], gq))
+    sb = {nm: harness.stats(sm)["min_us"] for nm, sm in
+          harness.time_interleaved(fbk, args.reps, 5, 2).items()}
+    detail["core_backward_B1024_N256_d16_us"] = {nm: round(t, 3) for nm, t in sb.items()}
+
     # ---- small-N, launch-bound regime (B=1024, d=16, k=2): eager vs graph --
     small = {}
     for n in (12, 24, 48, 96):

@@ -17,7 +17,8 @@
 //   D_i = sum_j w_j dw_j, ds_j = w_j (dw_j - D_i),
 //   dq_i = c sum_j ds_j k_j,  dk_j += c ds_j q_i,  dv_j += w_j dO_i.
 // dk and dv collect contributions from every query that retained j, with
-// fp32 atomic adds (accumulation order is not fixed).
+// fp32 atomic adds (accumulation order is not fixed): in LDS, one workgroup
+// per batch row, when the row's dK and dV fit 64 KiB; else in global memory.
 //
 // Dense, self pair excluded: P = softmax(c Q K^T), D_i = dO_i.O_i,
 //   dS = P o (dO V^T - D 1^T),  dQ = c dS K,  dK = c dS^T Q,  dV = P^T dO.
@@ -57,41 +58,65 @@ __device__ __forceinline__ void atomic_add_row(float* dst, const float (&x)[E], 
 // fixed peer set
 // ---------------------------------------------------------------------------
 
+// One query (a quad of lanes): dq is written; the dk / dv rows of its peers
+// receive atomic adds (global memory or LDS). Peers are taken U at a time
+// with all their index, K and V loads in flight together; when the set fits
+// one batch (kk <= U) the second pass reuses the rows from registers.
 template <int D, typename I>
-__global__ void __launch_bounds__(256)
-fixedset_bwd_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
-                    const float* __restrict__ V, const float* __restrict__ dO,
-                    const I* __restrict__ Idx, float* __restrict__ dQ, float* __restrict__ dK,
-                    float* __restrict__ dV, int B, int N, int kk, float scale) {
+__device__ __forceinline__ void fixedset_bwd_row(const float* __restrict__ qrow,
+                                                 const float* __restrict__ grow,
+                                                 const float* __restrict__ Kb,
+                                                 const float* __restrict__ Vb,
+                                                 const I* __restrict__ ir, float* __restrict__ dqrow,
+                                                 float* dK, float* dV, int N, int kk, float scale,
+                                                 int sub) {
   constexpr int E = D / 4;
-  const long row = (static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x) >> 2;
-  if (row >= static_cast<long>(B) * N) return;  // whole quads exit together
-  const int sub = threadIdx.x & 3;
-  const int b = static_cast<int>(row / N);
-  const size_t boff = static_cast<size_t>(b) * N * D;
-  const I* ir = Idx + static_cast<size_t>(row) * kk;
+  constexpr int U = E <= 4 ? 8 : (E <= 8 ? 4 : 2);
   float q[E], g[E];
-  ld_f32<E>(q, Q + static_cast<size_t>(row) * D + sub * E);
-  ld_f32<E>(g, dO + static_cast<size_t>(row) * D + sub * E);
+  ld_f32<E>(q, qrow + sub * E);
+  ld_f32<E>(g, grow + sub * E);
+  int p[U];
+  float kr[U][E], vr[U][E], sc[U], dw[U];
+  auto load_batch = [&](int j0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool live = j0 + u < kk;
+      p[u] = live ? static_cast<int>(ir[j0 + u]) : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int pc = min(max(p[u], 0), N - 1);
+      ld_f32<E>(kr[u], Kb + static_cast<size_t>(pc) * D + sub * E);
+      ld_f32<E>(vr[u], Vb + static_cast<size_t>(pc) * D + sub * E);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      sc[u] = j0 + u < kk ? quad_dot<E>(q, kr[u]) * scale : -INFINITY;
+      dw[u] = quad_dot<E>(g, vr[u]);
+    }
+  };
 
-  // pass 1: softmax statistics and D = sum_j w_j dw_j (online)
+  // pass 1: softmax statistics and D = sum_j w_j dw_j (online, per batch)
   float m = -INFINITY, l = 0.f, a = 0.f;
   bool bad = false;
-  for (int j = 0; j < kk; ++j) {
-    int p = static_cast<int>(ir[j]);
-    bad |= (p < 0) | (p >= N);
-    p = min(max(p, 0), N - 1);
-    float kr[E], vr[E];
-    ld_f32<E>(kr, Kx + boff + static_cast<size_t>(p) * D + sub * E);
-    ld_f32<E>(vr, V + boff + static_cast<size_t>(p) * D + sub * E);
-    const float s = quad_dot<E>(q, kr) * scale;
-    const float dw = quad_dot<E>(g, vr);
-    const float m_new = fmaxf(m, s);
-    const float alpha = m == -INFINITY ? 0.f : expf(m - m_new);
-    const float e = expf(s - m_new);
-    l = l * alpha + e;
-    a = a * alpha + e * dw;
-    m = m_new;
+  for (int j0 = 0; j0 < kk; j0 += U) {
+    load_batch(j0);
+    float mb = m;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      bad |= j0 + u < kk && ((p[u] < 0) | (p[u] >= N));
+      mb = fmaxf(mb, sc[u]);
+    }
+    const float alpha = m == -INFINITY ? 0.f : expf(m - mb);
+    l *= alpha;
+    a *= alpha;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float e = sc[u] == -INFINITY ? 0.f : expf(sc[u] - mb);
+      l += e;
+      a = fmaf(e, dw[u], a);
+    }
+    m = mb;
   }
   const float inv_l = 1.f / l;
   const float Dq = a * inv_l;
@@ -100,29 +125,74 @@ fixedset_bwd_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   float dq[E];
 #pragma unroll
   for (int c = 0; c < E; ++c) dq[c] = 0.f;
-  for (int j = 0; j < kk; ++j) {
-    const int p0 = static_cast<int>(ir[j]);
-    const bool ok = p0 >= 0 && p0 < N;
-    const int p = min(max(p0, 0), N - 1);
-    float kr[E], vr[E];
-    ld_f32<E>(kr, Kx + boff + static_cast<size_t>(p) * D + sub * E);
-    ld_f32<E>(vr, V + boff + static_cast<size_t>(p) * D + sub * E);
-    const float s = quad_dot<E>(q, kr) * scale;
-    const float dw = quad_dot<E>(g, vr);
-    const float w = expf(s - m) * inv_l;
-    const float ds = w * (dw - Dq);
+  for (int j0 = 0; j0 < kk; j0 += U) {
+    if (kk > U) load_batch(j0);  // else the single batch is still in registers
 #pragma unroll
-    for (int c = 0; c < E; ++c) dq[c] = fmaf(ds, kr[c], dq[c]);
-    if (ok) {
-      float* dkr = dK + boff + static_cast<size_t>(p) * D + sub * E;
-      float* dvr = dV + boff + static_cast<size_t>(p) * D + sub * E;
-      atomic_add_row<E>(dkr, q, ds * scale);
-      atomic_add_row<E>(dvr, g, w);
+    for (int u = 0; u < U; ++u) {
+      if (j0 + u >= kk) continue;
+      const float w = expf(sc[u] - m) * inv_l;
+      const float ds = w * (dw[u] - Dq);
+#pragma unroll
+      for (int c = 0; c < E; ++c) dq[c] = fmaf(ds, kr[u][c], dq[c]);
+      if (p[u] >= 0 && p[u] < N) {
+        atomic_add_row<E>(dK + static_cast<size_t>(p[u]) * D + sub * E, q, ds * scale);
+        atomic_add_row<E>(dV + static_cast<size_t>(p[u]) * D + sub * E, g, w);
+      }
     }
   }
 #pragma unroll
   for (int c = 0; c < E; ++c) dq[c] = bad ? __int_as_float(0x7fc00000) : dq[c] * scale;
-  st_f32<E>(dQ + static_cast<size_t>(row) * D + sub * E, dq);
+  st_f32<E>(dqrow + sub * E, dq);
+}
+
+// Global accumulation: one quad per query over the whole grid; dK, dV must
+// be zero on entry.
+template <int D, typename I>
+__global__ void __launch_bounds__(256)
+fixedset_bwd_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
+                    const float* __restrict__ V, const float* __restrict__ dO,
+                    const I* __restrict__ Idx, float* __restrict__ dQ, float* __restrict__ dK,
+                    float* __restrict__ dV, int B, int N, int kk, float scale) {
+  const long row = (static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x) >> 2;
+  if (row >= static_cast<long>(B) * N) return;  // whole quads exit together
+  const int b = static_cast<int>(row / N);
+  const size_t boff = static_cast<size_t>(b) * N * D;
+  fixedset_bwd_row<D, I>(Q + static_cast<size_t>(row) * D, dO + static_cast<size_t>(row) * D,
+                         Kx + boff, V + boff, Idx + static_cast<size_t>(row) * kk,
+                         dQ + static_cast<size_t>(row) * D, dK + boff, dV + boff, N, kk, scale,
+                         threadIdx.x & 3);
+}
+
+// LDS accumulation: one workgroup (256 query quads) per batch row sums dK and dV for its N keys
+// in LDS (fast atomics, no zeroing pass), then adds them to dK, dV once.
+template <int D, typename I>
+__global__ void __launch_bounds__(1024)
+fixedset_bwd_lds_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
+                        const float* __restrict__ V, const float* __restrict__ dO,
+                        const I* __restrict__ Idx, float* __restrict__ dQ,
+                        float* __restrict__ dK, float* __restrict__ dV, int N, int kk,
+                        float scale) {
+  extern __shared__ __align__(16) float acc[];  // dK rows then dV rows, N * D each
+  const int b = blockIdx.x;
+  const size_t boff = static_cast<size_t>(b) * N * D;
+  float* dKs = acc;
+  float* dVs = acc + static_cast<size_t>(N) * D;
+  for (int t = threadIdx.x; t < 2 * N * D; t += blockDim.x) acc[t] = 0.f;
+  __syncthreads();
+  const int quads = blockDim.x >> 2;
+  for (int i0 = 0; i0 < N; i0 += quads) {
+    const int i = i0 + (threadIdx.x >> 2);
+    if (i < N) {  // whole quads agree
+      const size_t row = static_cast<size_t>(b) * N + i;
+      fixedset_bwd_row<D, I>(Q + row * D, dO + row * D, Kx + boff, V + boff, Idx + row * kk,
+                             dQ + row * D, dKs, dVs, N, kk, scale, threadIdx.x & 3);
+    }
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < N * D; t += blockDim.x) {
+    dK[boff + t] += dKs[t];
+    dV[boff + t] += dVs[t];
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -263,11 +333,25 @@ dense_bwd_kv_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
 // launchers
 // ---------------------------------------------------------------------------
 
+constexpr size_t kBwdLdsBudget = 65536;
+
 template <int D>
 static hipError_t launch_fixedset_bwd(const FixedsetBwdArgs& a) {
   const long rows = static_cast<long>(a.B) * a.N;
   const int grid = static_cast<int>((rows * 4 + 255) / 256);
   hipStream_t st = static_cast<hipStream_t>(a.stream);
+  const size_t lds = static_cast<size_t>(2) * a.N * D * sizeof(float);
+  if (lds <= kBwdLdsBudget) {  // the batch row's dK, dV fit LDS
+    if (a.idx_is_i64)
+      hipLaunchKernelGGL((fixedset_bwd_lds_kernel<D, int64_t>), dim3(a.B), dim3(1024), lds, st,
+                         a.q, a.k, a.v, a.dout, static_cast<const int64_t*>(a.idx), a.dq, a.dk,
+                         a.dv, a.N, a.kk, a.scale);
+    else
+      hipLaunchKernelGGL((fixedset_bwd_lds_kernel<D, int32_t>), dim3(a.B), dim3(1024), lds, st,
+                         a.q, a.k, a.v, a.dout, static_cast<const int32_t*>(a.idx), a.dq, a.dk,
+                         a.dv, a.N, a.kk, a.scale);
+    return hipGetLastError();
+  }
   if (a.idx_is_i64)
     hipLaunchKernelGGL((fixedset_bwd_kernel<D, int64_t>), dim3(grid), dim3(256), 0, st, a.q, a.k,
                        a.v, a.dout, static_cast<const int64_t*>(a.idx), a.dq, a.dk, a.dv, a.B, a.N,
