@@ -111,7 +111,7 @@ def profile_one(args, q, k, v, dev) -> int:
         g = np.random.default_rng(4242)
         q4, k4, v4 = (torch.from_numpy(g.standard_normal((256, 1024, D)).astype(np.float32)).to(dev)
                       for _ in range(3))
-        fn = bound.topk(q4, k4, v4, 2, key_chunk=256)
+        fn = bound.topk(q4, k4, v4, 2, key_chunk=0)
     else:  # zorder
         g = np.random.default_rng(4242 + 512)
         q5, k5, v5 = (torch.from_numpy(g.standard_normal((1024, 512, D)).astype(np.float32)).to(dev)
@@ -279,9 +279,14 @@ def main() -> int:
     g4 = np.random.default_rng(4242)
     q4, k4, v4 = (torch.from_numpy(g4.standard_normal((b4, n4, D)).astype(np.float32)).to(dev)
                   for _ in range(3))
+    from tarmac.kernels import streaming_topk_attention
     f4 = {"dense": lambda: fused_dense_attention(q4, k4, v4)}
     for kk in KS:
-        f4[f"stream_k{kk}"] = (lambda kk=kk: topk_attention(q4, k4, v4, kk, key_chunk=256))
+        # the API default key chunk (the largest that fits LDS), and the
+        # reference's 256-key tile
+        f4[f"stream_k{kk}"] = (lambda kk=kk: streaming_topk_attention(q4, k4, v4, kk))
+        f4[f"stream_k{kk}_chunk256"] = (lambda kk=kk: streaming_topk_attention(q4, k4, v4, kk,
+                                                                               block_n=256))
     s4 = {n: harness.stats(s) for n, s in
           harness.time_interleaved(harness.as_graphs(f4), args.reps, 5, 2).items()}
     detail["streaming_B256_N1024"] = {

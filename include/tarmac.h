@@ -65,8 +65,9 @@ int tarmac_topk_fused_fwd(const void* q, const void* k, const void* v, void* out
                           int B, int N, int d, int topk, int dtype, void* stream);
 
 /*
- * Streaming top-k: keys pass through LDS in chunks of key_chunk rows, so the
- * N-wide score row is never resident; no cap on N.
+ * Streaming top-k: keys pass through LDS in chunks of key_chunk rows (<= 0:
+ * the largest chunk the LDS budget holds), so the N-wide score row is never
+ * resident; no cap on N.
  * Replaces src/kernels/streaming_topk_attention.py:206-258
  * (streaming_topk_attention, including return_indices).
  */

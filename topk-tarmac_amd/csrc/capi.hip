@@ -127,8 +127,8 @@ int tarmac_topk_stream_fwd(const void* q, const void* k, const void* v, void* ou
                            int32_t* idx_out, int B, int N, int d, int topk, int dtype,
                            int key_chunk, void* stream) {
   const char* fn = "tarmac_topk_stream_fwd";
-  if (key_chunk <= 0) key_chunk = 256;
   const int kmax = max_topk_chunk(dtype, d);
+  if (key_chunk <= 0) key_chunk = kmax;
   if (key_chunk > kmax) key_chunk = kmax;
   return topk_common(q, k, v, out, idx_out, B, N, d, topk, dtype, key_chunk, stream, fn);
 }

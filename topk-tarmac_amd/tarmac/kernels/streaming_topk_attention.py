@@ -14,7 +14,9 @@ import torch
 
 from .fused_topk_attention import topk_attention
 
-DEFAULT_KEY_CHUNK = 256
+#: 0 = the largest chunk the LDS budget holds (the reference's ``tuned=True``
+#: picks its key tile per shape, ``:191-203``)
+DEFAULT_KEY_CHUNK = 0
 
 
 def streaming_topk_attention(q: torch.Tensor, k: torch.Tensor,
@@ -32,7 +34,8 @@ def streaming_topk_attention(q: torch.Tensor, k: torch.Tensor,
 
     With ``return_indices`` also returns the retained peer indices (B, N, k)
     int32, ordered by score (descending) then index. ``block_n`` is the number
-    of keys staged per LDS pass (rounded up to 16; default 256). ``block_m``,
+    of keys staged per LDS pass (rounded up to 16; default: the largest chunk
+    that fits LDS, e.g. 576 keys at d=16 fp32). ``block_m``,
     ``num_warps``, ``num_stages``, ``tuned``, ``bitonic`` and ``early_exit``
     select Triton tilings and merge schemes in the reference and are accepted
     for signature compatibility; the result does not depend on them there
@@ -45,4 +48,5 @@ def streaming_topk_attention(q: torch.Tensor, k: torch.Tensor,
     if precision != "ieee":
         raise ValueError(f"precision={precision!r}: gfx950 has no TF32 mode; use 'ieee'")
     chunk = DEFAULT_KEY_CHUNK if block_n is None else -(-int(block_n) // 16) * 16
+    chunk = chunk if chunk > 0 else 0
     return topk_attention(q, k, v, topk, return_indices=return_indices, key_chunk=chunk)
