@@ -119,6 +119,32 @@ int tarmac_morton_window(const float* pos, void* idx_out, int idx_dtype, int64_t
                          int B, int N, int k, int bits, void* stream);
 
 /*
+ * k nearest peers per agent over all pairs: select_radius_knn
+ * (src/kernels/prescore_selection.py:35-42). pos fp32 [B, N, 2] (8-byte
+ * aligned); idx_out [B, N, k], int32 or int64. Squared fp32 distances
+ * (dx*dx + dy*dy, each operation rounded); the k smallest by (distance, agent
+ * index), the self pair excluded; emitted in ascending agent index. Requires
+ * 1 <= k <= N-1 and N <= 8192.
+ */
+int tarmac_knn_radius(const float* pos, void* idx_out, int idx_dtype, int B, int N, int k,
+                      void* stream);
+
+/*
+ * k nearest peers among the 3x3 grid cells around each agent: select_grid_knn
+ * (src/kernels/prescore_selection.py:107-164), grid shape from grid_knn_shape
+ * (:87-101). Agents are ordered by cell (equal cells by agent index); each
+ * neighbour column contributes a run of at most 3M agents; the k smallest
+ * slots by (distance, slot) are kept, emitted in ascending slot. Routes to
+ * tarmac_knn_radius when 9M >= N, as the reference does. N <= 4096.
+ */
+int tarmac_knn_grid(const float* pos, void* idx_out, int idx_dtype, int B, int N, int k,
+                    void* stream);
+
+/* grid_knn_shape (src/kernels/prescore_selection.py:87-101): grid side G and
+ * per-cell capacity M for N agents and k peers. Host only. */
+int tarmac_grid_knn_shape(int N, int k, int* G, int* M);
+
+/*
  * Selector and attention in one launch: the zorder_k core of
  * src/agents/mappo.py:265-292 and the "select+attend" total of
  * scripts/bench_prescore.py:253-257. idx_out: int32 [B, N, topk], nullable.

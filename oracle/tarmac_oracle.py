@@ -34,6 +34,20 @@ morton_code                 bit-by-bit interleave loop; golden vectors written
 select_morton_window        golden vectors from the reference; k distinct
                             peers, never self; curve-neighbour sets
 prescore_attention          dense softmax restricted to the selected set
+pair_d2                     float64 distances: within one fp32 rounding chain
+                            (3 ulp) of (c-p).(c-p); exact on integer grids
+select_radius_knn           scipy cKDTree (float64 kNN, an independent
+                            implementation) on rows without near-ties;
+                            brute-force ties on integer lattices
+grid_knn_shape              the reference's own values (golden vectors)
+grid_cells                  through select_grid_knn's golden vectors
+select_grid_knn             golden vectors from the reference on rows whose
+                            runs were not cut and hold >= k candidates; equals
+                            select_radius_knn where the k-th neighbour lies
+                            inside the 3x3 block and no run was cut; the
+                            all-pairs route when 9M >= N. Parity unpinned on
+                            cut / short rows (the reference's unstable argsort
+                            and topk tie order decide them)
 ordered_key                 exhaustive order check on special values and
                             random fp32 pairs (a < b iff key(a) < key(b))
 masked_threshold_keep       bisect >= 32: exactly {j : s_j >= k-th largest}
@@ -255,6 +269,107 @@ def select_morton_window(pos: np.ndarray, k: int, bits: int = 10) -> np.ndarray:
     np.put_along_axis(rank, order, np.broadcast_to(np.arange(N), (B, N)), axis=-1)
     nr = (rank[..., None] + window_offsets(k)[None, None, :]) % N
     return np.take_along_axis(order, nr.reshape(B, N * k), axis=1).reshape(B, N, k)
+
+
+def pair_d2(pos: np.ndarray, cand_pos: np.ndarray) -> np.ndarray:
+    """Squared distance in fp32, ``(c - p)^2`` summed x then y.
+
+    The arithmetic of ``(pc - pos.unsqueeze(2)).square().sum(-1)`` in
+    ``src/kernels/prescore_selection.py:155-156``: each difference, each square
+    and the one addition rounded to fp32 (no fused multiply-add).
+    ``pos`` [..., 2] broadcasts against ``cand_pos`` [..., 2].
+    """
+    diff = (np.asarray(cand_pos, np.float32) - np.asarray(pos, np.float32)).astype(np.float32)
+    sq = (diff * diff).astype(np.float32)
+    return (sq[..., 0] + sq[..., 1]).astype(np.float32)
+
+
+def select_radius_knn(pos: np.ndarray, k: int) -> np.ndarray:
+    """k nearest peers per agent -- ``src/kernels/prescore_selection.py:35-42``.
+
+    All-pairs squared distances (:func:`pair_d2`), the self pair at +inf (the
+    reference's ``masked_fill`` of the identity), then the k smallest by
+    (distance, agent index). The reference ranks ``torch.cdist`` distances,
+    which for N > 25 come from ``|x|^2 + |y|^2 - 2 x.y``; that rounding is not
+    restated (it only moves near-ties), and ``topk(sorted=False)`` leaves the
+    order of the k open: here the k are returned nearest first.
+    Returns int64 ``[B, N, k]``.
+    """
+    pos = np.asarray(pos, np.float32)
+    B, N, _ = pos.shape
+    d2 = pair_d2(pos[:, :, None, :], pos[:, None, :, :])
+    d2[:, np.arange(N), np.arange(N)] = np.inf
+    return np.argsort(d2, axis=-1, kind="stable")[..., :k].astype(np.int64)
+
+
+def grid_knn_shape(N: int, k: int) -> tuple[int, int]:
+    """Grid side G and cell capacity M -- ``src/kernels/prescore_selection.py:87-101``:
+    about ``max(2, k)`` agents per cell, capacity mean + 3 sqrt(mean) + 2."""
+    occ = max(2, k)
+    G = max(1, int((N / occ) ** 0.5))
+    mean = N / (G * G)
+    return G, int(mean + 3 * mean ** 0.5 + 2)
+
+
+def grid_cells(pos: np.ndarray, G: int) -> np.ndarray:
+    """Cell coordinates ``[B, N, 2]`` -- ``prescore_selection.py:134-136``:
+    per-batch fp32 normalisation, ``* G``, truncation, clamp to ``[0, G-1]``."""
+    pos = np.asarray(pos, np.float32)
+    lo = pos.min(axis=1, keepdims=True)
+    span = np.maximum(pos.max(axis=1, keepdims=True) - lo, np.float32(1e-6))
+    c = ((pos - lo) / span * np.float32(G)).astype(np.int64)
+    return np.clip(c, 0, G - 1)
+
+
+def select_grid_knn(pos: np.ndarray, k: int, slot_order: bool = False) -> np.ndarray:
+    """k nearest peers among the 3x3 cells around each agent --
+    ``src/kernels/prescore_selection.py:107-164``.
+
+    Agents sorted by cell ``x*G + y`` (equal cells by agent index: the
+    reference's ``argsort`` is not stable); for each neighbour column
+    ``x-1..x+1`` a run of at most ``L = 3M`` sorted agents from cell
+    ``(x', max(y-1, 0))`` to the end of cell ``(x', min(y+1, G-1))``; slots
+    past the run, of a column outside the grid, or holding the agent itself
+    are at +inf. The k smallest slots by (distance, slot) are kept, so a
+    query with fewer than k valid candidates keeps the first invalid slots,
+    whose agents are what the reference's gather reads there. Falls back to
+    :func:`select_radius_knn` when ``3L >= N`` (``:127-128``).
+    Returns int64 ``[B, N, k]``, nearest first (in ascending slot with
+    ``slot_order``; ascending agent index on the all-pairs route).
+    """
+    pos = np.asarray(pos, np.float32)
+    B, N, _ = pos.shape
+    G, M = grid_knn_shape(N, k)
+    L = 3 * M
+    if 3 * L >= N:
+        out = select_radius_knn(pos, k)
+        return np.sort(out, -1) if slot_order else out
+    cxy = grid_cells(pos, G)
+    cell = cxy[..., 0] * G + cxy[..., 1]
+    order = np.argsort(cell, axis=1, kind="stable")
+    start = np.zeros((B, G * G + 1), np.int64)
+    for b in range(B):
+        start[b, 1:] = np.cumsum(np.bincount(cell[b], minlength=G * G))
+    x = cxy[..., 0][..., None] + np.arange(-1, 2)
+    y = cxy[..., 1][..., None]
+    ok_col = (x >= 0) & (x < G)
+    xc = np.clip(x, 0, G - 1)
+    c_lo = xc * G + np.maximum(y - 1, 0)
+    c_hi = xc * G + np.minimum(y + 1, G - 1) + 1
+    s_lo = np.take_along_axis(start, c_lo.reshape(B, -1), 1).reshape(B, N, 3)
+    s_hi = np.take_along_axis(start, c_hi.reshape(B, -1), 1).reshape(B, N, 3)
+    s_hi = np.minimum(s_hi, s_lo + L)
+    idx = s_lo[..., None] + np.arange(L)
+    valid = (idx < s_hi[..., None]) & ok_col[..., None]
+    cand = np.take_along_axis(order, np.minimum(idx, N - 1).reshape(B, -1), 1).reshape(B, N, 3 * L)
+    valid = valid.reshape(B, N, 3 * L) & (cand != np.arange(N)[None, :, None])
+    pc = np.take_along_axis(pos, cand.reshape(B, -1, 1), 1).reshape(B, N, 3 * L, 2)
+    d2 = pair_d2(pos[:, :, None, :], pc)
+    d2 = np.where(valid, d2, np.float32(np.inf))
+    j = np.argsort(d2, axis=-1, kind="stable")[..., :k]
+    if slot_order:
+        j = np.sort(j, -1)
+    return np.take_along_axis(cand, j, -1).astype(np.int64)
 
 
 def prescore_attention(q, k, v, idx):

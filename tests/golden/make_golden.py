@@ -15,7 +15,11 @@ outputs) in ``tests/golden/reference_vectors.npz``:
   rows with equal codes have no pinned order and are left out);
 * ``src/agents/mappo.py:332-420`` ``AttentionComm.forward`` for the hot-path
   modes, with its weights, so the module composition (qkv split order, gelu,
-  projection) is pinned as well as the core.
+  projection) is pinned as well as the core;
+* ``src/kernels/prescore_selection.py:87-163`` ``grid_knn_shape`` and
+  ``select_grid_knn`` -- the cell quantisation, the capacity cut and what a
+  query with fewer than k candidates keeps are fixed by that code alone
+  (stored as sorted index sets: ``topk(sorted=False)`` leaves the order open).
 """
 
 from __future__ import annotations
@@ -33,7 +37,7 @@ def main(ref_root: str) -> None:
     sys.path.insert(0, ref_root)
     from src.agents.mappo import AttentionComm, MAPPOConfig  # noqa: E402
     from src.kernels.prescore_selection import (  # noqa: E402
-        _morton_code, select_morton_window)
+        _morton_code, grid_knn_shape, select_grid_knn, select_morton_window)
 
     data: dict[str, np.ndarray] = {}
     g = torch.Generator().manual_seed(20240601)
@@ -96,6 +100,29 @@ def main(ref_root: str) -> None:
                         if wkey in data:
                             assert np.array_equal(data[wkey], p.numpy())
                         data[wkey] = p.numpy()
+
+    # -- grid kNN selector ----------------------------------------------------
+    shapes = [(N, k) for N in (6, 48, 96, 192, 384, 512, 1024) for k in (1, 2, 4, 8, 16) if k < N]
+    data["grid_shape"] = np.array([(N, k) + tuple(grid_knn_shape(N, k)) for N, k in shapes],
+                                  dtype=np.int64)
+    gg = torch.Generator().manual_seed(4242)
+    cluster = torch.rand(2, 512, 2, generator=gg)
+    cluster[:, :200] = 0.45 + 0.1 * cluster[:, :200]      # one crowded area: capacity cut
+    cluster[:, 200:203] = torch.tensor([[0.0, 0.0], [1.0, 1.0], [0.0, 1.0]])
+    sparse = torch.rand(2, 512, 2, generator=gg) ** 3     # empty corner: short candidate lists
+    grid_cases = {
+        "g96": (torch.rand(2, 96, 2, generator=gg), (2,)),
+        "g192": (torch.rand(2, 192, 2, generator=gg), (2, 4)),
+        "g512": (torch.rand(2, 512, 2, generator=gg) * 2 - 1, (2, 4, 8, 16)),
+        "gclus": (cluster, (2, 4, 8)),
+        "gsparse": (sparse, (2, 4)),
+    }
+    for name, (pos, ks) in grid_cases.items():
+        pos = pos.float().contiguous()
+        data[f"{name}_pos"] = pos.numpy()
+        for k in ks:
+            idx = select_grid_knn(pos, k).sort(-1).values
+            data[f"{name}_grid{k}"] = idx.numpy().astype(np.int16)
 
     np.savez_compressed(OUT, **data)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes, {len(data)} arrays)")

@@ -135,3 +135,33 @@ def test_filter_mode_switch():
         assert lib.tarmac_set_topk_filter(1) == 0
     finally:
         lib.tarmac_set_topk_filter(prev)
+
+
+def test_grid_knn_shape_matches_the_reference_formula():
+    """tarmac_grid_knn_shape (host only) against the oracle's restatement of
+    grid_knn_shape (pinned to the reference's values) over a wide range."""
+    import tarmac_oracle as O
+    from tarmac.kernels import grid_knn_shape
+    for N in list(range(2, 600)) + [1000, 1023, 1024, 2047, 2048, 4095, 4096, 8192]:
+        for kk in (1, 2, 3, 4, 5, 7, 8, 9, 15, 16, 17, 31, 32, 64):
+            if kk < N:
+                assert grid_knn_shape(N, kk) == O.grid_knn_shape(N, kk), (N, kk)
+
+
+def test_knn_validation():
+    from tarmac import _lib
+    L = _lib.LIB
+    assert L.tarmac_knn_radius(None, _fake(), 1, 1, 8, 2, None) == 1
+    assert "null" in _lib.last_error()
+    assert L.tarmac_knn_radius(_fake(260), _fake(), 1, 1, 8, 2, None) == 1
+    assert "aligned" in _lib.last_error()
+    assert L.tarmac_knn_grid(_fake(), _fake(), 1, 1, 8, 8, None) == 1
+    assert "k <= N-1" in _lib.last_error()
+    assert L.tarmac_knn_grid(_fake(), _fake(), 3, 1, 8, 2, None) == 1
+    assert "idx dtype" in _lib.last_error()
+    assert L.tarmac_knn_radius(_fake(), _fake(), 1, 1, 9000, 2, None) == 2
+    assert "capacity" in _lib.last_error()
+    assert L.tarmac_knn_grid(_fake(), _fake(), 1, 1, 5000, 2, None) == 2
+    assert "capacity" in _lib.last_error()
+    G, M = ctypes.c_int(), ctypes.c_int()
+    assert L.tarmac_grid_knn_shape(0, 2, ctypes.byref(G), ctypes.byref(M)) == 1

@@ -391,6 +391,148 @@ def test_bf16_round_matches_torch():
 # planted mistakes: the pins must reject these mutants
 # ---------------------------------------------------------------------------
 
+# ---------------------------------------------------------------------------
+# kNN selectors
+# ---------------------------------------------------------------------------
+
+def _lattice(B, side, rng):
+    """Agents on an integer lattice (shuffled): many exactly equal distances."""
+    g = np.stack(np.meshgrid(np.arange(side), np.arange(side), indexing="ij"), -1).reshape(-1, 2)
+    return np.stack([g[rng.permutation(len(g))] for _ in range(B)]).astype(np.float32)
+
+
+def pin_pair_d2(fn) -> bool:
+    rng = np.random.default_rng(5)
+    p = rng.random((64, 2)).astype(np.float32)
+    c = (rng.random((64, 2)) * 3 - 1).astype(np.float32)
+    got = fn(p, c).astype(F64)
+    ref = ((c.astype(F64) - p.astype(F64)) ** 2).sum(-1)
+    ok = np.allclose(got, ref, rtol=4 * 2.0 ** -24, atol=0)
+    li = _lattice(1, 5, rng)[0]
+    ok &= np.array_equal(fn(li[:1], li), ((li - li[:1]) ** 2).sum(-1))
+    # bit for bit: torch's fp32 evaluation of the reference expression
+    # (pc - pos).square().sum(-1), prescore_selection.py:155-156
+    pt = (torch.from_numpy(c) - torch.from_numpy(p)).square().sum(-1).numpy()
+    ok &= np.array_equal(fn(p, c), pt)
+    return bool(ok)
+
+
+def pin_radius_knn(fn) -> bool:
+    """Against scipy's cKDTree (float64) on rows with no near-tie at the k-th
+    neighbour, and against brute force (index tie rule) on lattices."""
+    from scipy.spatial import cKDTree
+    rng = np.random.default_rng(11)
+    ok = True
+    for N, kk in ((7, 1), (7, 6), (48, 4), (96, 16), (300, 9)):
+        pos = (rng.random((3, N, 2)) * 2 - 1).astype(np.float32)
+        got = np.sort(fn(pos, kk), -1)
+        for b in range(3):
+            dist, ii = cKDTree(pos[b].astype(F64)).query(pos[b].astype(F64), kk + 2)
+            # drop the self pair, keep rows where the k-th and (k+1)-th differ clearly
+            for i in range(N):
+                row = [(d, j) for d, j in zip(dist[i], ii[i]) if j != i][: kk + 1]
+                if len(row) == kk + 1 and row[kk][0] - row[kk - 1][0] <= 1e-5 * (1 + row[kk][0]):
+                    continue
+                ok &= np.array_equal(got[b, i], np.sort([j for _, j in row[:kk]]))
+    lat = _lattice(2, 6, rng)
+    got = fn(lat, 5)
+    for b in range(2):
+        for i in range(36):
+            d = ((lat[b] - lat[b, i]) ** 2).sum(-1).astype(F64)
+            d[i] = np.inf
+            want = sorted(range(36), key=lambda j: (d[j], j))[:5]
+            ok &= sorted(got[b, i].tolist()) == sorted(want)
+    return bool(ok)
+
+
+def pin_grid_knn(fn, golden) -> bool:
+    """The reference's own outputs on rows whose runs were not cut and hold at
+    least k candidates; on other rows the unstable argsort / topk decide."""
+    checked = 0
+    ok = True
+    for name in ("g96", "g192", "g512", "gclus", "gsparse"):
+        pos = golden[f"{name}_pos"]
+        for key in [f for f in golden.files if f.startswith(name + "_grid")]:
+            kk = int(key[len(name) + 5:])
+            cut, short = _grid_row_flags(pos, kk)
+            got = np.sort(fn(pos, kk), -1)
+            ref = golden[key].astype(np.int64)
+            use = ~cut & ~short
+            ok &= np.array_equal(got[use], ref[use])
+            checked += int(use.sum())
+    return bool(ok) and checked > 3000
+
+
+def _grid_row_flags(pos, kk):
+    """(a run was cut at capacity, fewer than k candidates) per query."""
+    B, N, _ = pos.shape
+    G, M = O.grid_knn_shape(N, kk)
+    L = 3 * M
+    cxy = O.grid_cells(pos, G)
+    cell = cxy[..., 0] * G + cxy[..., 1]
+    start = np.zeros((B, G * G + 1), np.int64)
+    for b in range(B):
+        start[b, 1:] = np.cumsum(np.bincount(cell[b], minlength=G * G))
+    x = cxy[..., 0][..., None] + np.arange(-1, 2)
+    y = cxy[..., 1][..., None]
+    okc = (x >= 0) & (x < G)
+    xc = np.clip(x, 0, G - 1)
+    s_lo = np.take_along_axis(start, (xc * G + np.maximum(y - 1, 0)).reshape(B, -1), 1).reshape(B, N, 3)
+    s_hi = np.take_along_axis(start, (xc * G + np.minimum(y + 1, G - 1) + 1).reshape(B, -1), 1).reshape(B, N, 3)
+    cut = ((s_hi - s_lo > L) & okc).any(-1)
+    short = (np.minimum(s_hi - s_lo, L) * okc).sum(-1) - 1 < kk
+    return cut, short
+
+
+def test_pair_d2_pinned():
+    assert pin_pair_d2(O.pair_d2)
+
+
+def test_radius_knn_pinned():
+    assert pin_radius_knn(O.select_radius_knn)
+
+
+def test_grid_knn_shape_golden(golden):
+    for N, kk, G, M in golden["grid_shape"]:
+        assert O.grid_knn_shape(int(N), int(kk)) == (G, M)
+
+
+def test_grid_knn_pinned(golden):
+    assert pin_grid_knn(O.select_grid_knn, golden)
+
+
+@pytest.mark.parametrize("N,kk", [(96, 2), (512, 4), (512, 16)])
+def test_grid_knn_equals_radius_where_exact(N, kk):
+    """The reference's exactness condition: the k-th neighbour no farther
+    than the nearest edge of the 3x3 block, and no run cut."""
+    rng = np.random.default_rng(N + kk)
+    pos = rng.random((3, N, 2)).astype(np.float32)
+    grid = np.sort(O.select_grid_knn(pos, kk), -1)
+    rad = O.select_radius_knn(pos, kk)
+    G, M = O.grid_knn_shape(N, kk)
+    lo = pos.min(1, keepdims=True)
+    span = np.maximum(pos.max(1, keepdims=True) - lo, np.float32(1e-6))
+    u = ((pos - lo) / span * G).astype(F64)             # position in cell units
+    c = np.clip(np.floor(u), 0, G - 1)
+    # distance (cell units) to the nearest block edge that is not the grid border
+    edge = np.minimum(np.where(c > 0, u - (c - 1), np.inf), np.where(c < G - 1, c + 2 - u, np.inf)).min(-1)
+    kth = np.sqrt(O.pair_d2(pos, np.take_along_axis(pos, rad[..., -1:].repeat(2, -1), 1)))
+    kth_cells = kth * G / span.min(-1)
+    cut, short = _grid_row_flags(pos, kk)
+    safe = (kth_cells < edge * 0.999) & ~cut & ~short
+    assert safe.mean() > 0.5
+    assert np.array_equal(grid[safe], np.sort(rad, -1)[safe])
+
+
+def test_grid_knn_all_pairs_route():
+    """9M >= N: the reference calls select_radius_knn (:127-128)."""
+    rng = np.random.default_rng(2)
+    pos = rng.random((2, 48, 2)).astype(np.float32)
+    G, M = O.grid_knn_shape(48, 4)
+    assert 9 * M >= 48
+    assert np.array_equal(O.select_grid_knn(pos, 4), O.select_radius_knn(pos, 4))
+
+
 def test_pins_reject_planted_mistakes(golden):
     def scores_mul_sqrt(q, k):         # multiplies by sqrt(d) instead of dividing
         s = O.scores(q, k)
@@ -470,3 +612,39 @@ def test_pins_reject_planted_mistakes(golden):
         return O.topk_indices(s, topk)
 
     assert not pin_sort_select(sort_low_index)
+
+    # kNN: fused multiply-add in the distance; largest instead of smallest;
+    # self pair not excluded; cell rounding instead of truncation
+    def d2_fma(p, c):                   # x*x + (y*y) with one rounding (contracted)
+        diff = (np.asarray(c, np.float32) - np.asarray(p, np.float32)).astype(F64)
+        yy = (diff[..., 1] * diff[..., 1]).astype(np.float32).astype(F64)
+        return (diff[..., 0] * diff[..., 0] + yy).astype(np.float32)
+
+    assert not pin_pair_d2(d2_fma)
+
+    def radius_farthest(pos, kk):
+        d2 = O.pair_d2(pos[:, :, None, :], pos[:, None, :, :])
+        d2[:, np.arange(pos.shape[1]), np.arange(pos.shape[1])] = -np.inf
+        return np.argsort(-d2, -1, kind="stable")[..., :kk]
+
+    def radius_with_self(pos, kk):
+        d2 = O.pair_d2(pos[:, :, None, :], pos[:, None, :, :])
+        return np.argsort(d2, -1, kind="stable")[..., :kk]
+
+    def radius_high_index_ties(pos, kk):
+        n = pos.shape[1]
+        return n - 1 - O.select_radius_knn(pos[:, ::-1].copy(), kk)
+
+    assert not pin_radius_knn(radius_farthest)
+    assert not pin_radius_knn(radius_with_self)
+    assert not pin_radius_knn(radius_high_index_ties)
+
+    real_cells = O.grid_cells
+    try:
+        O.grid_cells = lambda pos, G: np.clip(np.rint(
+            (pos - pos.min(1, keepdims=True)) / np.maximum(
+                pos.max(1, keepdims=True) - pos.min(1, keepdims=True), np.float32(1e-6))
+            * np.float32(G)).astype(np.int64), 0, G - 1)
+        assert not pin_grid_knn(O.select_grid_knn, golden)
+    finally:
+        O.grid_cells = real_cells

@@ -196,6 +196,58 @@ int tarmac_morton_window(const float* pos, void* idx_out, int idx_dtype, int64_t
   return hip_status(tarmac::run_morton_window(a), fn);
 }
 
+namespace {
+
+int knn_common(const float* pos, void* idx_out, int idx_dtype, int B, int N, int k, int grid,
+               void* stream, const char* fn) {
+  if (!pos || !idx_out) return fail(TARMAC_ERR_INVALID, "%s: null pos or idx_out", fn);
+  if (!aligned(pos, 8)) return fail(TARMAC_ERR_INVALID, "%s: pos must be 8-byte aligned", fn);
+  if (B < 1 || N < 2) return fail(TARMAC_ERR_INVALID, "%s: need B >= 1 and N >= 2", fn);
+  if (k < 1 || k > N - 1)
+    return fail(TARMAC_ERR_INVALID, "%s: need 1 <= k <= N-1 (got k=%d, N=%d)", fn, k, N);
+  if (idx_dtype != TARMAC_IDX_I32 && idx_dtype != TARMAC_IDX_I64)
+    return fail(TARMAC_ERR_INVALID, "%s: unknown idx dtype %d", fn, idx_dtype);
+  if (!aligned(idx_out, idx_dtype == TARMAC_IDX_I64 ? 8 : 4))
+    return fail(TARMAC_ERR_INVALID, "%s: idx_out misaligned", fn);
+  if (static_cast<long long>(B) * N * k >= (1ll << 40))
+    return fail(TARMAC_ERR_UNSUPPORTED, "%s: tensor too large", fn);
+  tarmac::KnnArgs a{pos, idx_out, idx_dtype == TARMAC_IDX_I64, B, N, k, 0, 0, 0, stream};
+  if (grid) {
+    int G = 0, M = 0;
+    tarmac::grid_knn_shape(N, k, &G, &M);
+    // the reference's own route: all pairs when the 3x3 block would hold N or more
+    if (9ll * M < N) {
+      a.grid = 1;
+      a.G = G;
+      a.L = 3 * M;
+      if (tarmac::knn_grid_lds_bytes(N, G, tarmac::knn_grid_threads(N)) > kLdsBudget)
+        return fail(TARMAC_ERR_UNSUPPORTED, "%s: N=%d exceeds the per-row grid capacity", fn, N);
+    }
+  }
+  if (!a.grid && tarmac::knn_radius_lds_bytes(N) > kLdsBudget)
+    return fail(TARMAC_ERR_UNSUPPORTED, "%s: N=%d exceeds the per-row position capacity", fn, N);
+  return hip_status(tarmac::run_knn(a), fn);
+}
+
+}  // namespace
+
+int tarmac_knn_radius(const float* pos, void* idx_out, int idx_dtype, int B, int N, int k,
+                      void* stream) {
+  return knn_common(pos, idx_out, idx_dtype, B, N, k, 0, stream, "tarmac_knn_radius");
+}
+
+int tarmac_knn_grid(const float* pos, void* idx_out, int idx_dtype, int B, int N, int k,
+                    void* stream) {
+  return knn_common(pos, idx_out, idx_dtype, B, N, k, 1, stream, "tarmac_knn_grid");
+}
+
+int tarmac_grid_knn_shape(int N, int k, int* G, int* M) {
+  if (!G || !M) return fail(TARMAC_ERR_INVALID, "tarmac_grid_knn_shape: null output");
+  if (N < 1 || k < 1) return fail(TARMAC_ERR_INVALID, "tarmac_grid_knn_shape: need N >= 1, k >= 1");
+  tarmac::grid_knn_shape(N, k, G, M);
+  return ok();
+}
+
 int tarmac_zorder_fwd(const void* q, const void* k, const void* v, const float* pos, void* out,
                       int32_t* idx_out, int B, int N, int d, int topk, int bits, int dtype,
                       void* stream) {

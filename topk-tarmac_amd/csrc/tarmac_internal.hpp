@@ -110,6 +110,16 @@ struct ZorderArgs {
   void* stream;
 };
 
+struct KnnArgs {
+  const float* pos;   // [B, N, 2]
+  void* idx;          // [B, N, k]
+  int idx_is_i64;
+  int B, N, k;
+  int grid;           // 0: all pairs; 1: 3x3 grid cells
+  int G, L;           // grid side and run capacity (3 * cell capacity)
+  void* stream;
+};
+
 hipError_t run_topk(const TopkArgs& a);
 hipError_t run_topk_filter(const TopkArgs& a);
 bool topk_filter_supported(int dtype, int d, int topk);
@@ -123,10 +133,15 @@ hipError_t run_zorder(const ZorderArgs& a);
 hipError_t run_noop(float* out, void* stream);
 hipError_t run_fixedset_bwd(const FixedsetBwdArgs& a);
 hipError_t run_dense_bwd(const DenseBwdArgs& a);
+hipError_t run_knn(const KnnArgs& a);
+void grid_knn_shape(int N, int k, int* G, int* M);
+int knn_grid_threads(int N);
 
 size_t topk_lds_bytes(int dtype, int d, int kc);
 size_t topk_filter_lds_bytes(int d, int kc);
 size_t dense_lds_bytes(int dtype, int d, int kc);
 size_t zorder_lds_bytes(int N);
+size_t knn_radius_lds_bytes(int N);
+size_t knn_grid_lds_bytes(int N, int G, int threads);
 
 }  // namespace tarmac

@@ -42,6 +42,9 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tarmac_zorder_fwd": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
     "tarmac_fixedset_bwd": ([_P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I, _P], _I),
     "tarmac_dense_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P], _I),
+    "tarmac_knn_radius": ([_P, _P, _I, _I, _I, _I, _P], _I),
+    "tarmac_knn_grid": ([_P, _P, _I, _I, _I, _I, _P], _I),
+    "tarmac_grid_knn_shape": ([_I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)], _I),
     "tarmac_set_topk_filter": ([_I], _I),
     "tarmac_noop": ([_P, _P], _I),
 }

@@ -7,8 +7,9 @@ from .fused_topk_attention import (fused_topk_attention, fused_topk_attention_ma
                                    fused_topk_attention_sort, fused_topk_attention_tiled,
                                    reference_topk_attention, topk_attention,
                                    topk_variant_attention)
-from .prescore_selection import (_morton_code, prescore_attention, select_morton_window,
-                                 zorder_attention)
+from .prescore_selection import (SELECTORS, _morton_code, grid_knn_recall, grid_knn_shape,
+                                 prescore_attention, prescore_full, select_grid_knn,
+                                 select_morton_window, select_radius_knn, zorder_attention)
 from .streaming_topk_attention import streaming_topk_attention
 
 __all__ = [
@@ -16,6 +17,7 @@ __all__ = [
     "fused_dense_attention", "fused_prescore_attention", "fused_topk_attention",
     "fused_topk_attention_masked", "fused_topk_attention_sort", "fused_topk_attention_tiled",
     "reference_topk_attention", "topk_attention", "topk_variant_attention",
-    "prescore_attention", "select_morton_window",
+    "prescore_attention", "prescore_full", "select_morton_window", "select_radius_knn",
+    "select_grid_knn", "grid_knn_shape", "grid_knn_recall", "SELECTORS",
     "zorder_attention", "streaming_topk_attention", "_morton_code",
 ]
