@@ -13,7 +13,8 @@ Alongside, with the reference's protocol (interleaved event timing and graph
 replay, minimum over samples): the dense core, top-k at k=1/2/4, the fixed-set
 kernel given the exact top-k set (selection-time share), the streaming kernel
 at B=256 N=1024, the Z-order select+attend at B=1024 N=512 k=2
-(configs[4]), a bf16 point and the launch floor.
+(configs[4]), a bf16 point, the configs[1] sweep over N, the
+pre-score selectors (radius / grid kNN, Morton window) and the launch floor.
 
 Prints ONE JSON line. Exits non-zero (with a message) for --gpus > 1: this
 build measures one GPU.
@@ -154,7 +155,7 @@ def main() -> int:
 
     from tarmac import bound, harness
     from tarmac.kernels import fused_dense_attention, fused_prescore_attention, topk_attention
-    from tarmac.kernels import zorder_attention
+    from tarmac.kernels import SELECTORS, zorder_attention
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     dev = torch.device("cuda:0")
@@ -314,6 +315,26 @@ def main() -> int:
                           / (tz * 1e-6) / harness.PEAK_HBM_BYTES_PER_S, 4)}
     del q5, k5t, v5, pos5, f5
 
+    # ---- pre-score selectors (scripts/bench_prescore.py: B=256, d=16) -------
+    sel_rows = {}
+    for n6 in (192, 512):
+        g6 = np.random.default_rng(4242 + n6)
+        q6, k6, v6 = (torch.from_numpy(g6.standard_normal((256, n6, D)).astype(np.float32)).to(dev)
+                      for _ in range(3))
+        pos6 = torch.from_numpy(g6.random((256, n6, 2)).astype(np.float32)).to(dev)
+        for kk in (4, 16):
+            f6 = {}
+            for nm, sel in SELECTORS.items():
+                f6[f"sel:{nm}"] = (lambda sel=sel, kk=kk: sel(pos6, kk))
+                f6[f"total:{nm}"] = (lambda sel=sel, kk=kk:
+                                     fused_prescore_attention(q6, k6, v6, sel(pos6, kk)))
+            s6 = {n: harness.stats(s) for n, s in
+                  harness.time_interleaved(harness.as_graphs(f6), max(20, args.reps // 2), 5,
+                                           2).items()}
+            sel_rows[f"N{n6}_k{kk}"] = {n: round(s["min_us"], 3) for n, s in s6.items()}
+        del q6, k6, v6, pos6
+    detail["prescore_selectors_B256_d16_us"] = sel_rows
+
     # ---- one bf16 point, B=1024, N=256, d=16 -------------------
     qb, kb, vb = (t.to(torch.bfloat16) for t in (q, k, v))
     f3 = {"dense_bf16": lambda: fused_dense_attention(qb, kb, vb)}
@@ -430,6 +451,28 @@ def main() -> int:
                           "graph_us": {k_: round(v_, 3) for k_, v_ in sg.items()},
                           "launches_per_call": 1}
     detail["small_n_B1024_d16"] = small
+
+    # ---- configs[1] sweep: B=1024, d=16, N in {32..512}, k in {1,2,4} ------
+    sweep = {}
+    for n in (32, 64, 128, 256, 384, 512):
+        gs = np.random.default_rng(1234 + 7 * n + D)
+        qs, ks, vs = (torch.from_numpy(gs.standard_normal((B, n, D)).astype(np.float32)).to(dev)
+                      for _ in range(3))
+        fs = {"dense": bound.dense(qs, ks, vs)}
+        for kk in KS:
+            fs[f"topk_k{kk}"] = bound.topk(qs, ks, vs, kk)
+        se = {nm: harness.stats(sm)["min_us"] for nm, sm in
+              harness.time_interleaved(fs, max(20, args.reps // 2), 5, 2).items()}
+        row = {nm: round(t, 3) for nm, t in se.items()}
+        for kk in KS:
+            row[f"ratio_k{kk}"] = round(se[f"topk_k{kk}"] / se["dense"], 4)
+        row["dense_hbm_frac"] = round(harness.analytic_bytes("dense", B, n, D) / (se["dense"] * 1e-6)
+                                      / harness.PEAK_HBM_BYTES_PER_S, 4)
+        row["dense_mfma_frac"] = round(harness.analytic_flops("dense", B, n, D) / (se["dense"] * 1e-6)
+                                       / harness.PEAK_FP32_FLOPS, 4)
+        sweep[f"N{n}"] = row
+        del qs, ks, vs, fs
+    detail["sweep_B1024_d16_us"] = sweep
 
     line["detail"] = detail
     line["device"] = torch.cuda.get_device_name(dev)
