@@ -168,14 +168,26 @@ int tarmac_fixedset_bwd(const float* q, const float* k, const float* v, const fl
                         int B, int N, int d, void* stream);
 
 /*
+ * tarmac_dense_fwd for training (fp32, default key chunk): also writes the
+ * queries' log2-domain logsumexp into plane 0 of stats ([B, 2, N] floats),
+ * for tarmac_dense_bwd with stats_ready = 1. No kernel counterpart in the
+ * reference (its dense kernel is forward-only).
+ */
+int tarmac_dense_fwd_stats(const float* q, const float* k, const float* v, float* out,
+                           float* stats, int B, int N, int d, void* stream);
+
+/*
  * Backward of dense attention (fp32, self pair excluded): dq, dk, dv are
- * written. stats: caller-provided workspace of 2 * B * N floats (per query
- * logsumexp and dO.O). No kernel counterpart in the reference; replaces
- * autograd through src/agents/mappo.py:361-372 in training.
+ * written. stats: workspace of 2 * B * N floats, [B, 2, N]: plane 0 the
+ * queries' log2-domain logsumexp (taken as given when stats_ready = 1, i.e.
+ * written by tarmac_dense_fwd_stats on the same inputs; computed here when
+ * 0), plane 1 their dO.O (always computed here). No kernel counterpart in
+ * the reference; replaces autograd through src/agents/mappo.py:361-372 in
+ * training.
  */
 int tarmac_dense_bwd(const float* q, const float* k, const float* v, const float* out,
-                     const float* dout, float* dq, float* dk, float* dv, float* stats, int B, int N,
-                     int d, void* stream);
+                     const float* dout, float* dq, float* dk, float* dv, float* stats,
+                     int stats_ready, int B, int N, int d, void* stream);
 
 /*
  * fp32 top-k (d = 16, 32, 64; topk <= 8) can score all pairs on split-bf16

@@ -198,135 +198,316 @@ fixedset_bwd_lds_kernel(const float* __restrict__ Q, const float* __restrict__ K
 // ---------------------------------------------------------------------------
 // dense
 // ---------------------------------------------------------------------------
+//
+// P = softmax(scale * Q K^T) (self pair excluded), dP = dO V^T,
+// dS = P * (dP - rowsum(dO * O)), dQ = scale * dS K, dK = scale * dS^T Q,
+// dV = P^T dO, on fp32 MFMA in two passes:
+//   pass 1 (per query tile, keys streamed): S^T tiles as in the forward kernel
+//     (lane l: query l%16, keys 4*(l/16)+r), a first sweep for the row's
+//     log2-domain logsumexp, a second for dQ^T += K^T dS^T, whose B operand
+//     is each lane's own dS (contraction slot j of step u = key 4j+u);
+//   pass 2 (per key tile, queries streamed): S tiles (lane l: key l%16,
+//     queries 4*(l/16)+r), so dV^T += dO^T P and dK^T += Q^T dS take P and
+//     dS as B operands from the lane's own registers in the same way.
+// Pass 1 writes the per-query statistics pass 2 needs into the workspace:
+// stats[b][0][i] = log2-domain logsumexp of the scaled scores,
+// stats[b][1][i] = dO_i . O_i.
 
-// rows of the other side staged per LDS pass (two padded row arrays <= 48 KiB)
 template <int D>
-constexpr int bwd_chunk() { return D <= 16 ? 256 : (D <= 32 ? 128 : 64); }
+constexpr int bwd_block_tiles() { return D <= 32 ? 4 : 2; }
 
-// Pass 1: one quad per query; K and V of the batch row stream through LDS.
-template <int D>
-__global__ void __launch_bounds__(256)
-dense_bwd_q_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
-                   const float* __restrict__ V, const float* __restrict__ O,
-                   const float* __restrict__ dO, float* __restrict__ dQ,
-                   float* __restrict__ stats, int N, int n_qblk, float scale) {
-  constexpr int E = D / 4;
-  constexpr int LD = D + 4;  // padded LDS row (floats)
-  constexpr int kBwdChunk = bwd_chunk<D>();
-  __shared__ __align__(16) float Ks[kBwdChunk * LD];
-  __shared__ __align__(16) float Vs[kBwdChunk * LD];
-  const int b = blockIdx.x / n_qblk, qb = blockIdx.x - b * n_qblk;
-  const int sub = threadIdx.x & 3;
-  const int i_raw = qb * (blockDim.x >> 2) + (threadIdx.x >> 2);
-  const bool live = i_raw < N;
-  const int i = live ? i_raw : N - 1;
-  const size_t boff = static_cast<size_t>(b) * N * D;
-  const size_t roff = boff + static_cast<size_t>(i) * D + sub * E;
-  float q[E], g[E], o[E];
-  ld_f32<E>(q, Q + roff);
-  ld_f32<E>(g, dO + roff);
-  ld_f32<E>(o, O + roff);
-  const float Dq = quad_dot<E>(g, o);
-
-  float m = -INFINITY, l = 0.f;
-  float dq[E];
+// A^T-operand product: acc[h] (16 output channels x 16 columns) +=
+// Xt[16h + col][c0 + 4*grp + u] * w[u] over u, Xt transposed in LDS.
+template <int NX, int NH>
+__device__ __forceinline__ void mma_t(f32x4 (&acc)[NX][NH], const float* Xt, int ldt, int c0,
+                                      int lane, const float (&w)[NX][4]) {
+  const int col = lane & 15, grp = lane >> 4;
 #pragma unroll
-  for (int c = 0; c < E; ++c) dq[c] = 0.f;
-  // two sweeps over the key chunks: statistics, then gradients
-  for (int sweep = 0; sweep < 2; ++sweep) {
-    for (int c0 = 0; c0 < N; c0 += kBwdChunk) {
-      const int cn = min(kBwdChunk, N - c0);
-      __syncthreads();
-      stage_rows<float, D, LD>(Ks, Kx + boff + static_cast<size_t>(c0) * D, cn, cn);
-      if (sweep == 1) stage_rows<float, D, LD>(Vs, V + boff + static_cast<size_t>(c0) * D, cn, cn);
-      __syncthreads();
-      for (int jj = 0; jj < cn; ++jj) {
-        const int j = c0 + jj;
-        float kr[E];
-        ld_f32<E>(kr, Ks + jj * LD + sub * E);
-        const float s = quad_dot<E>(q, kr) * scale;
-        if (sweep == 0) {
-          if (j != i) {
-            const float m_new = fmaxf(m, s);
-            l = l * (m == -INFINITY ? 0.f : expf(m - m_new)) + expf(s - m_new);
-            m = m_new;
-          }
-        } else {
-          float vr[E];
-          ld_f32<E>(vr, Vs + jj * LD + sub * E);
-          const float p = j == i ? 0.f : expf(s - m) / l;
-          const float ds = p * (quad_dot<E>(g, vr) - Dq);
+  for (int h = 0; h < NH; ++h) {
+    const f32x4 xv = *reinterpret_cast<const f32x4*>(Xt + (16 * h + col) * ldt + c0 + 4 * grp);
 #pragma unroll
-          for (int c = 0; c < E; ++c) dq[c] = fmaf(ds, kr[c], dq[c]);
-        }
-      }
-    }
-  }
-  if (!live) return;
+    for (int u = 0; u < 4; ++u)
 #pragma unroll
-  for (int c = 0; c < E; ++c) dq[c] *= scale;
-  st_f32<E>(dQ + roff, dq);
-  if (sub == 0) {
-    float* st = stats + (static_cast<size_t>(b) * N + i) * 2;
-    st[0] = m + logf(l);
-    st[1] = Dq;
+      for (int x = 0; x < NX; ++x) acc[x][h] = mfma_f32_16x16x4(xv[u], w[x][u], acc[x][h]);
   }
 }
 
-// Pass 2: one quad per key; Q, dO and the query statistics stream through LDS.
-template <int D>
+template <int D, int QT>
 __global__ void __launch_bounds__(256)
-dense_bwd_kv_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
-                    const float* __restrict__ V, const float* __restrict__ dO,
-                    const float* __restrict__ stats, float* __restrict__ dK,
-                    float* __restrict__ dV, int N, int n_kblk, float scale) {
-  constexpr int E = D / 4;
-  constexpr int LD = D + 4;
-  constexpr int kBwdChunk = bwd_chunk<D>();
-  __shared__ __align__(16) float Qs[kBwdChunk * LD];
-  __shared__ __align__(16) float Gs[kBwdChunk * LD];
-  __shared__ __align__(16) float Ss[kBwdChunk * 2];
-  const int b = blockIdx.x / n_kblk, kb = blockIdx.x - b * n_kblk;
-  const int sub = threadIdx.x & 3;
-  const int j_raw = kb * (blockDim.x >> 2) + (threadIdx.x >> 2);
-  const bool live = j_raw < N;
-  const int j = live ? j_raw : N - 1;
+dense_bwd_dq_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
+                    const float* __restrict__ V, const float* __restrict__ O,
+                    const float* __restrict__ dO, float* __restrict__ dQ,
+                    float* __restrict__ stats, int have_lse, int N, int n_qblk, int kc,
+                    float scale, int nblocks) {
+  using F = Frag<float, D>;
+  constexpr int E = D / 4, LDK = F::LDK, NH = (D + 15) / 16, CP = 16 * NH;
+  constexpr int BT = bwd_block_tiles<D>(), BK = 16 * BT;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int kcp = (kc + BK - 1) / BK * BK, ldt = kcp + 4;
+  float* Ks = reinterpret_cast<float*>(smem_raw);
+  float* Vs = Ks + static_cast<size_t>(kcp) * LDK;
+  float* Kt = Vs + static_cast<size_t>(kcp) * LDK;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int blk = xcd_logical_block(blockIdx.x, nblocks);
+  const int b = blk / n_qblk, qblk = blk - b * n_qblk;
+  const int q0 = (qblk * nw + wave) * 16 * QT;
+  const int col = lane & 15, grp = lane >> 4;
   const size_t boff = static_cast<size_t>(b) * N * D;
-  const size_t roff = boff + static_cast<size_t>(j) * D + sub * E;
-  float kr[E], vr[E];
-  ld_f32<E>(kr, Kx + roff);
-  ld_f32<E>(vr, V + roff);
-  float dk[E], dv[E];
+  const float c2 = scale * kLog2eF;
+
+  F fq[QT], fg[QT];
+  float Di[QT];
 #pragma unroll
-  for (int c = 0; c < E; ++c) dk[c] = dv[c] = 0.f;
-  for (int c0 = 0; c0 < N; c0 += kBwdChunk) {
-    const int cn = min(kBwdChunk, N - c0);
-    __syncthreads();
-    stage_rows<float, D, LD>(Qs, Q + boff + static_cast<size_t>(c0) * D, cn, cn);
-    stage_rows<float, D, LD>(Gs, dO + boff + static_cast<size_t>(c0) * D, cn, cn);
-    for (int t = threadIdx.x; t < 2 * cn; t += blockDim.x)
-      Ss[t] = stats[(static_cast<size_t>(b) * N + c0) * 2 + t];
-    __syncthreads();
-    for (int ii = 0; ii < cn; ++ii) {
-      const int i = c0 + ii;
-      float q[E], g[E];
-      ld_f32<E>(q, Qs + ii * LD + sub * E);
-      ld_f32<E>(g, Gs + ii * LD + sub * E);
-      const float s = quad_dot<E>(q, kr) * scale;
-      const float p = i == j ? 0.f : expf(s - Ss[2 * ii]);
-      const float ds = p * (quad_dot<E>(g, vr) - Ss[2 * ii + 1]);
+  for (int qt = 0; qt < QT; ++qt) {
+    const size_t row = boff + static_cast<size_t>(min(q0 + 16 * qt + col, N - 1)) * D;
+    fq[qt].load_q(Q + row, grp, c2);
+    fg[qt].load_q(dO + row, grp, 1.f);
+    float o[E];
+    ld_f32<E>(o, O + row + grp * E);
+    float dd = 0.f;
 #pragma unroll
-      for (int c = 0; c < E; ++c) {
-        dv[c] = fmaf(p, g[c], dv[c]);
-        dk[c] = fmaf(ds, q[c], dk[c]);
+    for (int e = 0; e < E; ++e) dd = fmaf(fg[qt].q[e], o[e], dd);
+    dd += __shfl_xor(dd, 16);
+    dd += __shfl_xor(dd, 32);
+    Di[qt] = dd;
+  }
+
+  // sweep 1 (unless the forward saved it): per-lane running max / sum of
+  // 2^s, then combined per query into the log2-domain logsumexp
+  const bool single = N <= kc && !have_lse;  // sweep 1 stages everything once
+  float lse[QT];
+  if (have_lse) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+      lse[qt] = stats[static_cast<size_t>(b) * 2 * N + min(q0 + 16 * qt + col, N - 1)];
+  } else {
+    float m[QT], l[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) { m[qt] = -INFINITY; l[qt] = 0.f; }
+    for (int c0 = 0; c0 < N; c0 += kc) {
+      const int cn = min(kc, N - c0), cnp = (cn + BK - 1) / BK * BK;
+      __syncthreads();
+      stage_rows<float, D, LDK>(Ks, Kx + boff + static_cast<size_t>(c0) * D, cn, cnp);
+      if (single) {
+        stage_rows<float, D, LDK>(Vs, V + boff + static_cast<size_t>(c0) * D, cn, cnp);
+        stage_vt<float, D, CP>(Kt, ldt, Kx + boff + static_cast<size_t>(c0) * D, cn, cnp);
+      }
+      __syncthreads();
+      if (q0 >= N) continue;
+      for (int kb0 = 0; kb0 < cnp; kb0 += BK) {
+        f32x4 st[QT][BT];
+        block_scores<F, QT, BT>(fq, Ks, kb0, LDK, lane, st);
+        const int kabs = c0 + kb0;
+        const bool edge = (q0 < kabs + BK && kabs < q0 + 16 * QT) || kabs + BK > c0 + cn;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          float s[BT][4];
+          float mloc = -INFINITY;
+#pragma unroll
+          for (int t = 0; t < BT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int key = kabs + 16 * t + 4 * grp + r;
+              s[t][r] = (edge && (key >= c0 + cn || key == q0 + 16 * qt + col)) ? -INFINITY
+                                                                                  : st[qt][t][r];
+              mloc = fmaxf(mloc, s[t][r]);
+            }
+          const float m_new = fmaxf(m[qt], mloc);
+          if (m_new != -INFINITY) {
+            float acc = l[qt] * fast_exp2(m[qt] - m_new);
+#pragma unroll
+            for (int t = 0; t < BT; ++t)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc += fast_exp2(s[t][r] - m_new);
+            l[qt] = acc;
+            m[qt] = m_new;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float mm = fmaxf(m[qt], __shfl_xor(m[qt], 16));
+      mm = fmaxf(mm, __shfl_xor(mm, 32));
+      float ll = (m[qt] == -INFINITY) ? 0.f : l[qt] * fast_exp2(m[qt] - mm);
+      ll += __shfl_xor(ll, 16);
+      ll += __shfl_xor(ll, 32);
+      lse[qt] = mm + log2f(ll);
+    }
+  }
+
+  // sweep 2: dQ^T += K^T dS^T
+  f32x4 acc[QT][NH];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int h = 0; h < NH; ++h) acc[qt][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < N; c0 += kc) {
+    const int cn = min(kc, N - c0), cnp = (cn + BK - 1) / BK * BK;
+    if (!single) {
+      __syncthreads();
+      stage_rows<float, D, LDK>(Ks, Kx + boff + static_cast<size_t>(c0) * D, cn, cnp);
+      stage_rows<float, D, LDK>(Vs, V + boff + static_cast<size_t>(c0) * D, cn, cnp);
+      stage_vt<float, D, CP>(Kt, ldt, Kx + boff + static_cast<size_t>(c0) * D, cn, cnp);
+      __syncthreads();
+    }
+    if (q0 >= N) continue;
+    for (int kb0 = 0; kb0 < cnp; kb0 += BK) {
+      f32x4 st[QT][BT], dp[QT][BT];
+      block_scores<F, QT, BT>(fq, Ks, kb0, LDK, lane, st);
+      block_scores<F, QT, BT>(fg, Vs, kb0, LDK, lane, dp);
+      const int kabs = c0 + kb0;
+      const bool edge = (q0 < kabs + BK && kabs < q0 + 16 * QT) || kabs + BK > c0 + cn;
+#pragma unroll
+      for (int t = 0; t < BT; ++t) {
+        float ds[QT][4];
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = kabs + 16 * t + 4 * grp + r;
+            float p = fast_exp2(st[qt][t][r] - lse[qt]);
+            if (edge && (key >= c0 + cn || key == q0 + 16 * qt + col)) p = 0.f;
+            ds[qt][r] = p * (dp[qt][t][r] - Di[qt]);
+          }
+        mma_t<QT, NH>(acc, Kt, ldt, kb0 + 16 * t, lane, ds);
       }
     }
   }
-  if (!live) return;
+  if (q0 >= N) return;
 #pragma unroll
-  for (int c = 0; c < E; ++c) dk[c] *= scale;
-  st_f32<E>(dK + roff, dk);
-  st_f32<E>(dV + roff, dv);
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qi = q0 + 16 * qt + col;
+    if (qi >= N) continue;
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      const int cbase = 16 * h + 4 * grp;
+      if (cbase < D) {
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = acc[qt][h][r] * scale;
+        st_f32<4>(dQ + boff + static_cast<size_t>(qi) * D + cbase, o);
+      }
+    }
+    if (grp == 0) {
+      if (!have_lse) stats[static_cast<size_t>(b) * 2 * N + qi] = lse[qt];
+      stats[static_cast<size_t>(b) * 2 * N + N + qi] = Di[qt];
+    }
+  }
+}
+
+template <int D, int KT>
+__global__ void __launch_bounds__(256)
+dense_bwd_dkv_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
+                     const float* __restrict__ V, const float* __restrict__ dO,
+                     const float* __restrict__ stats, float* __restrict__ dK,
+                     float* __restrict__ dV, int N, int n_kblk, int qc, float scale,
+                     int nblocks) {
+  using F = Frag<float, D>;
+  constexpr int LDK = F::LDK, NH = (D + 15) / 16, CP = 16 * NH;
+  constexpr int BT = bwd_block_tiles<D>(), BQ = 16 * BT;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int qcp = (qc + BQ - 1) / BQ * BQ, ldt = qcp + 4;
+  float* Qs = reinterpret_cast<float*>(smem_raw);
+  float* Gs = Qs + static_cast<size_t>(qcp) * LDK;
+  float* Qt = Gs + static_cast<size_t>(qcp) * LDK;
+  float* Gt = Qt + static_cast<size_t>(CP) * ldt;
+  float* Ls = Gt + static_cast<size_t>(CP) * ldt;
+  float* Ds = Ls + qcp;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int blk = xcd_logical_block(blockIdx.x, nblocks);
+  const int b = blk / n_kblk, kblk = blk - b * n_kblk;
+  const int k0 = (kblk * nw + wave) * 16 * KT;
+  const int col = lane & 15, grp = lane >> 4;
+  const size_t boff = static_cast<size_t>(b) * N * D;
+  const float* st_b = stats + static_cast<size_t>(b) * 2 * N;
+
+  F fk[KT], fv[KT];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+    const size_t row = boff + static_cast<size_t>(min(k0 + 16 * kt + col, N - 1)) * D;
+    fk[kt].load_q(Kx + row, grp, scale * kLog2eF);
+    fv[kt].load_q(V + row, grp, 1.f);
+  }
+  f32x4 dk[KT][NH], dv[KT][NH];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+    for (int h = 0; h < NH; ++h) dk[kt][h] = dv[kt][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int c0 = 0; c0 < N; c0 += qc) {
+    const int cn = min(qc, N - c0), cnp = (cn + BQ - 1) / BQ * BQ;
+    __syncthreads();
+    stage_rows<float, D, LDK>(Qs, Q + boff + static_cast<size_t>(c0) * D, cn, cnp);
+    stage_rows<float, D, LDK>(Gs, dO + boff + static_cast<size_t>(c0) * D, cn, cnp);
+    stage_vt<float, D, CP>(Qt, ldt, Q + boff + static_cast<size_t>(c0) * D, cn, cnp);
+    stage_vt<float, D, CP>(Gt, ldt, dO + boff + static_cast<size_t>(c0) * D, cn, cnp);
+    for (int t = threadIdx.x; t < cnp; t += blockDim.x) {
+      Ls[t] = t < cn ? st_b[c0 + t] : INFINITY;  // padded queries: p = 0
+      Ds[t] = t < cn ? st_b[N + c0 + t] : 0.f;
+    }
+    __syncthreads();
+    if (k0 >= N) continue;
+    for (int qb0 = 0; qb0 < cnp; qb0 += BQ) {
+      f32x4 s[KT][BT], dp[KT][BT];
+      block_scores<F, KT, BT>(fk, Qs, qb0, LDK, lane, s);   // S: query 4*grp+r, key col
+      block_scores<F, KT, BT>(fv, Gs, qb0, LDK, lane, dp);
+      const int qabs = c0 + qb0;
+      const bool diag = k0 < qabs + BQ && qabs < k0 + 16 * KT;  // wave-uniform
+#pragma unroll
+      for (int t = 0; t < BT; ++t) {
+        const int qrow = qb0 + 16 * t + 4 * grp;
+        const f32x4 lse = *reinterpret_cast<const f32x4*>(Ls + qrow);
+        const f32x4 dd = *reinterpret_cast<const f32x4*>(Ds + qrow);
+        float p[KT][4], ds[KT][4];
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            p[kt][r] = fast_exp2(s[kt][t][r] - lse[r]);
+            if (diag && c0 + qrow + r == k0 + 16 * kt + col) p[kt][r] = 0.f;
+            ds[kt][r] = p[kt][r] * (dp[kt][t][r] - dd[r]);
+          }
+        mma_t<KT, NH>(dv, Gt, ldt, qb0 + 16 * t, lane, p);
+        mma_t<KT, NH>(dk, Qt, ldt, qb0 + 16 * t, lane, ds);
+      }
+    }
+  }
+  if (k0 >= N) return;
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+    const int kj = k0 + 16 * kt + col;
+    if (kj >= N) continue;
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      const int cbase = 16 * h + 4 * grp;
+      if (cbase < D) {
+        float a[4], v4[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          a[r] = dk[kt][h][r] * scale;
+          v4[r] = dv[kt][h][r];
+        }
+        st_f32<4>(dK + boff + static_cast<size_t>(kj) * D + cbase, a);
+        st_f32<4>(dV + boff + static_cast<size_t>(kj) * D + cbase, v4);
+      }
+    }
+  }
+}
+
+// LDS bytes of the two passes for a chunk of `c` rows.
+template <int D>
+constexpr size_t dq_lds_bytes(int c) {
+  constexpr int CP = 16 * ((D + 15) / 16);
+  return (static_cast<size_t>(c) * 2 * (D + 4) + static_cast<size_t>(CP) * (c + 4)) * 4;
+}
+template <int D>
+constexpr size_t dkv_lds_bytes(int c) {
+  constexpr int CP = 16 * ((D + 15) / 16);
+  return (static_cast<size_t>(c) * 2 * (D + 4) + static_cast<size_t>(2) * CP * (c + 4) +
+          static_cast<size_t>(2) * c) * 4;
 }
 
 // ---------------------------------------------------------------------------
@@ -375,15 +556,30 @@ hipError_t run_fixedset_bwd(const FixedsetBwdArgs& a) {
 
 template <int D>
 static hipError_t launch_dense_bwd(const DenseBwdArgs& a) {
-  const int per = 256 / 4;  // queries (keys) per workgroup
+  constexpr int T = 2;                              // 16-row tiles per wavefront
+  constexpr int BQ = 16 * bwd_block_tiles<D>();
+  const int waves = (a.N + 16 * T - 1) / (16 * T);
+  const int nw = waves >= 4 ? 4 : waves;
+  const int per = 16 * T * nw;
   const int nblk = (a.N + per - 1) / per;
+  const int nblocks = a.B * nblk;
+  // largest chunk (multiple of the block) within the LDS budget, capped at N
+  const int npad = (a.N + BQ - 1) / BQ * BQ;
+  int kc = BQ, qc = BQ;
+  while (kc + BQ <= npad && dq_lds_bytes<D>(kc + BQ) <= kBwdLdsBudget) kc += BQ;
+  while (qc + BQ <= npad && dkv_lds_bytes<D>(qc + BQ) <= kBwdLdsBudget) qc += BQ;
+  if (kc >= a.N) kc = a.N;
+  if (qc >= a.N) qc = a.N;
   hipStream_t st = static_cast<hipStream_t>(a.stream);
-  hipLaunchKernelGGL((dense_bwd_q_kernel<D>), dim3(a.B * nblk), dim3(256), 0, st, a.q, a.k, a.v,
-                     a.out, a.dout, a.dq, a.stats, a.N, nblk, a.scale);
+  const size_t lds_q = dq_lds_bytes<D>((kc + BQ - 1) / BQ * BQ);
+  const size_t lds_kv = dkv_lds_bytes<D>((qc + BQ - 1) / BQ * BQ);
+  hipLaunchKernelGGL((dense_bwd_dq_kernel<D, T>), dim3(nblocks), dim3(64 * nw), lds_q, st, a.q,
+                     a.k, a.v, a.out, a.dout, a.dq, a.stats, a.stats_ready, a.N, nblk, kc, a.scale,
+                     nblocks);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((dense_bwd_kv_kernel<D>), dim3(a.B * nblk), dim3(256), 0, st, a.q, a.k, a.v,
-                     a.dout, a.stats, a.dk, a.dv, a.N, nblk, a.scale);
+  hipLaunchKernelGGL((dense_bwd_dkv_kernel<D, T>), dim3(nblocks), dim3(64 * nw), lds_kv, st, a.q,
+                     a.k, a.v, a.dout, a.stats, a.dk, a.dv, a.N, nblk, qc, a.scale, nblocks);
   return hipGetLastError();
 }
 

@@ -100,9 +100,10 @@ int tarmac_abi_version(void) { return 1; }
 
 const char* tarmac_last_error(void) { return g_last_error.c_str(); }
 
-int tarmac_dense_fwd(const void* q, const void* k, const void* v, void* out, int B, int N, int d,
-                     int dtype, int key_chunk, void* stream) {
-  const char* fn = "tarmac_dense_fwd";
+namespace {
+
+int dense_common(const void* q, const void* k, const void* v, void* out, float* stats, int B,
+                 int N, int d, int dtype, int key_chunk, void* stream, const char* fn) {
   int rc = check_core(q, k, v, out, B, N, d, dtype, fn);
   if (rc) return rc;
   int kc = key_chunk;
@@ -114,8 +115,23 @@ int tarmac_dense_fwd(const void* q, const void* k, const void* v, void* out, int
   }
   if (tarmac::dense_lds_bytes(dtype, d, kc) > kLdsBudget)
     return fail(TARMAC_ERR_UNSUPPORTED, "%s: key_chunk %d exceeds the LDS budget at d=%d", fn, kc, d);
-  tarmac::DenseArgs a{q, k, v, out, B, N, d, dtype, kc, inv_sqrt(d), stream};
+  tarmac::DenseArgs a{q, k, v, out, B, N, d, dtype, kc, inv_sqrt(d), stream, stats};
   return hip_status(tarmac::run_dense(a), fn);
+}
+
+}  // namespace
+
+int tarmac_dense_fwd(const void* q, const void* k, const void* v, void* out, int B, int N, int d,
+                     int dtype, int key_chunk, void* stream) {
+  return dense_common(q, k, v, out, nullptr, B, N, d, dtype, key_chunk, stream,
+                      "tarmac_dense_fwd");
+}
+
+int tarmac_dense_fwd_stats(const float* q, const float* k, const float* v, float* out,
+                           float* stats, int B, int N, int d, void* stream) {
+  const char* fn = "tarmac_dense_fwd_stats";
+  if (!stats || !aligned(stats, 8)) return fail(TARMAC_ERR_INVALID, "%s: stats null or misaligned", fn);
+  return dense_common(q, k, v, out, stats, B, N, d, TARMAC_DTYPE_F32, 0, stream, fn);
 }
 
 int tarmac_topk_fused_fwd(const void* q, const void* k, const void* v, void* out, int32_t* idx_out,
@@ -283,8 +299,8 @@ int tarmac_fixedset_bwd(const float* q, const float* k, const float* v, const fl
 }
 
 int tarmac_dense_bwd(const float* q, const float* k, const float* v, const float* out,
-                     const float* dout, float* dq, float* dk, float* dv, float* stats, int B, int N,
-                     int d, void* stream) {
+                     const float* dout, float* dq, float* dk, float* dv, float* stats,
+                     int stats_ready, int B, int N, int d, void* stream) {
   const char* fn = "tarmac_dense_bwd";
   int rc = check_core(q, k, v, out, B, N, d, TARMAC_DTYPE_F32, fn);
   if (rc) return rc;
@@ -292,7 +308,10 @@ int tarmac_dense_bwd(const float* q, const float* k, const float* v, const float
   if (!aligned(dout, 16) || !aligned(dq, 16) || !aligned(dk, 16) || !aligned(dv, 16) ||
       !aligned(stats, 8))
     return fail(TARMAC_ERR_INVALID, "%s: misaligned buffer", fn);
-  tarmac::DenseBwdArgs a{q, k, v, out, dout, dq, dk, dv, stats, B, N, d, inv_sqrt(d), stream};
+  if (stats_ready != 0 && stats_ready != 1)
+    return fail(TARMAC_ERR_INVALID, "%s: stats_ready must be 0 or 1", fn);
+  tarmac::DenseBwdArgs a{q, k, v, out, dout, dq, dk, dv, stats, stats_ready, B, N, d,
+                         inv_sqrt(d), stream};
   return hip_status(tarmac::run_dense_bwd(a), fn);
 }
 

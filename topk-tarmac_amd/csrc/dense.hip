@@ -71,46 +71,11 @@ struct PvOperand<bf16, D> {
   }
 };
 
-// Stage V[rows, D] transposed into Vt[c][key] (row stride ldv), zero-filling
-// keys [rows, rows_pad) and channels [D, CP).
-template <typename T, int D, int CP>
-__device__ __forceinline__ void stage_vt(T* Vt, int ldv, const T* src, int rows, int rows_pad) {
-  constexpr int VE = 16 / sizeof(T);
-  constexpr int VPR = D / VE;
-  constexpr int U = kStageBatch;
-  const int total = rows_pad * VPR;
-  for (int v0 = threadIdx.x; v0 < total; v0 += U * blockDim.x) {
-    uint4 raw[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int v = v0 + u * blockDim.x, row = v / VPR, cv = v - row * VPR;
-      raw[u] = make_uint4(0u, 0u, 0u, 0u);
-      if (v < total && row < rows)
-        raw[u] = *reinterpret_cast<const uint4*>(src + static_cast<size_t>(row) * D + cv * VE);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int v = v0 + u * blockDim.x, row = v / VPR, cv = v - row * VPR;
-      if (v >= total) break;
-      T x[VE];
-      __builtin_memcpy(x, &raw[u], 16);
-#pragma unroll
-      for (int e = 0; e < VE; ++e) Vt[(cv * VE + e) * ldv + row] = x[e];
-    }
-  }
-  if constexpr (CP > D) {
-    const int pad = (CP - D) * rows_pad;
-    for (int v = threadIdx.x; v < pad; v += blockDim.x) {
-      const int c = D + v / rows_pad, row = v % rows_pad;
-      Vt[c * ldv + row] = T(0);
-    }
-  }
-}
-
 template <typename T, int D, int QT>
 __global__ void __launch_bounds__(256)
 dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
-             T* __restrict__ O, int N, int n_qblk, int kc, float scale, int nblocks) {
+             T* __restrict__ O, float* __restrict__ lse, int N, int n_qblk, int kc, float scale,
+             int nblocks) {
   using F = Frag<T, D>;
   using PV = PvOperand<T, D>;
   constexpr int LDK = F::LDK;
@@ -221,6 +186,9 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
     l_tot += __shfl_xor(l_tot, 32);
     const int qi = q0 + 16 * qt + col;
     if (qi >= N) continue;
+    // log2-domain logsumexp of the scaled scores, for the backward pass
+    if (lse != nullptr && grp == 0)
+      lse[static_cast<size_t>(b) * 2 * N + qi] = m_run[qt] + log2f(l_tot);
     // lane l holds O^T[c = 16h + 4*(l/16) + r][q = l%16]
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
@@ -248,7 +216,7 @@ static hipError_t launch_dense(const DenseArgs& a) {
   hipLaunchKernelGGL((dense_kernel<T, D, QT>), dim3(nblocks), dim3(64 * nw), lds,
                      static_cast<hipStream_t>(a.stream), static_cast<const T*>(a.q),
                      static_cast<const T*>(a.k), static_cast<const T*>(a.v), static_cast<T*>(a.out),
-                     a.N, n_qblk, a.key_chunk, a.scale, nblocks);
+                     a.stats, a.N, n_qblk, a.key_chunk, a.scale, nblocks);
   return hipGetLastError();
 }
 

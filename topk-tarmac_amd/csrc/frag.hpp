@@ -284,4 +284,40 @@ __device__ __forceinline__ void stage_rows(T* lds, const T* src, int rows, int r
   }
 }
 
+// Stage V[rows, D] transposed into Vt[c][key] (row stride ldv), zero-filling
+// keys [rows, rows_pad) and channels [D, CP).
+template <typename T, int D, int CP>
+__device__ __forceinline__ void stage_vt(T* Vt, int ldv, const T* src, int rows, int rows_pad) {
+  constexpr int VE = 16 / sizeof(T);
+  constexpr int VPR = D / VE;
+  constexpr int U = kStageBatch;
+  const int total = rows_pad * VPR;
+  for (int v0 = threadIdx.x; v0 < total; v0 += U * blockDim.x) {
+    uint4 raw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int v = v0 + u * blockDim.x, row = v / VPR, cv = v - row * VPR;
+      raw[u] = make_uint4(0u, 0u, 0u, 0u);
+      if (v < total && row < rows)
+        raw[u] = *reinterpret_cast<const uint4*>(src + static_cast<size_t>(row) * D + cv * VE);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int v = v0 + u * blockDim.x, row = v / VPR, cv = v - row * VPR;
+      if (v >= total) break;
+      T x[VE];
+      __builtin_memcpy(x, &raw[u], 16);
+#pragma unroll
+      for (int e = 0; e < VE; ++e) Vt[(cv * VE + e) * ldv + row] = x[e];
+    }
+  }
+  if constexpr (CP > D) {
+    const int pad = (CP - D) * rows_pad;
+    for (int v = threadIdx.x; v < pad; v += blockDim.x) {
+      const int c = D + v / rows_pad, row = v % rows_pad;
+      Vt[c * ldv + row] = T(0);
+    }
+  }
+}
+
 }  // namespace tarmac

@@ -45,6 +45,7 @@ struct DenseArgs {
   int key_chunk;
   float scale;
   void* stream;
+  float* stats = nullptr;  // nullable: [B, 2, N] workspace, plane 0 gets the logsumexp
 };
 
 struct FixedsetArgs {
@@ -83,7 +84,8 @@ struct DenseBwdArgs {
   float* dq;
   float* dk;
   float* dv;
-  float* stats;     // workspace [B, N, 2]: logsumexp and dO.O per query
+  float* stats;     // workspace [B, 2, N]: logsumexp and dO.O per query
+  int stats_ready;  // plane 0 already holds the forward's logsumexp
   int B, N, d;
   float scale;
   void* stream;

@@ -39,7 +39,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ..kernels.backward import dense_attention_backward, fixedset_attention_backward
+from ..kernels.backward import (dense_attention_backward, dense_attention_forward_stats,
+                                fixedset_attention_backward)
 from ..kernels.fused_dense_attention import fused_dense_attention
 from ..kernels.fused_topk_attention import topk_attention
 from ..kernels.prescore_selection import zorder_attention
@@ -78,14 +79,17 @@ class _DenseCore(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v):
-        out = fused_dense_attention(q, k, v)
-        ctx.save_for_backward(q, k, v, out)
+        if q.dtype == torch.float32:
+            out, stats = dense_attention_forward_stats(q, k, v)
+        else:  # the backward raises for bf16; nothing to keep
+            out, stats = fused_dense_attention(q, k, v), None
+        ctx.save_for_backward(q, k, v, out, stats)
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        q, k, v, out = ctx.saved_tensors
-        return dense_attention_backward(q, k, v, out, dout)
+        q, k, v, out, stats = ctx.saved_tensors
+        return dense_attention_backward(q, k, v, out, dout, stats)
 
 
 class _SetCore(torch.autograd.Function):

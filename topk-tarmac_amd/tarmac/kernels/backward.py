@@ -53,10 +53,29 @@ def fixedset_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tenso
     return dq, dk, dv
 
 
+def dense_attention_forward_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+    """Dense attention (fp32) that also returns the per-query statistics its
+    backward needs: ``(out, stats)``, stats ``[B, 2, N]`` with plane 0 the
+    log2-domain logsumexp of the scaled scores."""
+    q, k, v = _launch.core(q, k, v)
+    _f32(q)
+    B, N, d = q.shape
+    out = torch.empty_like(q)
+    stats = torch.empty(B, 2, N, device=q.device, dtype=torch.float32)
+    with torch.cuda.device(q.device):
+        _lib.check(_lib.LIB.tarmac_dense_fwd_stats(
+            _launch.ptr(q), _launch.ptr(k), _launch.ptr(v), _launch.ptr(out), _launch.ptr(stats),
+            B, N, d, _launch.stream(q)))
+    return out, stats
+
+
 def dense_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                             out: torch.Tensor, dout: torch.Tensor):
+                             out: torch.Tensor, dout: torch.Tensor,
+                             stats: torch.Tensor | None = None):
     """Gradients (dq, dk, dv) of dense attention with the self pair excluded,
-    given its forward output ``out``."""
+    given its forward output ``out`` (and, optionally, the ``stats`` returned
+    with it by :func:`dense_attention_forward_stats`, which saves recomputing
+    the logsumexp)."""
     q, k, v = _launch.core(q, k, v)
     _f32(q, out, dout)
     out, dout = out.contiguous(), dout.contiguous()
@@ -64,11 +83,16 @@ def dense_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         raise ValueError("out and dout must match q's shape")
     B, N, d = q.shape
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    stats = torch.empty(B, N, 2, device=q.device, dtype=torch.float32)
+    ready = stats is not None
+    if ready:
+        if stats.shape != (B, 2, N) or stats.dtype != torch.float32 or not stats.is_contiguous():
+            raise ValueError("stats must be the contiguous fp32 [B, 2, N] tensor of the forward")
+    else:
+        stats = torch.empty(B, 2, N, device=q.device, dtype=torch.float32)
     with torch.cuda.device(q.device):
         rc = _lib.LIB.tarmac_dense_bwd(
             _launch.ptr(q), _launch.ptr(k), _launch.ptr(v), _launch.ptr(out), _launch.ptr(dout),
-            _launch.ptr(dq), _launch.ptr(dk), _launch.ptr(dv), _launch.ptr(stats), B, N, d,
-            _launch.stream(q))
+            _launch.ptr(dq), _launch.ptr(dk), _launch.ptr(dv), _launch.ptr(stats), int(ready),
+            B, N, d, _launch.stream(q))
         _lib.check(rc)
     return dq, dk, dv
