@@ -25,6 +25,8 @@
 // Pass 1 (per query, quad of lanes) forms the row statistics, dQ, and stores
 // (logsumexp_i, D_i); pass 2 (per key) forms dK and dV from them. The other
 // side's rows stream through LDS in chunks.
+#include <algorithm>
+
 #include "frag.hpp"
 #include "tarmac_internal.hpp"
 
@@ -33,11 +35,6 @@ namespace tarmac {
 namespace {
 
 // quad dot: lane (l % 4) holds E of the d channels; the sum lands in all four
-__device__ __forceinline__ float quad_sum(float x) {
-  x += __shfl_xor(x, 1);
-  return x + __shfl_xor(x, 2);
-}
-
 template <int E>
 __device__ __forceinline__ float quad_dot(const float (&a)[E], const float (&b)[E]) {
   float s = 0.f;
@@ -60,18 +57,19 @@ __device__ __forceinline__ void atomic_add_row(float* dst, const float (&x)[E], 
 
 // One query (a quad of lanes): dq is written; the dk / dv rows of its peers
 // receive atomic adds (global memory or LDS). Peers are taken U at a time
-// with all their index, K and V loads in flight together; when the set fits
-// one batch (kk <= U) the second pass reuses the rows from registers.
+// with their index, K and V loads in flight together; when the set fits one
+// batch (kk <= U) the second pass reuses the rows from registers. Kb / Vb are the batch row's keys and values, in LDS
+// or global memory.
 template <int D, typename I>
 __device__ __forceinline__ void fixedset_bwd_row(const float* __restrict__ qrow,
                                                  const float* __restrict__ grow,
-                                                 const float* __restrict__ Kb,
-                                                 const float* __restrict__ Vb,
+                                                 const float* Kb, const float* Vb,
                                                  const I* __restrict__ ir, float* __restrict__ dqrow,
                                                  float* dK, float* dV, int N, int kk, float scale,
                                                  int sub) {
   constexpr int E = D / 4;
-  constexpr int U = E <= 4 ? 8 : (E <= 8 ? 4 : 2);
+  constexpr int U = E <= 4 ? 8 : (E <= 8 ? 4 : 1);  // within 128 VGPRs at 1024 threads
+  const float c2 = scale * kLog2eF;  // scores in the exp2 domain
   float q[E], g[E];
   ld_f32<E>(q, qrow + sub * E);
   ld_f32<E>(g, grow + sub * E);
@@ -79,10 +77,7 @@ __device__ __forceinline__ void fixedset_bwd_row(const float* __restrict__ qrow,
   float kr[U][E], vr[U][E], sc[U], dw[U];
   auto load_batch = [&](int j0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const bool live = j0 + u < kk;
-      p[u] = live ? static_cast<int>(ir[j0 + u]) : 0;
-    }
+    for (int u = 0; u < U; ++u) p[u] = j0 + u < kk ? static_cast<int>(ir[j0 + u]) : 0;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int pc = min(max(p[u], 0), N - 1);
@@ -91,7 +86,7 @@ __device__ __forceinline__ void fixedset_bwd_row(const float* __restrict__ qrow,
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      sc[u] = j0 + u < kk ? quad_dot<E>(q, kr[u]) * scale : -INFINITY;
+      sc[u] = j0 + u < kk ? quad_dot<E>(q, kr[u]) * c2 : -INFINITY;
       dw[u] = quad_dot<E>(g, vr[u]);
     }
   };
@@ -107,12 +102,12 @@ __device__ __forceinline__ void fixedset_bwd_row(const float* __restrict__ qrow,
       bad |= j0 + u < kk && ((p[u] < 0) | (p[u] >= N));
       mb = fmaxf(mb, sc[u]);
     }
-    const float alpha = m == -INFINITY ? 0.f : expf(m - mb);
+    const float alpha = m == -INFINITY ? 0.f : fast_exp2(m - mb);
     l *= alpha;
     a *= alpha;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const float e = sc[u] == -INFINITY ? 0.f : expf(sc[u] - mb);
+      const float e = fast_exp2(sc[u] - mb);  // 0 for the -inf padding
       l += e;
       a = fmaf(e, dw[u], a);
     }
@@ -130,7 +125,7 @@ __device__ __forceinline__ void fixedset_bwd_row(const float* __restrict__ qrow,
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (j0 + u >= kk) continue;
-      const float w = expf(sc[u] - m) * inv_l;
+      const float w = fast_exp2(sc[u] - m) * inv_l;
       const float ds = w * (dw[u] - Dq);
 #pragma unroll
       for (int c = 0; c < E; ++c) dq[c] = fmaf(ds, kr[u][c], dq[c]);
@@ -145,8 +140,8 @@ __device__ __forceinline__ void fixedset_bwd_row(const float* __restrict__ qrow,
   st_f32<E>(dqrow + sub * E, dq);
 }
 
-// Global accumulation: one quad per query over the whole grid; dK, dV must
-// be zero on entry.
+// Global accumulation: one quad per query over the whole grid; dK, dV are
+// zeroed by zero_fill_kernel first.
 template <int D, typename I>
 __global__ void __launch_bounds__(256)
 fixedset_bwd_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
@@ -163,35 +158,60 @@ fixedset_bwd_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
                          threadIdx.x & 3);
 }
 
-// LDS accumulation: one workgroup (256 query quads) per batch row sums dK and dV for its N keys
-// in LDS (fast atomics, no zeroing pass), then adds them to dK, dV once.
-template <int D, typename I>
+__global__ void __launch_bounds__(256) zero_fill_kernel(float4* __restrict__ a, float4* __restrict__ b,
+                                                        long n4) {
+  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (long t = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; t < n4;
+       t += static_cast<long>(gridDim.x) * blockDim.x) {
+    a[t] = z;
+    b[t] = z;
+  }
+}
+
+// LDS accumulation: one workgroup (256 query quads) per batch row sums dK
+// and dV for its N keys in LDS and writes them once. With STAGE, the row's K
+// and V are staged in LDS too, so the peer gathers are LDS reads.
+template <int D, typename I, bool STAGE>
 __global__ void __launch_bounds__(1024)
 fixedset_bwd_lds_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
                         const float* __restrict__ V, const float* __restrict__ dO,
                         const I* __restrict__ Idx, float* __restrict__ dQ,
                         float* __restrict__ dK, float* __restrict__ dV, int N, int kk,
                         float scale) {
-  extern __shared__ __align__(16) float acc[];  // dK rows then dV rows, N * D each
+  extern __shared__ __align__(16) float acc[];  // dK, dV rows (then K, V rows), N * D each
   const int b = blockIdx.x;
   const size_t boff = static_cast<size_t>(b) * N * D;
+  const int nd = N * D;
   float* dKs = acc;
-  float* dVs = acc + static_cast<size_t>(N) * D;
-  for (int t = threadIdx.x; t < 2 * N * D; t += blockDim.x) acc[t] = 0.f;
+  float* dVs = acc + nd;
+  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int t = threadIdx.x; t < nd / 2; t += blockDim.x) reinterpret_cast<float4*>(acc)[t] = z;
+  const float* Kb = Kx + boff;
+  const float* Vb = V + boff;
+  if constexpr (STAGE) {
+    float* Ks = acc + 2 * nd;
+    float* Vs = Ks + nd;
+    for (int t = threadIdx.x; t < nd / 4; t += blockDim.x) {
+      reinterpret_cast<float4*>(Ks)[t] = reinterpret_cast<const float4*>(Kb)[t];
+      reinterpret_cast<float4*>(Vs)[t] = reinterpret_cast<const float4*>(Vb)[t];
+    }
+    Kb = Ks;
+    Vb = Vs;
+  }
   __syncthreads();
   const int quads = blockDim.x >> 2;
   for (int i0 = 0; i0 < N; i0 += quads) {
     const int i = i0 + (threadIdx.x >> 2);
     if (i < N) {  // whole quads agree
       const size_t row = static_cast<size_t>(b) * N + i;
-      fixedset_bwd_row<D, I>(Q + row * D, dO + row * D, Kx + boff, V + boff, Idx + row * kk,
-                             dQ + row * D, dKs, dVs, N, kk, scale, threadIdx.x & 3);
+      fixedset_bwd_row<D, I>(Q + row * D, dO + row * D, Kb, Vb, Idx + row * kk, dQ + row * D,
+                             dKs, dVs, N, kk, scale, threadIdx.x & 3);
     }
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < N * D; t += blockDim.x) {
-    dK[boff + t] += dKs[t];
-    dV[boff + t] += dVs[t];
+  for (int t = threadIdx.x; t < nd / 4; t += blockDim.x) {
+    reinterpret_cast<float4*>(dK + boff)[t] = reinterpret_cast<const float4*>(dKs)[t];
+    reinterpret_cast<float4*>(dV + boff)[t] = reinterpret_cast<const float4*>(dVs)[t];
   }
 }
 
@@ -516,32 +536,35 @@ constexpr size_t dkv_lds_bytes(int c) {
 
 constexpr size_t kBwdLdsBudget = 65536;
 
-template <int D>
-static hipError_t launch_fixedset_bwd(const FixedsetBwdArgs& a) {
-  const long rows = static_cast<long>(a.B) * a.N;
-  const int grid = static_cast<int>((rows * 4 + 255) / 256);
+template <int D, typename I>
+static hipError_t launch_fixedset_bwd_t(const FixedsetBwdArgs& a) {
   hipStream_t st = static_cast<hipStream_t>(a.stream);
-  const size_t lds = static_cast<size_t>(2) * a.N * D * sizeof(float);
-  if (lds <= kBwdLdsBudget) {  // the batch row's dK, dV fit LDS
-    if (a.idx_is_i64)
-      hipLaunchKernelGGL((fixedset_bwd_lds_kernel<D, int64_t>), dim3(a.B), dim3(1024), lds, st,
-                         a.q, a.k, a.v, a.dout, static_cast<const int64_t*>(a.idx), a.dq, a.dk,
-                         a.dv, a.N, a.kk, a.scale);
-    else
-      hipLaunchKernelGGL((fixedset_bwd_lds_kernel<D, int32_t>), dim3(a.B), dim3(1024), lds, st,
-                         a.q, a.k, a.v, a.dout, static_cast<const int32_t*>(a.idx), a.dq, a.dk,
-                         a.dv, a.N, a.kk, a.scale);
+  const I* idx = static_cast<const I*>(a.idx);
+  const size_t row_bytes = static_cast<size_t>(a.N) * D * sizeof(float);
+  if (4 * row_bytes <= kBwdLdsBudget) {  // dK, dV and the staged K, V fit LDS
+    hipLaunchKernelGGL((fixedset_bwd_lds_kernel<D, I, true>), dim3(a.B), dim3(1024), 4 * row_bytes,
+                       st, a.q, a.k, a.v, a.dout, idx, a.dq, a.dk, a.dv, a.N, a.kk, a.scale);
     return hipGetLastError();
   }
-  if (a.idx_is_i64)
-    hipLaunchKernelGGL((fixedset_bwd_kernel<D, int64_t>), dim3(grid), dim3(256), 0, st, a.q, a.k,
-                       a.v, a.dout, static_cast<const int64_t*>(a.idx), a.dq, a.dk, a.dv, a.B, a.N,
-                       a.kk, a.scale);
-  else
-    hipLaunchKernelGGL((fixedset_bwd_kernel<D, int32_t>), dim3(grid), dim3(256), 0, st, a.q, a.k,
-                       a.v, a.dout, static_cast<const int32_t*>(a.idx), a.dq, a.dk, a.dv, a.B, a.N,
-                       a.kk, a.scale);
+  if (2 * row_bytes <= kBwdLdsBudget) {  // the batch row's dK, dV fit LDS
+    hipLaunchKernelGGL((fixedset_bwd_lds_kernel<D, I, false>), dim3(a.B), dim3(1024), 2 * row_bytes,
+                       st, a.q, a.k, a.v, a.dout, idx, a.dq, a.dk, a.dv, a.N, a.kk, a.scale);
+    return hipGetLastError();
+  }
+  const long n4 = static_cast<long>(a.B) * a.N * D / 4;
+  const int zgrid = static_cast<int>(std::min<long>((n4 + 255) / 256, 4096));
+  hipLaunchKernelGGL(zero_fill_kernel, dim3(zgrid), dim3(256), 0, st,
+                     reinterpret_cast<float4*>(a.dk), reinterpret_cast<float4*>(a.dv), n4);
+  const long rows = static_cast<long>(a.B) * a.N;
+  const int grid = static_cast<int>((rows * 4 + 255) / 256);
+  hipLaunchKernelGGL((fixedset_bwd_kernel<D, I>), dim3(grid), dim3(256), 0, st, a.q, a.k, a.v,
+                     a.dout, idx, a.dq, a.dk, a.dv, a.B, a.N, a.kk, a.scale);
   return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_fixedset_bwd(const FixedsetBwdArgs& a) {
+  return a.idx_is_i64 ? launch_fixedset_bwd_t<D, int64_t>(a) : launch_fixedset_bwd_t<D, int32_t>(a);
 }
 
 hipError_t run_fixedset_bwd(const FixedsetBwdArgs& a) {

@@ -86,6 +86,43 @@ __device__ __forceinline__ void interleave_mfma_valu() {
   }
 }
 
+// Lane moves inside a 16-lane row with DPP: VALU operations, no LDS traffic
+// (a __shfl_xor becomes ds_bpermute, an LDS-pipeline instruction).
+constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int dpp_row_ror(int n) { return 0x120 + n; }
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(dpp_mov<CTRL>(__float_as_int(x)));
+}
+
+// Sum over the 4 lanes of a quad; every lane gets the same value.
+__device__ __forceinline__ float quad_sum(float x) {
+  x += dpp_mov<kDppQuadXor1>(x);
+  return x + dpp_mov<kDppQuadXor2>(x);
+}
+
+// Reductions over the 16 lanes of a row (rotations by 8, 4, 2, 1: each step
+// adds a lane's partner's partial, so every lane ends with the same value).
+template <typename T, typename Op>
+__device__ __forceinline__ T row16_reduce(T x, Op op) {
+  x = op(x, dpp_mov<dpp_row_ror(8)>(x));
+  x = op(x, dpp_mov<dpp_row_ror(4)>(x));
+  x = op(x, dpp_mov<dpp_row_ror(2)>(x));
+  return op(x, dpp_mov<dpp_row_ror(1)>(x));
+}
+// Over the lanes of a row that agree in (lane % 4): rotations by 8 and 4.
+template <typename T, typename Op>
+__device__ __forceinline__ T row16_reduce_stride4(T x, Op op) {
+  x = op(x, dpp_mov<dpp_row_ror(8)>(x));
+  return op(x, dpp_mov<dpp_row_ror(4)>(x));
+}
+
 // (a, ia) ranks before (b, ib): higher score first, lower index on ties.
 __device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
   return a > b || (a == b && ia < ib);

@@ -28,9 +28,10 @@
 // Radius: workgroup = 64 queries of one batch row, row positions in LDS; four
 // lanes per query (lane l: query l % 16 of its wave, candidates
 // j = 8u + 2(l/16) + {0,1}); the four lane lists merge with two xor shuffles.
-// Grid: workgroup per batch row; cell ids, a bitonic sort of (cell, agent) in
-// LDS (equal cells in agent order), cell starts, then one lane per query
-// scans the three column runs of its 3x3 block.
+// Grid: workgroup per batch row; cell ids, a bitonic sort of (cell, agent)
+// words (equal cells in agent order; keys in registers, LDS only across
+// wavefronts), cell starts, then one lane per query scans the three column
+// runs of its 3x3 block.
 //
 // Output order within a row: the reference's topk(sorted=False) leaves it
 // open; here the radius selector emits ascending agent index and the grid
@@ -38,6 +39,7 @@
 #include <cmath>
 
 #include "common.hpp"
+#include "sort.hpp"
 #include "tarmac_internal.hpp"
 
 #pragma clang fp contract(off)
@@ -372,6 +374,35 @@ size_t knn_grid_lds_bytes(int N, int G, int threads) {
          16 * static_cast<size_t>(threads / 64);
 }
 
+struct GridQuant {
+  float lo0, lo1, span0, span1, g;
+  int G;
+};
+
+template <int R>
+__device__ void grid_sort(const GridSmem& sm, int N, int Pn, const GridQuant& gq) {
+  const int t = threadIdx.x;
+  const bool active = t * R < Pn;
+  uint32_t key[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int a = t * R + r;
+    key[r] = kNoKey;
+    if (active && a < N) {
+      const float2 p = sm.P[a];
+      const int cx = grid_coord(p.x, gq.lo0, gq.span0, gq.g, gq.G - 1);
+      const int cy = grid_coord(p.y, gq.lo1, gq.span1, gq.g, gq.G - 1);
+      key[r] = (static_cast<uint32_t>(cx * gq.G + cy) << 16) | static_cast<uint32_t>(a);
+    }
+  }
+  block_bitonic_sort<uint32_t, R>(key, sm.keys, Pn, t, active);
+  __syncthreads();  // the last LDS stage's reads are done before the keys land
+  if (active) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) sm.keys[t * R + r] = key[r];
+  }
+}
+
 template <int K, typename I>
 __global__ void __launch_bounds__(1024)
 knn_grid_kernel(const float* __restrict__ pos, I* __restrict__ idx, int N, int Pn, int k, int G,
@@ -409,30 +440,19 @@ knn_grid_kernel(const float* __restrict__ pos, I* __restrict__ idx, int N, int P
   const float span0 = fmaxf(hi0 - lo0, 1e-6f), span1 = fmaxf(hi1 - lo1, 1e-6f);
   const float g = static_cast<float>(G);
 
-  // 2. cell keys, sorted by (cell, agent)
-  for (int i = tid; i < Pn; i += nt) {
-    uint32_t key = kNoKey;
-    if (i < N) {
-      const float2 p = sm.P[i];
-      const int cx = grid_coord(p.x, lo0, span0, g, G - 1);
-      const int cy = grid_coord(p.y, lo1, span1, g, G - 1);
-      key = (static_cast<uint32_t>(cx * G + cy) << 16) | static_cast<uint32_t>(i);
+  // 2. cell keys (cell << 16 | agent), sorted in registers / across lanes,
+  //    through LDS only across wavefronts; padding sorts last
+  {
+    const int R = Pn / nt < 2 ? 2 : Pn / nt;
+    const GridQuant gq{lo0, lo1, span0, span1, g, G};
+    switch (R) {
+      case 2: grid_sort<2>(sm, N, Pn, gq); break;
+      case 4: grid_sort<4>(sm, N, Pn, gq); break;
+      case 8: grid_sort<8>(sm, N, Pn, gq); break;
+      default: grid_sort<16>(sm, N, Pn, gq); break;
     }
-    sm.keys[i] = key;
   }
   __syncthreads();
-  for (int size = 2; size <= Pn; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int t = tid; t < (Pn >> 1); t += nt) {
-        const int a = 2 * stride * (t / stride) + (t % stride);
-        const int c = a + stride;
-        const bool up = (a & size) == 0;
-        const uint32_t x = sm.keys[a], y = sm.keys[c];
-        if ((x > y) == up) { sm.keys[a] = y; sm.keys[c] = x; }
-      }
-      __syncthreads();
-    }
-  }
   // 3. start[c] = first sorted position whose cell is >= c
   for (int r = tid; r <= N; r += nt) {
     const int prev = r == 0 ? -1 : static_cast<int>(sm.keys[r - 1] >> 16);

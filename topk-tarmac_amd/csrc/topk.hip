@@ -414,9 +414,7 @@ topk_wide16_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
     int c = 0;
 #pragma unroll
     for (int t = 0; t < NS; ++t) c += key[t] >= m ? 1 : 0;
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) c += __shfl_xor(c, o);
-    return c;
+    return row16_reduce(c, [](int a, int b) { return a + b; });
   };
 
   long lo, hi;
@@ -432,11 +430,8 @@ topk_wide16_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
         if (j != i) kmin = min(kmin, key[t]);
       }
     }
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-      kmin = min(kmin, __shfl_xor(kmin, o));
-      kmx = max(kmx, __shfl_xor(kmx, o));
-    }
+    kmin = row16_reduce(kmin, [](int a, int b) { return min(a, b); });
+    kmx = row16_reduce(kmx, [](int a, int b) { return max(a, b); });
     lo = kmin;
     hi = kmx;
     iters = bisect;
@@ -468,11 +463,8 @@ topk_wide16_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
     gt += key[t] > thr ? 1 : 0;
     eq += (key[t] == thr && sub + 16 * t < N) ? 1 : 0;
   }
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) {
-    gt += __shfl_xor(gt, o);
-    eq += __shfl_xor(eq, o);
-  }
+  gt = row16_reduce(gt, [](int a, int b) { return a + b; });
+  eq = row16_reduce(eq, [](int a, int b) { return a + b; });
   const int need_ties = mode == kSelMasked ? eq : topk - gt;
   const int skip_ties = mode == kSelSort ? eq - need_ties : 0;
 
@@ -498,8 +490,7 @@ topk_wide16_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
     taken += __popcll(pmask);
     ties += __popcll(tmask);
   }
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  mx = row16_reduce(mx, [](float a, float b) { return fmaxf(a, b); });
   __syncthreads();  // the compacted lists, written by other lanes, are read below
 
   // aggregation: lane s = 4 slot + g takes rows slot, slot + 4, ..., channels g*E..
@@ -518,12 +509,9 @@ topk_wide16_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
 #pragma unroll
     for (int c = 0; c < E; ++c) acc[c] = fmaf(w, vr[c], acc[c]);
   }
+  den = row16_reduce_stride4(den, [](float a, float b) { return a + b; });
 #pragma unroll
-  for (int o = 4; o < 16; o <<= 1) {
-    den += __shfl_xor(den, o);
-#pragma unroll
-    for (int c = 0; c < E; ++c) acc[c] += __shfl_xor(acc[c], o);
-  }
+  for (int c = 0; c < E; ++c) acc[c] = row16_reduce_stride4(acc[c], [](float a, float b) { return a + b; });
   if (!live) return;
   if (slot == 0) {
     const float inv = 1.f / den;

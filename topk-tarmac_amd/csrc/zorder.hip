@@ -16,13 +16,15 @@
 //   1. per-axis min/max over the agents (workgroup reduction);
 //   2. fp32 quantisation exactly as torch does it: (p - lo) / span * (2^bits-1),
 //      truncated, clamped; x bits to even positions, y bits to odd;
-//   3. a bitonic sort in LDS of the packed words (code << 32 | agent), so equal
-//      codes come out in agent order;
+//   3. a bitonic sort of the packed words (code << 32 | agent), so equal codes
+//      come out in agent order: keys in registers, exchanges between lanes
+//      by xor shuffles, through LDS only across wavefronts;
 //   4. rank[order[r]] = r, and agent i's peers are order[(rank[i] + off) mod N]
 //      for off = +1..+ceil(k/2), -1..-floor(k/2).
 // The fused variant then runs the fixed-set attention for the batch row from
 // the peer lists in LDS, in the same launch.
 #include "frag.hpp"
+#include "sort.hpp"
 #include "tarmac_internal.hpp"
 
 #pragma clang fp contract(off)
@@ -31,10 +33,111 @@ namespace tarmac {
 
 // One workgroup per batch row for the selector.
 constexpr int kZorderThreads = 256;
+// Queries per quad per pass of the fused Z-order attention.
+template <int D>
+constexpr int zorder_rows() { return D <= 32 ? 2 : 1; }
 
 // ---------------------------------------------------------------------------
 // fixed-set attention for one query (a quad of lanes)
 // ---------------------------------------------------------------------------
+
+// QR queries per quad at once (row r: query row qrow[r], peers peer(r, j));
+// live[r] false skips row r's loads and store. All index, K and V loads of
+// a batch of U peers of every row are in flight together.
+template <typename T, int D, int QR, typename IdxFn>
+__device__ __forceinline__ void quad_fixedset_rows(const T* const (&qrow)[QR],
+                                                   const T* __restrict__ Kb,
+                                                   const T* __restrict__ Vb,
+                                                   T* const (&orow)[QR], const bool (&live)[QR],
+                                                   int N, int kk, float scale, int sub,
+                                                   IdxFn peer) {
+  constexpr int E = D / 4;
+  // peers per batch: fewer when several rows share the registers
+  constexpr int U = QR == 1 ? (E <= 4 ? 4 : (E <= 8 ? 2 : 1)) : (E <= 4 ? 2 : 1);
+  float q[QR][E], acc[QR][E], m_run[QR], l_run[QR];
+  bool bad[QR];
+#pragma unroll
+  for (int r = 0; r < QR; ++r) {
+    if (live[r]) ld_row<T, E>(q[r], qrow[r] + sub * E);
+    else
+#pragma unroll
+      for (int c = 0; c < E; ++c) q[r][c] = 0.f;
+#pragma unroll
+    for (int c = 0; c < E; ++c) acc[r][c] = 0.f;
+    m_run[r] = -INFINITY;
+    l_run[r] = 0.f;
+    bad[r] = false;
+  }
+  for (int j0 = 0; j0 < kk; j0 += U) {
+    int p[QR][U];
+#pragma unroll
+    for (int r = 0; r < QR; ++r)
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool ok = live[r] && j0 + u < kk;
+        p[r][u] = ok ? peer(r, j0 + u) : 0;
+        bad[r] |= ok && ((p[r][u] < 0) | (p[r][u] >= N));
+        p[r][u] = min(max(p[r][u], 0), N - 1);
+      }
+    float kr[QR][U][E], vr[QR][U][E];
+#pragma unroll
+    for (int r = 0; r < QR; ++r)
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (live[r] && j0 + u < kk) {
+          ld_row<T, E>(kr[r][u], Kb + static_cast<size_t>(p[r][u]) * D + sub * E);
+          ld_row<T, E>(vr[r][u], Vb + static_cast<size_t>(p[r][u]) * D + sub * E);
+        } else {
+#pragma unroll
+          for (int c = 0; c < E; ++c) kr[r][u][c] = vr[r][u][c] = 0.f;
+        }
+      }
+#pragma unroll
+    for (int r = 0; r < QR; ++r) {
+      // scores of the batch (log2 domain), then one rescale of the running sums
+      float s[U];
+      float m_b = m_run[r];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float t = 0.f;
+#pragma unroll
+        for (int c = 0; c < E; ++c) t = fmaf(q[r][c], kr[r][u][c], t);
+        t = quad_sum(t);
+        s[u] = j0 + u < kk ? t * scale * kLog2eF : -INFINITY;
+        m_b = fmaxf(m_b, s[u]);
+      }
+      const float alpha = m_run[r] == -INFINITY ? 0.f : fast_exp2(m_run[r] - m_b);
+      l_run[r] *= alpha;
+#pragma unroll
+      for (int c = 0; c < E; ++c) acc[r][c] *= alpha;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float w = s[u] == -INFINITY ? 0.f : fast_exp2(s[u] - m_b);
+        l_run[r] += w;
+#pragma unroll
+        for (int c = 0; c < E; ++c) acc[r][c] = fmaf(w, vr[r][u][c], acc[r][c]);
+      }
+      m_run[r] = m_b;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < QR; ++r) {
+    if (!live[r]) continue;
+    const float inv = 1.f / l_run[r];
+    float o[E];
+#pragma unroll
+    for (int c = 0; c < E; ++c) o[c] = bad[r] ? __int_as_float(0x7fc00000) : acc[r][c] * inv;
+    if constexpr (E % 4 == 0) {
+      st_row<T, E>(orow[r] + sub * E, o);
+    } else {
+#pragma unroll
+      for (int c = 0; c < E; ++c) {
+        if constexpr (sizeof(T) == 4) orow[r][sub * E + c] = o[c];
+        else orow[r][sub * E + c] = f32_to_bf16(o[c]);
+      }
+    }
+  }
+}
 
 template <typename T, int D, typename IdxFn>
 __device__ __forceinline__ void quad_fixedset_row(const T* __restrict__ qrow,
@@ -42,75 +145,11 @@ __device__ __forceinline__ void quad_fixedset_row(const T* __restrict__ qrow,
                                                   const T* __restrict__ Vb, T* __restrict__ orow,
                                                   int N, int kk, float scale, int sub,
                                                   IdxFn peer) {
-  constexpr int E = D / 4;
-  // peers per batch: all their index, K and V loads are in flight together
-  constexpr int U = E <= 4 ? 4 : (E <= 8 ? 2 : 1);
-  float q[E];
-  ld_row<T, E>(q, qrow + sub * E);
-  float acc[E];
-#pragma unroll
-  for (int c = 0; c < E; ++c) acc[c] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
-  bool bad = false;
-  for (int j0 = 0; j0 < kk; j0 += U) {
-    int p[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const bool live = j0 + u < kk;
-      p[u] = live ? peer(j0 + u) : 0;
-      bad |= live && ((p[u] < 0) | (p[u] >= N));
-      p[u] = min(max(p[u], 0), N - 1);
-    }
-    float kr[U][E], vr[U][E];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (j0 + u < kk) {
-        ld_row<T, E>(kr[u], Kb + static_cast<size_t>(p[u]) * D + sub * E);
-        ld_row<T, E>(vr[u], Vb + static_cast<size_t>(p[u]) * D + sub * E);
-      } else {
-#pragma unroll
-        for (int c = 0; c < E; ++c) kr[u][c] = vr[u][c] = 0.f;
-      }
-    }
-    // scores of the batch (log2 domain), then one rescale of the running sums
-    float s[U];
-    float m_b = m_run;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float t = 0.f;
-#pragma unroll
-      for (int c = 0; c < E; ++c) t = fmaf(q[c], kr[u][c], t);
-      t += __shfl_xor(t, 1);
-      t += __shfl_xor(t, 2);
-      s[u] = j0 + u < kk ? t * scale * kLog2eF : -INFINITY;
-      m_b = fmaxf(m_b, s[u]);
-    }
-    const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(m_run - m_b);
-    l_run *= alpha;
-#pragma unroll
-    for (int c = 0; c < E; ++c) acc[c] *= alpha;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float w = s[u] == -INFINITY ? 0.f : fast_exp2(s[u] - m_b);
-      l_run += w;
-#pragma unroll
-      for (int c = 0; c < E; ++c) acc[c] = fmaf(w, vr[u][c], acc[c]);
-    }
-    m_run = m_b;
-  }
-  const float inv = 1.f / l_run;
-  float o[E];
-#pragma unroll
-  for (int c = 0; c < E; ++c) o[c] = bad ? __int_as_float(0x7fc00000) : acc[c] * inv;
-  if constexpr (E % 4 == 0) {
-    st_row<T, E>(orow + sub * E, o);
-  } else {
-#pragma unroll
-    for (int c = 0; c < E; ++c) {
-      if constexpr (sizeof(T) == 4) orow[sub * E + c] = o[c];
-      else orow[sub * E + c] = f32_to_bf16(o[c]);
-    }
-  }
+  const T* const qr[1] = {qrow};
+  T* const orr[1] = {orow};
+  const bool lv[1] = {true};
+  quad_fixedset_rows<T, D, 1>(qr, Kb, Vb, orr, lv, N, kk, scale, sub,
+                              [&](int, int j) { return peer(j); });
 }
 
 template <typename T, int D, typename I>
@@ -151,6 +190,37 @@ __device__ __forceinline__ int quantise(float p, float lo, float span, float top
   return static_cast<int>(g);
 }
 
+struct MortonQuant {
+  float lo0, lo1, span0, span1, top;
+  int topi;
+};
+
+template <int R>
+__device__ void morton_sort(const float* __restrict__ pos, int N, int P, const MortonQuant& mq,
+                            uint64_t* keys) {
+  const int t = threadIdx.x;
+  const bool active = t * R < P;
+  uint64_t key[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int a = t * R + r;
+    key[r] = ~0ull;
+    if (active && a < N) {
+      const float2 p = reinterpret_cast<const float2*>(pos)[a];
+      const uint32_t gx = quantise(p.x, mq.lo0, mq.span0, mq.top, mq.topi);
+      const uint32_t gy = quantise(p.y, mq.lo1, mq.span1, mq.top, mq.topi);
+      const uint32_t code = spread_bits16(gx) | (spread_bits16(gy) << 1);
+      key[r] = (static_cast<uint64_t>(code) << 32) | static_cast<uint32_t>(a);
+    }
+  }
+  block_bitonic_sort<uint64_t, R>(key, keys, P, t, active);
+  __syncthreads();  // the last LDS stage's reads are done before the keys land
+  if (active) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) keys[t * R + r] = key[r];
+  }
+}
+
 struct ZorderSmem {
   uint64_t* keys;   // [P] packed (code << 32 | agent)
   int* order;       // [N]
@@ -186,32 +256,17 @@ __device__ void morton_order_rank(const float* __restrict__ pos, int N, int P, i
   }
   const float span0 = fmaxf(hi0 - lo0, 1e-6f), span1 = fmaxf(hi1 - lo1, 1e-6f);
   const int topi = (1 << bits) - 1;
-  const float top = static_cast<float>(topi);
-  for (int i = tid; i < P; i += nt) {
-    uint64_t key = ~0ull;  // padding sorts last
-    if (i < N) {
-      const float2 p = reinterpret_cast<const float2*>(pos)[i];
-      const uint32_t gx = quantise(p.x, lo0, span0, top, topi);
-      const uint32_t gy = quantise(p.y, lo1, span1, top, topi);
-      const uint32_t code = spread_bits16(gx) | (spread_bits16(gy) << 1);
-      key = (static_cast<uint64_t>(code) << 32) | static_cast<uint32_t>(i);
-    }
-    sm.keys[i] = key;
+  const MortonQuant mq{lo0, lo1, span0, span1, static_cast<float>(topi), topi};
+  // (code << 32 | agent) words, sorted in registers / across lanes, LDS only
+  // for the strides that cross wavefronts; padding sorts last
+  const int R = P / nt < 2 ? 2 : P / nt;
+  switch (R) {
+    case 2: morton_sort<2>(pos, N, P, mq, sm.keys); break;
+    case 4: morton_sort<4>(pos, N, P, mq, sm.keys); break;
+    case 8: morton_sort<8>(pos, N, P, mq, sm.keys); break;
+    default: morton_sort<16>(pos, N, P, mq, sm.keys); break;
   }
   __syncthreads();
-  // Bitonic sort, ascending, P a power of two.
-  for (int size = 2; size <= P; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int t = tid; t < (P >> 1); t += nt) {
-        const int lo = 2 * stride * (t / stride) + (t % stride);
-        const int hi = lo + stride;
-        const bool up = (lo & size) == 0;
-        const uint64_t a = sm.keys[lo], c = sm.keys[hi];
-        if ((a > c) == up) { sm.keys[lo] = c; sm.keys[hi] = a; }
-      }
-      __syncthreads();
-    }
-  }
   for (int r = tid; r < N; r += nt) {
     const int agent = static_cast<int>(sm.keys[r] & 0xffffffffu);
     sm.order[r] = agent;
@@ -272,13 +327,30 @@ zorder_attn_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
   const size_t boff = static_cast<size_t>(b) * N * D;
   const int lane = threadIdx.x & 63;
   const int quads = blockDim.x >> 2;
-  for (int i = threadIdx.x >> 2; i < N; i += quads) {
-    quad_fixedset_row<T, D>(Q + boff + static_cast<size_t>(i) * D, Kx + boff, V + boff,
-                            O + boff + static_cast<size_t>(i) * D, N, k, scale, lane & 3,
-                            [&](int j) { return window_peer(sm, i, j, k, N); });
+  // several queries per quad per pass: their peer loads overlap
+  constexpr int QR = zorder_rows<D>();
+  for (int i0 = threadIdx.x >> 2; i0 < N; i0 += QR * quads) {
+    const T* qr[QR];
+    T* orr[QR];
+    bool lv[QR];
+#pragma unroll
+    for (int r = 0; r < QR; ++r) {
+      const int i = i0 + r * quads;
+      lv[r] = i < N;
+      const int ic = lv[r] ? i : 0;
+      qr[r] = Q + boff + static_cast<size_t>(ic) * D;
+      orr[r] = O + boff + static_cast<size_t>(ic) * D;
+    }
+    quad_fixedset_rows<T, D, QR>(qr, Kx + boff, V + boff, orr, lv, N, k, scale, lane & 3,
+                                 [&](int r, int j) { return window_peer(sm, i0 + r * quads, j, k, N); });
     if (idx_out != nullptr && (lane & 3) == 0) {
-      for (int j = 0; j < k; ++j)
-        idx_out[(static_cast<size_t>(b) * N + i) * k + j] = window_peer(sm, i, j, k, N);
+#pragma unroll
+      for (int r = 0; r < QR; ++r) {
+        const int i = i0 + r * quads;
+        if (!lv[r]) continue;
+        for (int j = 0; j < k; ++j)
+          idx_out[(static_cast<size_t>(b) * N + i) * k + j] = window_peer(sm, i, j, k, N);
+      }
     }
   }
 }

@@ -42,8 +42,8 @@ def fixedset_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tenso
     if idx.dtype not in (torch.int32, torch.int64):
         raise ValueError("idx must be int32 or int64")
     dq = torch.empty_like(q)
-    dk = torch.zeros_like(k)
-    dv = torch.zeros_like(v)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
     with torch.cuda.device(q.device):
         rc = _lib.LIB.tarmac_fixedset_bwd(
             _launch.ptr(q), _launch.ptr(k), _launch.ptr(v), _launch.ptr(dout), _launch.ptr(idx),
