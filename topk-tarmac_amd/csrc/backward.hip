@@ -58,15 +58,16 @@ __device__ __forceinline__ void atomic_add_row(float* dst, const float (&x)[E], 
 // One query (a quad of lanes): dq is written; the dk / dv rows of its peers
 // receive atomic adds (global memory or LDS). Peers are taken U at a time
 // with their index, K and V loads in flight together; when the set fits one
-// batch (kk <= U) the second pass reuses the rows from registers. Kb / Vb are the batch row's keys and values, in LDS
-// or global memory.
-template <int D, typename I>
+// batch (kk <= U) the second pass reuses the rows from registers. Kb / Vb are
+// the batch row's keys and values, in LDS or global memory. For each valid
+// peer, sink(j, p, q, g, ds, w) receives the query's contribution to dk_p
+// (scale * ds * q) and dv_p (w * g); every lane of the quad calls it.
+template <int D, typename I, typename Sink>
 __device__ __forceinline__ void fixedset_bwd_row(const float* __restrict__ qrow,
                                                  const float* __restrict__ grow,
                                                  const float* Kb, const float* Vb,
                                                  const I* __restrict__ ir, float* __restrict__ dqrow,
-                                                 float* dK, float* dV, int N, int kk, float scale,
-                                                 int sub) {
+                                                 int N, int kk, float scale, int sub, Sink sink) {
   constexpr int E = D / 4;
   constexpr int U = E <= 4 ? 8 : (E <= 8 ? 4 : 1);  // within 128 VGPRs at 1024 threads
   const float c2 = scale * kLog2eF;  // scores in the exp2 domain
@@ -129,16 +130,29 @@ __device__ __forceinline__ void fixedset_bwd_row(const float* __restrict__ qrow,
       const float ds = w * (dw[u] - Dq);
 #pragma unroll
       for (int c = 0; c < E; ++c) dq[c] = fmaf(ds, kr[u][c], dq[c]);
-      if (p[u] >= 0 && p[u] < N) {
-        atomic_add_row<E>(dK + static_cast<size_t>(p[u]) * D + sub * E, q, ds * scale);
-        atomic_add_row<E>(dV + static_cast<size_t>(p[u]) * D + sub * E, g, w);
-      }
+      if (p[u] >= 0 && p[u] < N) sink(j0 + u, p[u], q, g, ds, w);
     }
   }
 #pragma unroll
   for (int c = 0; c < E; ++c) dq[c] = bad ? __int_as_float(0x7fc00000) : dq[c] * scale;
   st_f32<E>(dqrow + sub * E, dq);
 }
+
+// The scatter of a peer's contribution with fp32 atomic adds (global memory
+// or LDS); lane (l % 4) adds its E channels.
+template <int D>
+struct AtomicSink {
+  float* dK;
+  float* dV;
+  int sub;
+  float scale;
+  template <int E>
+  __device__ __forceinline__ void operator()(int, int p, const float (&q)[E], const float (&g)[E],
+                                             float ds, float w) const {
+    atomic_add_row<E>(dK + static_cast<size_t>(p) * D + sub * E, q, ds * scale);
+    atomic_add_row<E>(dV + static_cast<size_t>(p) * D + sub * E, g, w);
+  }
+};
 
 // Global accumulation: one quad per query over the whole grid; dK, dV are
 // zeroed by zero_fill_kernel first.
@@ -152,10 +166,11 @@ fixedset_bwd_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   if (row >= static_cast<long>(B) * N) return;  // whole quads exit together
   const int b = static_cast<int>(row / N);
   const size_t boff = static_cast<size_t>(b) * N * D;
+  const int sub = threadIdx.x & 3;
   fixedset_bwd_row<D, I>(Q + static_cast<size_t>(row) * D, dO + static_cast<size_t>(row) * D,
                          Kx + boff, V + boff, Idx + static_cast<size_t>(row) * kk,
-                         dQ + static_cast<size_t>(row) * D, dK + boff, dV + boff, N, kk, scale,
-                         threadIdx.x & 3);
+                         dQ + static_cast<size_t>(row) * D, N, kk, scale, sub,
+                         AtomicSink<D>{dK + boff, dV + boff, sub, scale});
 }
 
 __global__ void __launch_bounds__(256) zero_fill_kernel(float4* __restrict__ a, float4* __restrict__ b,
@@ -204,14 +219,140 @@ fixedset_bwd_lds_kernel(const float* __restrict__ Q, const float* __restrict__ K
     const int i = i0 + (threadIdx.x >> 2);
     if (i < N) {  // whole quads agree
       const size_t row = static_cast<size_t>(b) * N + i;
-      fixedset_bwd_row<D, I>(Q + row * D, dO + row * D, Kb, Vb, Idx + row * kk, dQ + row * D,
-                             dKs, dVs, N, kk, scale, threadIdx.x & 3);
+      const int sub = threadIdx.x & 3;
+      fixedset_bwd_row<D, I>(Q + row * D, dO + row * D, Kb, Vb, Idx + row * kk, dQ + row * D, N,
+                             kk, scale, sub, AtomicSink<D>{dKs, dVs, sub, scale});
     }
   }
   __syncthreads();
   for (int t = threadIdx.x; t < nd / 4; t += blockDim.x) {
     reinterpret_cast<float4*>(dK + boff)[t] = reinterpret_cast<const float4*>(dKs)[t];
     reinterpret_cast<float4*>(dV + boff)[t] = reinterpret_cast<const float4*>(dVs)[t];
+  }
+}
+
+// Gather form (no float atomics), one workgroup per batch row:
+//   1. K, V rows in LDS; each query (a quad) computes dq and, per peer slot
+//      e = i*kk + j, ds and w into LDS, counting its peers per key;
+//   2. an exclusive scan of the counts gives each key's list start; every
+//      entry takes a place in its key's list (an integer atomic);
+//   3. Q, dO rows replace K, V in LDS; each key (a quad) sums its list:
+//      dk = scale * sum ds q_i, dv = sum w g_i, written once.
+// Entry order within a key's list follows the atomics, so dk, dv are summed
+// in no fixed order, like the atomic forms.
+template <int D>
+struct GatherSink {
+  float* e_ds;
+  float* e_w;
+  int* cnt;
+  int row0;  // i * kk
+  int sub;
+  template <int E>
+  __device__ __forceinline__ void operator()(int j, int p, const float (&)[E], const float (&)[E],
+                                             float ds, float w) const {
+    if (sub == 0) {
+      e_ds[row0 + j] = ds;
+      e_w[row0 + j] = w;
+      atomicAdd(cnt + p, 1);
+    }
+  }
+};
+
+size_t fixedset_gather_lds_bytes(int N, int D, int kk) {
+  return (static_cast<size_t>(2) * N * D + 3 * static_cast<size_t>(N) * kk +
+          3 * static_cast<size_t>(N) + 1) * 4;
+}
+
+template <int D, typename I>
+__global__ void __launch_bounds__(1024)
+fixedset_bwd_gather_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
+                           const float* __restrict__ V, const float* __restrict__ dO,
+                           const I* __restrict__ Idx, float* __restrict__ dQ,
+                           float* __restrict__ dK, float* __restrict__ dV, int N, int kk,
+                           float scale) {
+  constexpr int E = D / 4;
+  extern __shared__ __align__(16) float smem[];
+  const int nd = N * D, nk = N * kk;
+  float* rows = smem;                 // [2 * N * D]: K, V, then Q, dO
+  float* e_ds = rows + 2 * nd;        // [N * kk]
+  float* e_w = e_ds + nk;             // [N * kk]
+  int* perm = reinterpret_cast<int*>(e_w + nk);  // [N * kk]: entries in key order
+  int* cnt = perm + nk;               // [N]
+  int* start = cnt + N;               // [N + 1]
+  int* cursor = start + N + 1;        // [N]
+  const int b = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
+  const size_t boff = static_cast<size_t>(b) * nd;
+  const int sub = tid & 3, quads = nt >> 2;
+
+  for (int t = tid; t < N; t += nt) { cnt[t] = 0; cursor[t] = 0; }
+  for (int t = tid; t < nd / 4; t += nt) {
+    reinterpret_cast<float4*>(rows)[t] = reinterpret_cast<const float4*>(Kx + boff)[t];
+    reinterpret_cast<float4*>(rows + nd)[t] = reinterpret_cast<const float4*>(V + boff)[t];
+  }
+  __syncthreads();
+  // 1. per query
+  for (int i0 = 0; i0 < N; i0 += quads) {
+    const int i = i0 + (tid >> 2);
+    if (i < N) {  // whole quads agree
+      const size_t row = static_cast<size_t>(b) * N + i;
+      fixedset_bwd_row<D, I>(Q + row * D, dO + row * D, rows, rows + nd, Idx + row * kk,
+                             dQ + row * D, N, kk, scale, sub,
+                             GatherSink<D>{e_ds, e_w, cnt, i * kk, sub});
+    }
+  }
+  __syncthreads();
+  // 2. list starts (one wavefront scans), then places
+  if (tid < 64) {
+    int carry = 0;
+    for (int c0 = 0; c0 < N; c0 += 64) {
+      const int c = c0 + tid < N ? cnt[c0 + tid] : 0;
+      int x = c;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (tid >= o) x += y;
+      }
+      if (c0 + tid < N) start[c0 + tid] = carry + x - c;
+      carry += __shfl(x, 63);
+    }
+    if (tid == 0) start[N] = carry;
+  }
+  __syncthreads();
+  for (int e = tid; e < nk; e += nt) {
+    const int i = e / kk;
+    const int p = static_cast<int>(Idx[(static_cast<size_t>(b) * N + i) * kk + (e - i * kk)]);
+    if (p >= 0 && p < N) perm[start[p] + atomicAdd(cursor + p, 1)] = e;
+  }
+  for (int t = tid; t < nd / 4; t += nt) {  // K, V are no longer read
+    reinterpret_cast<float4*>(rows)[t] = reinterpret_cast<const float4*>(Q + boff)[t];
+    reinterpret_cast<float4*>(rows + nd)[t] = reinterpret_cast<const float4*>(dO + boff)[t];
+  }
+  __syncthreads();
+  // 3. per key
+  for (int j0 = 0; j0 < N; j0 += quads) {
+    const int j = j0 + (tid >> 2);
+    if (j >= N) continue;
+    float dk[E], dv[E];
+#pragma unroll
+    for (int c = 0; c < E; ++c) dk[c] = dv[c] = 0.f;
+    const int s1 = start[j + 1];
+    for (int s = start[j]; s < s1; ++s) {
+      const int e = perm[s];
+      const int i = e / kk;
+      const float ds = e_ds[e], w = e_w[e];
+      float q[E], g[E];
+      ld_f32<E>(q, rows + i * D + sub * E);
+      ld_f32<E>(g, rows + nd + i * D + sub * E);
+#pragma unroll
+      for (int c = 0; c < E; ++c) {
+        dk[c] = fmaf(ds, q[c], dk[c]);
+        dv[c] = fmaf(w, g[c], dv[c]);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < E; ++c) dk[c] *= scale;
+    st_f32<E>(dK + boff + static_cast<size_t>(j) * D + sub * E, dk);
+    st_f32<E>(dV + boff + static_cast<size_t>(j) * D + sub * E, dv);
   }
 }
 
@@ -541,6 +682,12 @@ static hipError_t launch_fixedset_bwd_t(const FixedsetBwdArgs& a) {
   hipStream_t st = static_cast<hipStream_t>(a.stream);
   const I* idx = static_cast<const I*>(a.idx);
   const size_t row_bytes = static_cast<size_t>(a.N) * D * sizeof(float);
+  const size_t gather_lds = fixedset_gather_lds_bytes(a.N, D, a.kk);
+  if (gather_lds <= kBwdLdsBudget) {  // rows and per-entry lists fit LDS
+    hipLaunchKernelGGL((fixedset_bwd_gather_kernel<D, I>), dim3(a.B), dim3(1024), gather_lds, st,
+                       a.q, a.k, a.v, a.dout, idx, a.dq, a.dk, a.dv, a.N, a.kk, a.scale);
+    return hipGetLastError();
+  }
   if (4 * row_bytes <= kBwdLdsBudget) {  // dK, dV and the staged K, V fit LDS
     hipLaunchKernelGGL((fixedset_bwd_lds_kernel<D, I, true>), dim3(a.B), dim3(1024), 4 * row_bytes,
                        st, a.q, a.k, a.v, a.dout, idx, a.dq, a.dk, a.dv, a.N, a.kk, a.scale);
