@@ -14,7 +14,11 @@
 // V is staged transposed in LDS so the A operand of the PV product is a
 // contiguous read. The running max is shared by the 4 lanes of a query
 // (two xor shuffles per 64-key block); the running sum stays per lane and is
-// combined once at the end.
+// combined once at the end. fp32 scores come out of the product already in
+// the log2 domain (q is pre-multiplied by scale*log2(e), exact for the
+// power-of-two scales); bf16 scores stay raw and the factor is applied inside
+// the exponent's argument, fma(s, c, -c*m), after a max taken on raw scores
+// (c > 0, so the max commutes with the scaling).
 #include "frag.hpp"
 #include "tarmac_internal.hpp"
 
@@ -27,15 +31,17 @@ constexpr int kDenseQueryTiles = 2;  // 16-query tiles per wavefront
 template <typename T, int D>
 struct PvOperand;
 
-// fp32: O^T block h (channels 16h..16h+15) += V^T(16 x 4 keys) * P^T(4 keys x 16 q).
-// The V^T fragment of a (tile, h) is read once and used by every query tile.
+// fp32: O^T block h (channels 16h..16h+15) += V^T(16 x 4 keys) * P^T(4 keys x 16 q),
+// four steps per 16-key tile. The V^T fragment of a (tile, h) is read once
+// and used by every query tile.
 template <int D>
 struct PvOperand<float, D> {
   static constexpr int NH = (D + 15) / 16;  // output blocks of 16 channels
   static constexpr int CP = NH * 16;        // padded channel count in LDS
+  static constexpr int TILES = 1;           // 16-key tiles per step
   template <int QT>
-  __device__ __forceinline__ static void pv_tile(f32x4 (&acc)[QT][NH], const float* Vt, int ldv,
-                                                 int kb, int lane, const float (&p)[QT][4]) {
+  __device__ __forceinline__ static void pv_step(f32x4 (&acc)[QT][NH], const float* Vt, int ldv,
+                                                 int kb, int lane, const float (&p)[QT][TILES][4]) {
     const int col = lane & 15, grp = lane >> 4;
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
@@ -43,30 +49,49 @@ struct PvOperand<float, D> {
 #pragma unroll
       for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) acc[qt][h] = mfma_f32_16x16x4(vv[u], p[qt][u], acc[qt][h]);
+        for (int qt = 0; qt < QT; ++qt) acc[qt][h] = mfma_f32_16x16x4(vv[u], p[qt][0][u], acc[qt][h]);
     }
   }
 };
 
-// bf16: O^T block h += V^T(16 x 16 keys) * P^T(16 keys x 16 q), one MFMA
+// Four probabilities as bf16 (round to nearest even, the rounding of
+// Tensor.to(torch.bfloat16)), two hardware conversions.
+__device__ __forceinline__ bf16x8 pack_p_pair(const float (&a)[4], const float (&b)[4]) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    bf16x2_t lo = {static_cast<__bf16>(a[2 * i]), static_cast<__bf16>(a[2 * i + 1])};
+    bf16x2_t hi = {static_cast<__bf16>(b[2 * i]), static_cast<__bf16>(b[2 * i + 1])};
+    w[i] = __builtin_bit_cast(uint32_t, lo);
+    w[2 + i] = __builtin_bit_cast(uint32_t, hi);
+  }
+  return __builtin_bit_cast(bf16x8, w);
+}
+
+// bf16: one 16x16x32 MFMA per output block and pair of 16-key tiles. The
+// contraction index j = 8 (l/16) + e of lane l maps to key 4 (l/16) + e of the
+// first tile (e < 4) and of the second (e >= 4): the B operand is the lane's
+// own eight probabilities, the A operand two 8-byte V^T reads.
 template <int D>
 struct PvOperand<bf16, D> {
   static constexpr int NH = D / 16;
   static constexpr int CP = NH * 16;
+  static constexpr int TILES = 2;  // 16-key tiles per step
   template <int QT>
-  __device__ __forceinline__ static void pv_tile(f32x4 (&acc)[QT][NH], const bf16* Vt, int ldv,
-                                                 int kb, int lane, const float (&p)[QT][4]) {
+  __device__ __forceinline__ static void pv_step(f32x4 (&acc)[QT][NH], const bf16* Vt, int ldv,
+                                                 int kb, int lane, const float (&p)[QT][TILES][4]) {
     const int col = lane & 15, grp = lane >> 4;
-    i16x4 pb[QT];
+    bf16x8 pb[QT];
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int u = 0; u < 4; ++u) pb[qt][u] = static_cast<short>(f32_to_bf16(p[qt][u]));
+    for (int qt = 0; qt < QT; ++qt) pb[qt] = pack_p_pair(p[qt][0], p[qt][1]);
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
-      const i16x4 vv = *reinterpret_cast<const i16x4*>(Vt + (16 * h + col) * ldv + kb + 4 * grp);
+      const bf16* r = Vt + (16 * h + col) * ldv + kb + 4 * grp;
+      uint2 w[2] = {*reinterpret_cast<const uint2*>(r), *reinterpret_cast<const uint2*>(r + 16)};
+      const bf16x8 vv = __builtin_bit_cast(bf16x8, w);
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) acc[qt][h] = mfma_bf16_16x16x16(vv, pb[qt], acc[qt][h]);
+      for (int qt = 0; qt < QT; ++qt) acc[qt][h] = mfma_bf16_16x16x32(vv, pb[qt], acc[qt][h]);
     }
   }
 };
@@ -96,7 +121,7 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
   const size_t boff = static_cast<size_t>(b) * N * D;
 
   // fp32 scores come out pre-multiplied by scale*log2(e), ready for exp2;
-  // bf16 scores are scaled after the product (the factor is not exact in bf16).
+  // bf16 scores are scaled inside the exponent (the factor is not exact in bf16).
   F frag[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
@@ -104,6 +129,7 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
     frag[qt].load_q(Q + boff + static_cast<size_t>(min(qi, N - 1)) * D, grp,
                     sizeof(T) == 4 ? scale * kLog2e : 1.f);
   }
+  // exponent factor: 1 for fp32 (folded into q), scale*log2(e) for bf16
   const float post = (sizeof(T) == 4) ? 1.f : scale * kLog2e;
 
   f32x4 acc[QT][NH];
@@ -121,20 +147,18 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
     const int cnp = (cn + BK - 1) / BK * BK;
     __syncthreads();
     stage_rows<T, D, LDK>(Ks, Kx + boff + static_cast<size_t>(c0) * D, cn, cnp);
-    stage_vt<T, D, PV::CP>(Vt, ldv, V + boff + static_cast<size_t>(c0) * D, cn, cnp);
+    // bf16 rows transpose four at a time (8-byte stores instead of 2-byte
+    // ones); fp32 keeps one store per element, measured no slower
+    if constexpr (sizeof(T) == 4)
+      stage_vt<T, D, PV::CP>(Vt, ldv, V + boff + static_cast<size_t>(c0) * D, cn, cnp);
+    else
+      stage_vt_quads<T, D, PV::CP>(Vt, ldv, V + boff + static_cast<size_t>(c0) * D, cn, cnp);
     __syncthreads();
     if (q0 >= N) continue;
     const int kend = c0 + cn;  // rows past the chunk end are zero padding
     for (int kb0 = 0; kb0 < cnp; kb0 += BK) {
-      f32x4 st[QT][BT];
-      block_scores<F, QT, BT>(frag, Ks, kb0, LDK, lane, st);
-      float s[QT][BT][4];
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-        for (int t = 0; t < BT; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) s[qt][t][r] = st[qt][t][r] * post;
+      f32x4 s[QT][BT];
+      block_scores<F, QT, BT>(frag, Ks, kb0, LDK, lane, s);
       const int kabs = c0 + kb0;
       if ((q0 < kabs + BK && kabs < q0 + 16 * QT) || kabs + BK > kend) {  // wave-uniform
 #pragma unroll
@@ -147,7 +171,7 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
               if (key >= kend || key == q0 + 16 * qt + col) s[qt][t][r] = -INFINITY;
             }
       }
-      float m_use[QT];
+      float neg[QT];  // -post * (running max): the exponent's offset
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
         float mloc = -INFINITY;
@@ -158,24 +182,29 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
         mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
         const float m_new = fmaxf(m_run[qt], mloc);
-        m_use[qt] = (m_new == -INFINITY) ? 0.f : m_new;
-        const float alpha = fast_exp2(m_run[qt] - m_use[qt]);  // 0 while nothing has been seen
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        const float alpha = fast_exp2((m_run[qt] - m_use) * post);  // 0 while nothing has been seen
         l_run[qt] *= alpha;
 #pragma unroll
         for (int h = 0; h < NH; ++h) acc[qt][h] *= alpha;
         m_run[qt] = m_new;
+        neg[qt] = -m_use * post;
       }
+      constexpr int TS = PV::TILES;
+      static_assert(BT % TS == 0, "whole PV steps per block");
 #pragma unroll
-      for (int t = 0; t < BT; ++t) {
-        float p[QT][4];
+      for (int t0 = 0; t0 < BT; t0 += TS) {
+        float p[QT][TS][4];
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            p[qt][r] = fast_exp2(s[qt][t][r] - m_use[qt]);
-            l_run[qt] += p[qt][r];
-          }
-        PV::template pv_tile<QT>(acc, Vt, ldv, kb0 + 16 * t, lane, p);
+          for (int t = 0; t < TS; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              p[qt][t][r] = fast_exp2(fmaf(s[qt][t0 + t][r], post, neg[qt]));
+              l_run[qt] += p[qt][t][r];
+            }
+        PV::template pv_step<QT>(acc, Vt, ldv, kb0 + 16 * t0, lane, p);
       }
     }
   }
@@ -188,7 +217,7 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
     if (qi >= N) continue;
     // log2-domain logsumexp of the scaled scores, for the backward pass
     if (lse != nullptr && grp == 0)
-      lse[static_cast<size_t>(b) * 2 * N + qi] = m_run[qt] + log2f(l_tot);
+      lse[static_cast<size_t>(b) * 2 * N + qi] = m_run[qt] * post + log2f(l_tot);
     // lane l holds O^T[c = 16h + 4*(l/16) + r][q = l%16]
 #pragma unroll
     for (int h = 0; h < NH; ++h) {

@@ -266,15 +266,18 @@ __device__ __forceinline__ void stage_rows(T* lds, const T* src, int rows, int r
   constexpr int VPR = D / VE;
   constexpr int U = kStageBatch;
   static_assert(D % VE == 0 && (LDK * sizeof(T)) % 16 == 0, "16-byte staging");
+  // the rows are contiguous in global memory: vector v sits at byte 16 v of
+  // the chunk (a 32-bit offset from the uniform base)
+  const char* base = reinterpret_cast<const char*>(src);
   const int total = rows_pad * VPR;
+  const int avail = rows * VPR;  // vectors backed by source rows
   for (int v0 = threadIdx.x; v0 < total; v0 += U * blockDim.x) {
     uint4 x[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int v = v0 + u * blockDim.x, row = v / VPR, cv = v - row * VPR;
+      const int v = v0 + u * blockDim.x;
       x[u] = make_uint4(0u, 0u, 0u, 0u);
-      if (v < total && row < rows)
-        x[u] = *reinterpret_cast<const uint4*>(src + static_cast<size_t>(row) * D + cv * VE);
+      if (v < avail) x[u] = *reinterpret_cast<const uint4*>(base + static_cast<uint32_t>(v) * 16u);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -309,6 +312,57 @@ __device__ __forceinline__ void stage_vt(T* Vt, int ldv, const T* src, int rows,
       __builtin_memcpy(x, &raw[u], 16);
 #pragma unroll
       for (int e = 0; e < VE; ++e) Vt[(cv * VE + e) * ldv + row] = x[e];
+    }
+  }
+  if constexpr (CP > D) {
+    const int pad = (CP - D) * rows_pad;
+    for (int v = threadIdx.x; v < pad; v += blockDim.x) {
+      const int c = D + v / rows_pad, row = v % rows_pad;
+      Vt[c * ldv + row] = T(0);
+    }
+  }
+}
+
+// As stage_vt, four rows per thread: each thread loads one 16-byte vector
+// from each of four consecutive rows and writes, per channel, the four rows'
+// elements as one 4-element store (8 bytes for bf16, 16 for fp32) -- a
+// quarter of the LDS write instructions of one store per element. rows_pad
+// is a multiple of 4; ldv * sizeof(T) a multiple of 4 * sizeof(T).
+template <typename T, int D, int CP>
+__device__ __forceinline__ void stage_vt_quads(T* Vt, int ldv, const T* src, int rows,
+                                               int rows_pad) {
+  constexpr int VE = 16 / sizeof(T);
+  constexpr int VPR = D / VE;
+  static_assert(D % VE == 0, "16-byte staging");
+  const char* base = reinterpret_cast<const char*>(src);  // rows contiguous, 16 VPR bytes each
+  const int total = (rows_pad / 4) * VPR;
+  for (int v = threadIdx.x; v < total; v += blockDim.x) {
+    const int quad = v / VPR, cv = v - quad * VPR, row0 = 4 * quad;
+    uint4 x[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[j] = make_uint4(0u, 0u, 0u, 0u);
+      if (row0 + j < rows)
+        x[j] = *reinterpret_cast<const uint4*>(
+            base + static_cast<uint32_t>((row0 + j) * VPR + cv) * 16u);
+    }
+    const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&x[0]);
+    const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&x[1]);
+    const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&x[2]);
+    const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&x[3]);
+#pragma unroll
+    for (int e = 0; e < VE; ++e) {
+      T* dst = Vt + (cv * VE + e) * ldv + row0;
+      if constexpr (sizeof(T) == 4) {
+        *reinterpret_cast<uint4*>(dst) = make_uint4(w0[e], w1[e], w2[e], w3[e]);
+      } else {
+        // element e is the low (e even) or high (e odd) half of word e / 2:
+        // one byte permute per pair of rows
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        *reinterpret_cast<uint2*>(dst) =
+            make_uint2(__builtin_amdgcn_perm(w1[e / 2], w0[e / 2], sel),
+                       __builtin_amdgcn_perm(w3[e / 2], w2[e / 2], sel));
+      }
     }
   }
   if constexpr (CP > D) {
