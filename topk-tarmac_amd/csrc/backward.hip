@@ -162,7 +162,8 @@ fixedset_bwd_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
                     const float* __restrict__ V, const float* __restrict__ dO,
                     const I* __restrict__ Idx, float* __restrict__ dQ, float* __restrict__ dK,
                     float* __restrict__ dV, int B, int N, int kk, float scale) {
-  const long row = (static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x) >> 2;
+  const int blk = xcd_logical_block(blockIdx.x, gridDim.x);  // a batch row's blocks share an XCD
+  const long row = (static_cast<long>(blk) * blockDim.x + threadIdx.x) >> 2;
   if (row >= static_cast<long>(B) * N) return;  // whole quads exit together
   const int b = static_cast<int>(row / N);
   const size_t boff = static_cast<size_t>(b) * N * D;

@@ -205,7 +205,8 @@ knn_radius_kernel(const float* __restrict__ pos, I* __restrict__ idx, int N, int
                   int cbits) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   float2* P = reinterpret_cast<float2*>(smem_raw);
-  const int b = blockIdx.x / n_qblk, qb = blockIdx.x - b * n_qblk;
+  const int blk = xcd_logical_block(blockIdx.x, gridDim.x);  // a batch row's blocks share an XCD
+  const int b = blk / n_qblk, qb = blk - b * n_qblk;
   const float2* prow = reinterpret_cast<const float2*>(pos) + static_cast<size_t>(b) * N;
   const int N8 = (N + 7) & ~7;
   for (int j = threadIdx.x; j < N8; j += blockDim.x)

@@ -214,7 +214,8 @@ topk_wide_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __r
   constexpr int KST = D + 16 / static_cast<int>(sizeof(T));  // padded LDS key row
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  const int b = blockIdx.x / n_qblk, qb = blockIdx.x - b * n_qblk;
+  const int blk = xcd_logical_block(blockIdx.x, gridDim.x);  // a batch row's blocks share an XCD
+  const int b = blk / n_qblk, qb = blk - b * n_qblk;
   const int i_raw = qb * nw + wave;
   const bool live = i_raw < N;  // wave-uniform
   const int i = live ? i_raw : N - 1;
@@ -374,7 +375,8 @@ topk_wide16_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int qs = lane >> 4, sub = lane & 15;
-  const int b = blockIdx.x / n_qblk, qb = blockIdx.x - b * n_qblk;
+  const int blk = xcd_logical_block(blockIdx.x, gridDim.x);  // a batch row's blocks share an XCD
+  const int b = blk / n_qblk, qb = blk - b * n_qblk;
   const int qslot = 4 * wave + qs;                 // query slot in the workgroup
   const int i_raw = 16 * qb + qslot;
   const bool live = i_raw < N;                     // uniform over the 16 lanes

@@ -157,7 +157,10 @@ __global__ void __launch_bounds__(256)
 fixedset_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
                 const I* __restrict__ Idx, T* __restrict__ O, int B, int N, int kk, float scale) {
   const int lane = threadIdx.x & 63;
-  const long row = (static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x) >> 2;
+  // consecutive logical blocks (the queries of one batch row) share an XCD,
+  // so the row's K and V rows are fetched into one L2
+  const int blk = xcd_logical_block(blockIdx.x, gridDim.x);
+  const long row = (static_cast<long>(blk) * blockDim.x + threadIdx.x) >> 2;
   if (row >= static_cast<long>(B) * N) return;  // whole quads exit together
   const int b = static_cast<int>(row / N);
   const size_t boff = static_cast<size_t>(b) * N * D;
@@ -195,8 +198,10 @@ struct MortonQuant {
   int topi;
 };
 
+// Thread t holds agents t*R .. t*R+R-1 (positions already in registers;
+// padding agents a >= N sort last).
 template <int R>
-__device__ void morton_sort(const float* __restrict__ pos, int N, int P, const MortonQuant& mq,
+__device__ void morton_sort(const float2 (&p)[R], int N, int P, const MortonQuant& mq,
                             uint64_t* keys) {
   const int t = threadIdx.x;
   const bool active = t * R < P;
@@ -206,9 +211,8 @@ __device__ void morton_sort(const float* __restrict__ pos, int N, int P, const M
     const int a = t * R + r;
     key[r] = ~0ull;
     if (active && a < N) {
-      const float2 p = reinterpret_cast<const float2*>(pos)[a];
-      const uint32_t gx = quantise(p.x, mq.lo0, mq.span0, mq.top, mq.topi);
-      const uint32_t gy = quantise(p.y, mq.lo1, mq.span1, mq.top, mq.topi);
+      const uint32_t gx = quantise(p[r].x, mq.lo0, mq.span0, mq.top, mq.topi);
+      const uint32_t gy = quantise(p[r].y, mq.lo1, mq.span1, mq.top, mq.topi);
       const uint32_t code = spread_bits16(gx) | (spread_bits16(gy) << 1);
       key[r] = (static_cast<uint64_t>(code) << 32) | static_cast<uint32_t>(a);
     }
@@ -229,16 +233,25 @@ struct ZorderSmem {
 };
 
 // Workgroup-wide: codes, sort, order and rank for batch row `pos` ([N, 2]).
-__device__ void morton_order_rank(const float* __restrict__ pos, int N, int P, int bits,
-                                  const ZorderSmem& sm) {
+// Each thread loads the positions of the agents it sorts, once.
+template <int R>
+__device__ void morton_order_rank_r(const float* __restrict__ pos, int N, int P, int bits,
+                                    const ZorderSmem& sm) {
   const int tid = threadIdx.x, nt = blockDim.x;
   const int lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
+  float2 p[R];
   float lo0 = INFINITY, lo1 = INFINITY, hi0 = -INFINITY, hi1 = -INFINITY;
-  for (int i = tid; i < N; i += nt) {
-    const float2 p = reinterpret_cast<const float2*>(pos)[i];
-    lo0 = fminf(lo0, p.x); hi0 = fmaxf(hi0, p.x);
-    lo1 = fminf(lo1, p.y); hi1 = fmaxf(hi1, p.y);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int a = tid * R + r;
+    p[r] = make_float2(0.f, 0.f);
+    if (a < N) {
+      p[r] = reinterpret_cast<const float2*>(pos)[a];
+      lo0 = fminf(lo0, p[r].x); hi0 = fmaxf(hi0, p[r].x);
+      lo1 = fminf(lo1, p[r].y); hi1 = fmaxf(hi1, p[r].y);
+    }
   }
+  // every agent is covered: nt * R >= P = next_pow2(N) >= N
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     lo0 = fminf(lo0, __shfl_xor(lo0, o)); hi0 = fmaxf(hi0, __shfl_xor(hi0, o));
@@ -259,13 +272,7 @@ __device__ void morton_order_rank(const float* __restrict__ pos, int N, int P, i
   const MortonQuant mq{lo0, lo1, span0, span1, static_cast<float>(topi), topi};
   // (code << 32 | agent) words, sorted in registers / across lanes, LDS only
   // for the strides that cross wavefronts; padding sorts last
-  const int R = P / nt < 2 ? 2 : P / nt;
-  switch (R) {
-    case 2: morton_sort<2>(pos, N, P, mq, sm.keys); break;
-    case 4: morton_sort<4>(pos, N, P, mq, sm.keys); break;
-    case 8: morton_sort<8>(pos, N, P, mq, sm.keys); break;
-    default: morton_sort<16>(pos, N, P, mq, sm.keys); break;
-  }
+  morton_sort<R>(p, N, P, mq, sm.keys);
   __syncthreads();
   for (int r = tid; r < N; r += nt) {
     const int agent = static_cast<int>(sm.keys[r] & 0xffffffffu);
@@ -273,6 +280,17 @@ __device__ void morton_order_rank(const float* __restrict__ pos, int N, int P, i
     sm.rank[agent] = r;
   }
   __syncthreads();
+}
+
+__device__ void morton_order_rank(const float* __restrict__ pos, int N, int P, int bits,
+                                  const ZorderSmem& sm) {
+  const int R = P / static_cast<int>(blockDim.x) < 2 ? 2 : P / static_cast<int>(blockDim.x);
+  switch (R) {
+    case 2: morton_order_rank_r<2>(pos, N, P, bits, sm); break;
+    case 4: morton_order_rank_r<4>(pos, N, P, bits, sm); break;
+    case 8: morton_order_rank_r<8>(pos, N, P, bits, sm); break;
+    default: morton_order_rank_r<16>(pos, N, P, bits, sm); break;
+  }
 }
 
 __device__ __forceinline__ int window_peer(const ZorderSmem& sm, int i, int j, int k, int N) {
@@ -323,8 +341,8 @@ zorder_attn_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const ZorderSmem sm = zorder_smem(smem_raw, N, P);
   const int b = blockIdx.x;
-  morton_order_rank(pos + static_cast<size_t>(b) * N * 2, N, P, bits, sm);
   const size_t boff = static_cast<size_t>(b) * N * D;
+  morton_order_rank(pos + static_cast<size_t>(b) * N * 2, N, P, bits, sm);
   const int lane = threadIdx.x & 63;
   const int quads = blockDim.x >> 2;
   // several queries per quad per pass: their peer loads overlap
