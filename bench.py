@@ -13,8 +13,9 @@ Alongside, with the reference's protocol (interleaved event timing and graph
 replay, minimum over samples): the dense core, top-k at k=1/2/4, the fixed-set
 kernel given the exact top-k set (selection-time share), the streaming kernel
 at B=256 N=1024, the Z-order select+attend at B=1024 N=512 k=2
-(configs[4]), a bf16 point, the configs[1] sweep over N, the
-pre-score selectors (radius / grid kNN, Morton window) and the launch floor.
+(configs[4]), the configs[2] bf16 grid (B = 1024, 4096), the configs[1] sweep
+over N, the pre-score selectors (radius / grid kNN, Morton window) and the
+launch floor.
 
 Prints ONE JSON line. Exits non-zero (with a message) for --gpus > 1: this
 build measures one GPU.
@@ -335,18 +336,32 @@ def main() -> int:
         del q6, k6, v6, pos6
     detail["prescore_selectors_B256_d16_us"] = sel_rows
 
-    # ---- one bf16 point, B=1024, N=256, d=16 -------------------
-    qb, kb, vb = (t.to(torch.bfloat16) for t in (q, k, v))
-    f3 = {"dense_bf16": lambda: fused_dense_attention(qb, kb, vb)}
-    for kk in (1, 2):
-        f3[f"topk_bf16_k{kk}"] = (lambda kk=kk: topk_attention(qb, kb, vb, kk))
-    s3 = {n: harness.stats(s) for n, s in
-          harness.time_interleaved(harness.as_graphs(f3), args.reps, 5, 2).items()}
-    td = s3["dense_bf16"]["min_us"]
-    detail["bf16_B1024_N256_d16"] = {n: round(s["min_us"], 3) for n, s in s3.items()}
-    detail["bf16_B1024_N256_d16"]["dense_hbm_frac"] = round(
-        harness.analytic_bytes("dense", B, N, D, itemsize=2) / (td * 1e-6)
-        / harness.PEAK_HBM_BYTES_PER_S, 4)
+    # ---- bf16 (inputs N(0,1) cast to bf16, fp32 accumulation),
+    # B in {1024, 4096}, N in {64, 256, 512}, d in {16, 32, 64}; dense on bf16
+    # MFMA with its HBM and MFMA fractions, top-k k = 1, 2 beside it
+    bf16_rows = {}
+    for d3 in (16, 32, 64):
+        for n3 in (64, 256, 512):
+            for b3 in (1024, 4096):
+                g3 = np.random.default_rng(77 + n3 + d3)
+                q3, k3, v3 = (torch.from_numpy(g3.standard_normal((b3, n3, d3)).astype(np.float32))
+                              .to(dev).to(torch.bfloat16) for _ in range(3))
+                f3 = {"dense": bound.dense(q3, k3, v3)}
+                for kk in (1, 2):
+                    f3[f"topk_k{kk}"] = bound.topk(q3, k3, v3, kk)
+                s3 = {n: harness.stats(s)["min_us"] for n, s in
+                      harness.time_interleaved(f3, max(10, args.reps // 4), 3, 2).items()}
+                td = s3["dense"]
+                bf16_rows[f"B{b3}_N{n3}_d{d3}"] = {
+                    **{n: round(t, 3) for n, t in s3.items()},
+                    "dense_hbm_frac": round(harness.analytic_bytes("dense", b3, n3, d3, itemsize=2)
+                                            / (td * 1e-6) / harness.PEAK_HBM_BYTES_PER_S, 4),
+                    "dense_mfma_frac": round(harness.analytic_flops("dense", b3, n3, d3)
+                                             / (td * 1e-6) / harness.PEAK_BF16_FLOPS, 4)}
+                del q3, k3, v3, f3
+    detail["bf16_configs2_us"] = bf16_rows
+    best = max(bf16_rows.items(), key=lambda kv: kv[1]["dense_hbm_frac"])
+    detail["bf16_dense_best_hbm_frac"] = {"shape": best[0], "frac": best[1]["dense_hbm_frac"]}
 
     # ---- the whole AttentionComm forward (qkv Linear, core, gelu, proj) ---
     # the reference's module microbenchmark cell (scripts/microbenchmark_comm.py:

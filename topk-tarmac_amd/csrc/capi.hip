@@ -35,6 +35,7 @@ int hip_status(hipError_t e, const char* what) {
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 constexpr size_t kLdsBudget = 64 * 1024;
+constexpr size_t kBf16TopkLds = 40 * 1024;
 
 float inv_sqrt(int d) { return static_cast<float>(1.0 / std::sqrt(static_cast<double>(d))); }
 
@@ -80,6 +81,11 @@ int topk_common(const void* q, const void* k, const void* v, void* out, int32_t*
   int kc;
   if (key_chunk <= 0) {
     kc = n64 < kmax ? n64 : kmax;
+    // bf16 always runs the register-list kernel: keep its key copy within
+    // 40 KiB so four workgroups share a CU (a whole 512-key row at d = 64
+    // would allow two, and measured 1.4x slower than 256-key chunks)
+    if (dtype == tarmac::kBf16)
+      while (kc > 64 && tarmac::topk_lds_bytes(dtype, d, kc) > kBf16TopkLds) kc -= 64;
   } else {
     if (key_chunk % 16 != 0)
       return fail(TARMAC_ERR_INVALID, "%s: key_chunk must be a multiple of 16 (got %d)", fn, key_chunk);

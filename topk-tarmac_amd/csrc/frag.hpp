@@ -164,15 +164,22 @@ struct FragBf16Wide {
   static constexpr int NI = D / 32;     // 16x16x32 instructions per tile
   static constexpr int LDK = D + 8;
   bf16x8 q[NI];
+  // One 16-byte load per half; the power-of-two rescale is exact, so the
+  // packed round-to-nearest conversion back to bf16 returns x * pre exactly.
   __device__ __forceinline__ void load_q(const bf16* qrow, int grp, float pre) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 #pragma unroll
     for (int h = 0; h < NI; ++h) {
-      const bf16* p = qrow + 32 * h + 8 * grp;
+      const uint4 raw = *reinterpret_cast<const uint4*>(qrow + 32 * h + 8 * grp);
+      const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+      uint32_t o[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        bf16 x = scale_bf16(p[e], pre);
-        q[h][e] = __builtin_bit_cast(__bf16, x);
+      for (int e = 0; e < 4; ++e) {
+        const bf16x2_t y = {static_cast<__bf16>(__uint_as_float(w[e] << 16) * pre),
+                            static_cast<__bf16>(__uint_as_float(w[e] & 0xffff0000u) * pre)};
+        o[e] = __builtin_bit_cast(uint32_t, y);
       }
+      q[h] = __builtin_bit_cast(bf16x8, o);
     }
   }
   struct KF { bf16x8 v[NI]; };
