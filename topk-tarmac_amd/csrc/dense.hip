@@ -218,14 +218,16 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
     // log2-domain logsumexp of the scaled scores, for the backward pass
     if (lse != nullptr && grp == 0)
       lse[static_cast<size_t>(b) * 2 * N + qi] = m_run[qt] * post + log2f(l_tot);
-    // lane l holds O^T[c = 16h + 4*(l/16) + r][q = l%16]
+    // lane l holds O^T[c = 16h + 4*(l/16) + r][q = l%16]; one reciprocal
+    // per row instead of a division per channel
+    const float inv = 1.f / l_tot;
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
       const int cbase = 16 * h + 4 * grp;
       if (cbase < D) {
         float o[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[r] = acc[qt][h][r] / l_tot;
+        for (int r = 0; r < 4; ++r) o[r] = acc[qt][h][r] * inv;
         st_row<T, 4>(O + boff + static_cast<size_t>(qi) * D + cbase, o);
       }
     }
