@@ -36,6 +36,8 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 
 constexpr size_t kLdsBudget = 64 * 1024;
 constexpr size_t kBf16TopkLds = 40 * 1024;
+constexpr int kZorderMaxN = 4096;  // agents per row the Morton selector sorts
+constexpr size_t kZorderLds = 160 * 1024;  // LDS per workgroup on gfx950
 
 float inv_sqrt(int d) { return static_cast<float>(1.0 / std::sqrt(static_cast<double>(d))); }
 
@@ -212,8 +214,9 @@ int tarmac_morton_window(const float* pos, void* idx_out, int idx_dtype, int64_t
       return fail(TARMAC_ERR_INVALID, "%s: idx_out misaligned", fn);
   }
   if (codes_out && !aligned(codes_out, 8)) return fail(TARMAC_ERR_INVALID, "%s: codes_out misaligned", fn);
-  if (tarmac::zorder_lds_bytes(N) > kLdsBudget)
-    return fail(TARMAC_ERR_UNSUPPORTED, "%s: N=%d exceeds the per-row sort capacity", fn, N);
+  if (N > kZorderMaxN || tarmac::zorder_lds_bytes(N) > kZorderLds)
+    return fail(TARMAC_ERR_UNSUPPORTED, "%s: N=%d exceeds the per-row sort capacity (%d)", fn, N,
+                kZorderMaxN);
   tarmac::MortonArgs a{pos, idx_out, idx_dtype == TARMAC_IDX_I64, codes_out, B, N, k, bits, stream};
   return hip_status(tarmac::run_morton_window(a), fn);
 }
@@ -281,8 +284,9 @@ int tarmac_zorder_fwd(const void* q, const void* k, const void* v, const float* 
     return fail(TARMAC_ERR_INVALID, "%s: need 1 <= topk <= N-1 (got topk=%d, N=%d)", fn, topk, N);
   if (bits < 1 || bits > 16) return fail(TARMAC_ERR_INVALID, "%s: bits must be 1..16 (got %d)", fn, bits);
   if (idx_out && !aligned(idx_out, 4)) return fail(TARMAC_ERR_INVALID, "%s: idx_out misaligned", fn);
-  if (tarmac::zorder_lds_bytes(N) > kLdsBudget)
-    return fail(TARMAC_ERR_UNSUPPORTED, "%s: N=%d exceeds the per-row sort capacity", fn, N);
+  if (N > kZorderMaxN || tarmac::zorder_lds_bytes(N) > kZorderLds)
+    return fail(TARMAC_ERR_UNSUPPORTED, "%s: N=%d exceeds the per-row sort capacity (%d)", fn, N,
+                kZorderMaxN);
   tarmac::ZorderArgs a{q, k, v, pos, out, idx_out, B, N, d, topk, bits, dtype, inv_sqrt(d), stream};
   return hip_status(tarmac::run_zorder(a), fn);
 }

@@ -138,4 +138,30 @@ __device__ void block_bitonic_sort(K (&key)[R], K* lds, int P, int t, bool activ
   }
 }
 
+// Bitonic sort (ascending) of 64 * R keys by one wavefront: lane l holds
+// positions l*R .. l*R+R-1. Every stage is a register or lane stage (no LDS,
+// no barrier); sizes and strides are compile-time, so the stages unroll into
+// straight-line code and the R exchanges of a lane stage overlap.
+template <typename K, int R>
+__device__ __forceinline__ void wave_bitonic_sort(K (&key)[R], int lane) {
+  const int base = lane * R;
+#pragma unroll
+  for (int size = 2; size <= 64 * R; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride >= R; stride >>= 1) {
+      if constexpr (R <= 32) {
+        switch (stride / R) {
+          case 1: bitonic_lane_stage<K, R, 1>(key, base, stride, size); break;
+          case 2: bitonic_lane_stage<K, R, 2>(key, base, stride, size); break;
+          case 4: bitonic_lane_stage<K, R, 4>(key, base, stride, size); break;
+          case 8: bitonic_lane_stage<K, R, 8>(key, base, stride, size); break;
+          case 16: bitonic_lane_stage<K, R, 16>(key, base, stride, size); break;
+          default: bitonic_lane_stage<K, R, 32>(key, base, stride, size); break;
+        }
+      }
+    }
+    bitonic_register_stages<K, R>(key, base, size);
+  }
+}
+
 }  // namespace tarmac
