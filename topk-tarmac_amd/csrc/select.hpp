@@ -111,6 +111,22 @@ __device__ __forceinline__ void mask_block(f32x4 (&s)[QT][BT], const bool (&self
   }
 }
 
+// Packed candidates. A score keeps its top 24 bits and carries, in the low 8
+// mantissa bits, the key's position u within the lane's stream (u < 256).
+// Clearing low bits rounds toward zero, a monotone map, so packed order
+// refines the order of the truncated scores and distinct keys give distinct
+// packed values: a scan keeps values only (max / med3) and the key comes back
+// from the bits.
+constexpr uint32_t kLow8 = 0xffu, kLow10 = 0x3ffu;
+constexpr float kMasked = -3.40282347e38f;   // -FLT_MAX: stays finite when packed
+constexpr float kMaskedBelow = -1.0e38f;     // list entries below this are masked keys
+
+// Bits 8..31 from s, bits 0..7 from u (< 256): one v_perm_b32 (the compiler
+// turns the and/or form into two instructions).
+__device__ __forceinline__ float pack8(float s, uint32_t u) {
+  return __uint_as_float(__builtin_amdgcn_perm(__float_as_uint(s), u, 0x07060500u));
+}
+
 // Value-only insertion into a descending list: L max/med3 operations.
 template <int L>
 __device__ __forceinline__ void vinsert(float (&v)[L], float s) {

@@ -544,7 +544,9 @@ static hipError_t launch_small(const TopkArgs& a, int kc) {
   const int qb = per_wave * nw;
   const int n_qblk = (a.N + qb - 1) / qb;
   const int nblocks = a.B * n_qblk;
-  const size_t lds = topk_lds_bytes(a.dtype, a.d, kc);
+  // this kernel's own key copy (topk_lds_bytes also covers the filter
+  // kernel's larger split rows; allocating that would cost occupancy)
+  const size_t lds = plain_lds_bytes(a.dtype, a.d, kc);
   const T* q = static_cast<const T*>(a.q);
   const T* k = static_cast<const T*>(a.k);
   const T* v = static_cast<const T*>(a.v);
@@ -660,10 +662,14 @@ hipError_t run_topk(const TopkArgs& a) {
   return hipErrorInvalidValue;
 }
 
-size_t topk_lds_bytes(int dtype, int d, int kc) {
+size_t plain_lds_bytes(int dtype, int d, int kc) {
   const int row = dtype == kF32 ? (d + 4) * 4 : (d + 8) * 2;
   const int kcb = (kc + kBlockKeys - 1) / kBlockKeys * kBlockKeys;
-  const size_t plain = static_cast<size_t>(kcb) * row;
+  return static_cast<size_t>(kcb) * row;
+}
+
+size_t topk_lds_bytes(int dtype, int d, int kc) {
+  const size_t plain = plain_lds_bytes(dtype, d, kc);
   if (dtype != kF32 || d == 8) return plain;
   const size_t filt = topk_filter_lds_bytes(d, kc);
   return plain > filt ? plain : filt;

@@ -330,24 +330,12 @@ constexpr int kFilterMaxWaves = 8;
 // 16-key tiles per selection block (the unit of masking and packing)
 constexpr int kFilterBlockTiles = 4;
 
-// Packed candidates. During the scan a lane's filter score keeps its top 24
-// bits and carries, in the low 8 mantissa bits, the key's position
-// u = 4 * tile + r within the current 1024-key segment (the lane sees keys
-// seg + 16 * tile + 4 * grp + r, tile < 64, r < 4). Clearing low bits rounds
-// toward zero, a monotone map, so packed order refines the order of the
-// truncated scores and distinct keys give distinct packed values: the scan
-// keeps values only (max / med3) and the key comes back from the bits.
+// Packed candidates (pack8, select.hpp): during the scan a lane's filter
+// score carries the key's position u = 4 * tile + r within the current
+// 1024-key segment (the lane sees keys seg + 16 * tile + 4 * grp + r,
+// tile < 64, r < 4).
 constexpr int kSegKeys = 1024;
-constexpr uint32_t kLow8 = 0xffu, kLow10 = 0x3ffu;
-constexpr float kMasked = -3.40282347e38f;   // -FLT_MAX: stays finite when packed
-constexpr float kMaskedBelow = -1.0e38f;     // list entries below this are masked keys
 constexpr float kNormLimit = 1.329228e36f;   // 2^120: |q| max|k| at or above fails the proof
-
-// Bits 8..31 from s, bits 0..7 from u (< 256): one v_perm_b32 (the compiler
-// turns the and/or form into two instructions).
-__device__ __forceinline__ float pack8(float s, uint32_t u) {
-  return __uint_as_float(__builtin_amdgcn_perm(__float_as_uint(s), u, 0x07060500u));
-}
 
 // Largest value whose truncation (bits `mask` cleared) is at most trunc(t).
 __device__ __forceinline__ float trunc_ceiling(float t, uint32_t mask) {
