@@ -109,6 +109,12 @@ def profile_one(args, q, k, v, dev) -> int:
         idx = bound.topk(q, k, v, 2, with_idx=True)
         idx()
         fn = bound.fixedset(q, k, v, idx.idx)
+    elif name == "dense_bf16":
+        # configs[2] point where bf16 dense is HBM-bound: B=4096, N=64, d=64
+        g = np.random.default_rng(77 + 64 + 64)
+        qb, kb, vb = (torch.from_numpy(g.standard_normal((4096, 64, 64)).astype(np.float32))
+                      .to(dev).to(torch.bfloat16) for _ in range(3))
+        fn = bound.dense(qb, kb, vb)
     elif name == "stream2":
         g = np.random.default_rng(4242)
         q4, k4, v4 = (torch.from_numpy(g.standard_normal((256, 1024, D)).astype(np.float32)).to(dev)
@@ -123,6 +129,12 @@ def profile_one(args, q, k, v, dev) -> int:
     for _ in range(args.warmup + args.steps):
         fn()
     torch.cuda.synchronize()
+    if args.copy_probe:
+        src = torch.ones(16 << 20, device=dev)   # 64 MiB of fp32
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     print(json.dumps({"profiled": name, "calls": args.warmup + args.steps}), flush=True)
     return 0
 
@@ -138,7 +150,8 @@ def main() -> int:
     ap.add_argument("--value-only", action="store_true",
                     help="time only the value kernel (for profiler runs)")
     ap.add_argument("--profile-kernel", default=None,
-                    choices=["dense", "topk1", "topk2", "topk4", "fixedset2", "zorder", "stream2"],
+                    choices=["dense", "dense_bf16", "topk1", "topk2", "topk4", "fixedset2", "zorder",
+                             "stream2"],
                     help="run only this kernel (headline shape; zorder/stream at their configs) "
                          "--warmup + --steps times, for profiler counter passes")
     ap.add_argument("--copy-probe", action="store_true",
