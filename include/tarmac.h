@@ -195,8 +195,8 @@ int tarmac_dense_bwd(const float* q, const float* k, const float* v, const float
  * MFMA, rescore k+1 candidates in the canonical fp32 order and prove the
  * result is the exact top k (16-query tiles where the proof fails recompute
  * in fp32). The result is identical either way; only the time differs.
- * mode: 0 = never, 1 = where it is faster (default: N >= 512, or N >= 256
- * with topk >= 3), 2 = always.
+ * mode: 0 = never, 1 = where it is faster (default: d = 16 with N >= 512,
+ * or N >= 256 with topk >= 3), 2 = always.
  * Process-wide. Returns the previous mode, or -1 (and sets the last error)
  * for an invalid mode. No counterpart in the reference (its kernels have one
  * path).

@@ -635,10 +635,14 @@ static hipError_t dispatch_topk(const TopkArgs& a) {
 int g_topk_filter_mode = kFilterAuto;
 
 // Where the filter-and-verify kernel beats the plain fp32 pass (measured on
-// MI355X, d = 16): its fixed per-query cost (split staging, merge, exact
+// MI355X): at d = 16 its fixed per-query cost (split staging, merge, exact
 // rescoring) pays off once each query scans 512 keys, or 256 keys when the
-// plain pass's per-score selection cost grows with k >= 3.
-static bool filter_pays(const TopkArgs& a) { return a.N >= 512 || (a.N >= 256 && a.topk >= 3); }
+// plain pass's per-score selection cost grows with k >= 3. At d = 32 and 64
+// the six split products per score cost more than the selection they save
+// (N = 512: 1.2x to 1.7x slower than the plain pass), so it is not used.
+static bool filter_pays(const TopkArgs& a) {
+  return a.d == 16 && (a.N >= 512 || (a.N >= 256 && a.topk >= 3));
+}
 
 hipError_t run_topk(const TopkArgs& a) {
   if (a.select == kSelTopk && g_topk_filter_mode != kFilterOff &&

@@ -9,7 +9,8 @@
 //     >= 2^-16, which approximates the fp32 dot to
 //     |a - q.k| <= 2^-21 sum_c |q_c k_c| (representation 2^-22, bf16 MFMA
 //     accumulation measured <= 2^-21.9 of the term magnitudes); the canonical
-//     fp32 dot is within 2^-20 of q.k. Selection runs on packed values (the
+//     fp32 dot is within d 2^-24 sum_c |q_c k_c| of q.k. Selection runs on
+//     packed values (the
 //     filter score with the key's position in its low mantissa bits, see
 //     pack8): each lane keeps its k+2 largest with max / med3 only, and the
 //     four lane lists of a query merge into k+1 candidates plus the (k+2)-th
@@ -17,8 +18,10 @@
 //  2. verify: the k+1 candidates are rescored in the canonical fp32 order and
 //     their exact top k taken. Every other key's filter score is at most C,
 //     the largest value that truncates like the (k+2)-th entry. If C plus
-//     eps = 2^-18 |q| max_j |k_j| (>= the bounds above, with margin), scaled,
-//     is strictly below the k-th exact score, no other key can reach the top
+//     eps |q| max_j |k_j| (eps = filter_eps<d>(), at least the filter's error
+//     plus the canonical chain's d roundings, d 2^-24 sum_c |q_c k_c|, with
+//     margin; sum_c |q_c k_c| <= |q| |k_j|), scaled, is strictly below the
+//     k-th exact score, no other key can reach the top
 //     k, so the result IS the exact top k. Rescoring one spare candidate
 //     settles near-ties between the k-th and (k+1)-th scores (duplicated keys
 //     included) without the fallback.
@@ -301,19 +304,25 @@ __device__ __forceinline__ void exact_tile(const float* __restrict__ Qb,
 
 // Canonical fp32 score of one (query row, key row) pair: fmaf chain with
 // element kk*(D/4)+t at step t, slot kk (the MFMA chain's order), then scaled.
+// Four steps at a time (4-element runs of each quarter row), so at most 32
+// elements are live instead of both whole rows.
 template <int D, bool POW2>
 __device__ __forceinline__ float canon_pair(const float* qrow, const float* krow, float scale) {
-  float q[D], k[D];
-  ld_f32<D>(q, qrow);
-  ld_f32<D>(k, krow);
+  constexpr int QD = D / 4;
   float acc = 0.f;
 #pragma unroll
-  for (int t = 0; t < D / 4; ++t)
+  for (int t0 = 0; t0 < QD; t0 += 4) {
+    float q[4][4], k[4][4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const int c = kk * (D / 4) + t;
-      acc = fmaf(POW2 ? q[c] * scale : q[c], k[c], acc);
+      ld_f32<4>(q[kk], qrow + kk * QD + t0);
+      ld_f32<4>(k[kk], krow + kk * QD + t0);
     }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) acc = fmaf(POW2 ? q[kk][t] * scale : q[kk][t], k[kk][t], acc);
+  }
   return POW2 ? acc : acc * scale;
 }
 
@@ -321,7 +330,13 @@ __device__ __forceinline__ float canon_pair(const float* qrow, const float* krow
 // the kernel
 // ---------------------------------------------------------------------------
 
-constexpr float kFilterEps = 1.0f / 262144.0f;  // 2^-18
+// Slack of the filter proof, relative to |q| max_j |k_j|: at least the
+// filter's error (2^-21) plus the canonical chain's (d 2^-24), with margin
+// for the fp32 arithmetic of the bound itself.
+template <int D>
+constexpr float filter_eps() {
+  return D <= 32 ? 1.0f / 262144.0f : 1.0f / 131072.0f;  // 2^-18, 2^-17
+}
 
 // Waves per workgroup: every wave of a workgroup shares one staged key chunk,
 // so larger groups stage each batch row's keys fewer times and amortise the
@@ -365,8 +380,15 @@ __device__ __forceinline__ void flush_segment(float (&pv)[QT][L], float (&rv)[QT
 
 // ONESEG: one chunk of at most one segment holds every key (kc >= N, N <= 1024),
 // so the lists stay packed until the merge.
+// Waves per SIMD the register budget is sized for: 5 (96 VGPRs); at d = 64
+// the split query and key fragments alone take 72 VGPRs, so 4 (128) there.
+template <int D>
+constexpr int filter_min_waves() {
+  return D == 64 ? 4 : 5;
+}
+
 template <int D, int K, int QT, bool ONESEG>
-__global__ void __launch_bounds__(kFilterMaxWaves * 64, 5)
+__global__ void __launch_bounds__(kFilterMaxWaves * 64, filter_min_waves<D>())
 topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
                    const float* __restrict__ V, float* __restrict__ O, int32_t* __restrict__ Idx,
                    int N, int n_qblk, int kc, float scale, int nblocks) {
@@ -558,7 +580,7 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
 #pragma unroll
     for (int m = 0; m < K; ++m) { val[qt][m] = cv[m]; ix[qt][m] = cand[qt][m]; }
     const float nprod = sqrtf(qn2[qt]) * kmax;
-    const float bound = (ceil_f[qt] + kFilterEps * nprod) * scale;
+    const float bound = (ceil_f[qt] + filter_eps<D>() * nprod) * scale;
     ok[qt] = self[qt] >= N || (nprod < kNormLimit && bound < val[qt][K - 1]);
   }
 
