@@ -12,7 +12,8 @@ aggregation). ``value`` is its device time per call in microseconds.
 Alongside, with the reference's protocol (interleaved event timing and graph
 replay, minimum over samples): the dense core, top-k at k=1/2/4, the fixed-set
 kernel given the exact top-k set (selection-time share), the streaming kernel
-at B=256 N=1024, the Z-order select+attend at B=1024 N=512 k=2
+at B=256 N=1024, the reference's masked-bisection and sort
+selection variants at the metric point, the Z-order select+attend at B=1024 N=512 k=2
 (configs[4]), the configs[2] bf16 grid (B = 1024, 4096), the configs[1] sweep
 over N, the pre-score selectors (radius / grid kNN, Morton window) and the
 launch floor. Streaming and Z-order are single launches here: their headline
@@ -290,6 +291,30 @@ def main() -> int:
                   for n, s in gst.items()},
     }
     del fns, gfns
+
+    # ---- the reference's fused implementations (scripts/bench_attention_core.py:160-170)
+    # at the metric point: gather (the value kernel), masked bisection, sort rule
+    from tarmac.kernels import fused_topk_attention_masked, fused_topk_attention_sort
+    fi = {"dense_fused": lambda: fused_dense_attention(q, k, v)}
+    for kk in KS:
+        fi[f"topk_fused_gather_k{kk}"] = (lambda kk=kk: topk_attention(q, k, v, kk))
+        fi[f"topk_fused_masked_k{kk}"] = (lambda kk=kk: fused_topk_attention_masked(q, k, v, kk))
+        fi[f"topk_fused_sort_k{kk}"] = (lambda kk=kk: fused_topk_attention_sort(q, k, v, kk))
+    si = {n: harness.stats(s) for n, s in
+          harness.time_interleaved(fi, max(10, args.reps // 2), 3, 2).items()}
+    detail["impls_B1024_N256_d16_us"] = {n: round(s["min_us"], 3) for n, s in si.items()}
+    # and at B=256, N=384, k=2, a row of the reference's results/attention_core_sort.json
+    g7 = np.random.default_rng(1234 + 7 * 384 + D)
+    q7, k7, v7 = (torch.from_numpy(g7.standard_normal((256, 384, D)).astype(np.float32)).to(dev)
+                  for _ in range(3))
+    fi = {"dense_fused": lambda: fused_dense_attention(q7, k7, v7),
+          "topk_fused_gather": lambda: topk_attention(q7, k7, v7, 2),
+          "topk_fused_masked": lambda: fused_topk_attention_masked(q7, k7, v7, 2),
+          "topk_fused_sort": lambda: fused_topk_attention_sort(q7, k7, v7, 2)}
+    si = {n: harness.stats(s) for n, s in
+          harness.time_interleaved(fi, max(10, args.reps // 2), 3, 2).items()}
+    detail["impls_B256_N384_d16_k2_us"] = {n: round(s["min_us"], 3) for n, s in si.items()}
+    del fi, q7, k7, v7
 
     # ---- streaming top-k, B=256, N=1024 ------------------------
     b4, n4 = 256, 1024
