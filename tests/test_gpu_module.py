@@ -117,3 +117,18 @@ def test_module_backward_matches_torch_autograd(golden, mode, k):
         got, want = p.grad.cpu().numpy(), W[name].grad.numpy()
         assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max(), name
     assert np.abs(x.grad.cpu().numpy() - xr.grad.numpy()).max() <= 1e-4 * xr.grad.abs().max().item()
+
+
+@pytest.mark.parametrize("mode,k", [("dense", 0), ("topk_gather", 2), ("zorder_k", 2)])
+def test_module_empty_batch(golden, mode, k):
+    """An empty batch of episodes passes through the module (forward and
+    backward) with correctly shaped empty results."""
+    tag = "comm_n6_d16"
+    mod = _module(mode, k, 6, 16, golden, tag).train()
+    mod.collect_info = False
+    x = torch.zeros(0, 6, 32, device="cuda", requires_grad=True)
+    pos = torch.zeros(0, 6, 2, device="cuda")
+    out, _ = mod(x, pos if mode == "zorder_k" else None)
+    assert out.shape[:2] == (0, 6)
+    out.sum().backward()
+    assert x.grad.shape == (0, 6, 32)

@@ -309,3 +309,37 @@ def test_variant_argument_errors():
         topk_variant_attention(q, k, v, 2, 7)
     with pytest.raises(ValueError, match="bisect"):
         topk_variant_attention(q, k, v, 2, _lib.VARIANT_MASKED, bisect=-1)
+
+
+def test_empty_batch_returns_empty_outputs():
+    """B = 0: every entry point returns correctly shaped empty outputs (as the
+    reference's torch compositions do) without launching anything."""
+    from tarmac.kernels import (fused_dense_attention, fused_prescore_attention,
+                                fused_topk_attention_masked, fused_topk_attention_sort,
+                                select_grid_knn, select_morton_window, select_radius_knn,
+                                zorder_attention)
+    from tarmac.kernels.backward import (dense_attention_backward,
+                                         dense_attention_forward_stats,
+                                         fixedset_attention_backward)
+    from tarmac.kernels.prescore_selection import _morton_code
+    q = torch.zeros(0, 6, 16, device="cuda")
+    pos = torch.zeros(0, 6, 2, device="cuda")
+    idx = torch.zeros(0, 6, 2, dtype=torch.int32, device="cuda")
+    from tarmac.kernels import topk_attention
+    out, ix = topk_attention(q, q, q, 2, return_indices=True)
+    assert out.shape == (0, 6, 16) and ix.shape == (0, 6, 2)
+    assert topk_attention(q, q, q, 2, key_chunk=64).shape == (0, 6, 16)
+    assert fused_dense_attention(q, q, q).shape == (0, 6, 16)
+    assert fused_topk_attention_masked(q, q, q, 2).shape == (0, 6, 16)
+    assert fused_topk_attention_sort(q, q, q, 2).shape == (0, 6, 16)
+    assert fused_prescore_attention(q, q, q, idx).shape == (0, 6, 16)
+    assert zorder_attention(q, q, q, pos, 2, 16).shape == (0, 6, 16)
+    assert select_morton_window(pos, 2).shape == (0, 6, 2)
+    assert _morton_code(pos).shape == (0, 6)
+    assert select_radius_knn(pos, 2).shape == (0, 6, 2)
+    assert select_grid_knn(pos, 2).shape == (0, 6, 2)
+    o, st = dense_attention_forward_stats(q, q, q)
+    assert o.shape == (0, 6, 16) and st.shape == (0, 2, 6)
+    assert all(t.shape == (0, 6, 16) for t in dense_attention_backward(q, q, q, o, q, st))
+    assert all(t.shape == (0, 6, 16) for t in fixedset_attention_backward(q, q, q, idx, q))
+    torch.cuda.synchronize()

@@ -44,6 +44,8 @@ def fixedset_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tenso
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
+    if B == 0:  # an empty batch: nothing to launch
+        return dq, dk, dv
     with torch.cuda.device(q.device):
         rc = _lib.LIB.tarmac_fixedset_bwd(
             _launch.ptr(q), _launch.ptr(k), _launch.ptr(v), _launch.ptr(dout), _launch.ptr(idx),
@@ -62,6 +64,8 @@ def dense_attention_forward_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
     B, N, d = q.shape
     out = torch.empty_like(q)
     stats = torch.empty(B, 2, N, device=q.device, dtype=torch.float32)
+    if B == 0:
+        return out, stats
     with torch.cuda.device(q.device):
         _lib.check(_lib.LIB.tarmac_dense_fwd_stats(
             _launch.ptr(q), _launch.ptr(k), _launch.ptr(v), _launch.ptr(out), _launch.ptr(stats),
@@ -89,6 +93,8 @@ def dense_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             raise ValueError("stats must be the contiguous fp32 [B, 2, N] tensor of the forward")
     else:
         stats = torch.empty(B, 2, N, device=q.device, dtype=torch.float32)
+    if B == 0:
+        return dq, dk, dv
     with torch.cuda.device(q.device):
         rc = _lib.LIB.tarmac_dense_bwd(
             _launch.ptr(q), _launch.ptr(k), _launch.ptr(v), _launch.ptr(out), _launch.ptr(dout),

@@ -34,6 +34,8 @@ def fused_dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     B, N, d = q.shape
     out = torch.empty_like(q)
     chunk = 0 if block_kn is None else -(-int(block_kn) // 16) * 16
+    if B == 0:  # an empty batch: nothing to launch
+        return out
     with torch.cuda.device(q.device):
         _lib.check(_lib.LIB.tarmac_dense_fwd(
             _launch.ptr(q), _launch.ptr(k), _launch.ptr(v), _launch.ptr(out),

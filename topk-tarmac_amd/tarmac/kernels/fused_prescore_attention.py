@@ -32,6 +32,8 @@ def fused_prescore_attention(q: torch.Tensor, k: torch.Tensor,
         idx, code = idx.to(torch.int32), _lib.IDX_I32
     idx = _launch.ready(idx, 8)
     out = torch.empty_like(q)
+    if B == 0:  # an empty batch: nothing to launch
+        return out
     with torch.cuda.device(q.device):
         _lib.check(_lib.LIB.tarmac_fixedset_fwd(
             _launch.ptr(q), _launch.ptr(k), _launch.ptr(v), _launch.ptr(idx), code,

@@ -42,6 +42,8 @@ def topk_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, topk: int,
     kk = max(1, min(int(topk), N - 1))
     out = torch.empty_like(q)
     idx = torch.empty(B, N, kk, device=q.device, dtype=torch.int32) if return_indices else None
+    if B == 0:  # an empty batch: nothing to launch
+        return (out, idx) if return_indices else out
     with torch.cuda.device(q.device):
         if key_chunk is None:
             rc = _lib.LIB.tarmac_topk_fused_fwd(
@@ -94,6 +96,8 @@ def topk_variant_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, to
     kk = max(1, min(int(topk), N - 1))
     out = torch.empty_like(q)
     idx = torch.empty(B, N, kk, device=q.device, dtype=torch.int32) if return_indices else None
+    if B == 0:
+        return (out, idx) if return_indices else out
     with torch.cuda.device(q.device):
         rc = _lib.LIB.tarmac_topk_variant_fwd(
             _launch.ptr(q), _launch.ptr(k), _launch.ptr(v), _launch.ptr(out), _launch.ptr(idx),

@@ -45,6 +45,8 @@ def _morton_code(pos: torch.Tensor, bits: int = 10) -> torch.Tensor:
     pos = _pos(pos)
     B, N, _ = pos.shape
     codes = torch.empty(B, N, device=pos.device, dtype=torch.int64)
+    if B == 0:  # an empty batch: nothing to launch
+        return codes
     with torch.cuda.device(pos.device):
         _lib.check(_lib.LIB.tarmac_morton_window(
             _launch.ptr(pos), _launch.ptr(None), _lib.IDX_I64, _launch.ptr(codes),
@@ -57,6 +59,8 @@ def select_morton_window(pos: torch.Tensor, k: int, bits: int = 10) -> torch.Ten
     pos = _pos(pos)
     B, N, _ = pos.shape
     idx = torch.empty(B, N, k, device=pos.device, dtype=torch.int64)
+    if B == 0:
+        return idx
     with torch.cuda.device(pos.device):
         _lib.check(_lib.LIB.tarmac_morton_window(
             _launch.ptr(pos), _launch.ptr(idx), _lib.IDX_I64, _launch.ptr(None),
@@ -68,6 +72,8 @@ def _knn(fn, pos: torch.Tensor, k: int) -> torch.Tensor:
     pos = _pos(pos)
     B, N, _ = pos.shape
     idx = torch.empty(B, N, int(k), device=pos.device, dtype=torch.int64)
+    if B == 0:
+        return idx
     with torch.cuda.device(pos.device):
         _lib.check(fn(_launch.ptr(pos), _launch.ptr(idx), _lib.IDX_I64, B, N, int(k),
                       _launch.stream(pos)))
@@ -118,6 +124,8 @@ def zorder_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: tor
         raise ValueError("pos must be [B, N, 2] matching q")
     out = torch.empty_like(q)
     idx = torch.empty(B, N, topk, device=q.device, dtype=torch.int32) if return_indices else None
+    if B == 0:
+        return (out, idx) if return_indices else out
     with torch.cuda.device(q.device):
         _lib.check(_lib.LIB.tarmac_zorder_fwd(
             _launch.ptr(q), _launch.ptr(k), _launch.ptr(v), _launch.ptr(pos), _launch.ptr(out),
