@@ -27,6 +27,11 @@ __device__ __forceinline__ float vmax(float a, float b) {
   return __builtin_amdgcn_fmed3f(a, b, opaque_inf());
 }
 
+// min(a, b) as one v_med3_f32 against an opaque -inf (see vmax).
+__device__ __forceinline__ float vmin(float a, float b) {
+  return __builtin_amdgcn_fmed3f(a, b, -opaque_inf());
+}
+
 template <int K>
 __device__ __forceinline__ void topk_insert(float (&val)[K], int (&ix)[K], float s, int j) {
   // New keys arrive in ascending index order, so a strict '>' keeps the

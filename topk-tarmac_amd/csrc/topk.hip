@@ -16,7 +16,8 @@
 //     see disjoint interleaved key subsets of one query, each in ascending key
 //     order;
 //   * every lane keeps a sorted (score desc, index asc) list of its best k in
-//     registers; strict '>' insertion keeps the lower index on ties;
+//     registers; strict '>' insertion keeps the lower index on ties (bf16
+//     inputs with k <= 2 select by lane group instead: group_insert);
 //   * two xor-shuffle merge steps (16, 32) combine the four lists, after which
 //     the 4 lanes of a query each compute d/4 output channels from the k
 //     gathered V rows.
@@ -29,6 +30,69 @@
 #include "tarmac_internal.hpp"
 
 namespace tarmac {
+
+// bf16 inputs, k <= 2: selection by lane group. A lane's four scores of one
+// 16-key tile (rows r = 0..3) carry r in their low 2 mantissa bits (a
+// truncation of at most 2^-21 of the score, below the bf16 MFMA's own
+// accumulation error), so a tile's best (and second best) come from
+// max3 / min without index bookkeeping, and only whole groups enter the
+// running state: the best group's max and second, the second group's max,
+// and their tiles. The two best scores of everything seen are among those
+// three values. 2.25 (k = 1) and 4.75 (k = 2) VALU operations per score
+// instead of 3 and 7 for per-score insertion.
+struct GroupTop2 {
+  float v1, s1, v2;  // packed values
+  int i1, i2;        // tile offsets (16 t) of the best and second groups
+};
+
+__device__ __forceinline__ float pack_row(float s, uint32_t r) {
+  return __uint_as_float((__float_as_uint(s) & ~3u) | r);
+}
+
+template <int K>
+__device__ __forceinline__ void group_insert(GroupTop2& g, const f32x4& s, int tile_off) {
+  const float p0 = pack_row(s[0], 0u), p1 = pack_row(s[1], 1u);
+  const float p2 = pack_row(s[2], 2u), p3 = pack_row(s[3], 3u);
+  if constexpr (K == 1) {
+    const float m = vmax(vmax(p0, p1), vmax(p2, p3));
+    const bool c = m > g.v1;
+    g.v1 = vmax(g.v1, m);
+    g.i1 = c ? tile_off : g.i1;
+  } else {
+    const float hi_a = vmax(p0, p1), lo_a = vmin(p0, p1);
+    const float hi_b = vmax(p2, p3), lo_b = vmin(p2, p3);
+    const float m = vmax(hi_a, hi_b);
+    // second of the four: the middle of (hi_a, hi_b, max(lo_a, lo_b)), as
+    // that max never exceeds max(hi_a, hi_b)
+    const float sec = __builtin_amdgcn_fmed3f(vmax(lo_a, lo_b), hi_a, hi_b);
+    const bool c1 = m > g.v1, c2 = m > g.v2;
+    g.v2 = __builtin_amdgcn_fmed3f(g.v1, g.v2, m);
+    // two plain selects (a nested conditional compiles to a branch)
+    const int i2 = c2 ? tile_off : g.i2;
+    g.i2 = c1 ? g.i1 : i2;
+    g.v1 = vmax(g.v1, m);
+    g.i1 = c1 ? tile_off : g.i1;
+    g.s1 = c1 ? sec : g.s1;
+  }
+}
+
+// The lane's best K as (value, relative index) lists, values with the row
+// bits cleared.
+template <int K>
+__device__ __forceinline__ void group_to_list(const GroupTop2& g, float (&val)[K], int (&ix)[K]) {
+  const int r1 = static_cast<int>(__float_as_uint(g.v1) & 3u);
+  val[0] = __uint_as_float(__float_as_uint(g.v1) & ~3u);
+  ix[0] = g.i1 + r1;
+  if constexpr (K == 2) {
+    const int ia = g.i1 + static_cast<int>(__float_as_uint(g.s1) & 3u);
+    const int ib = g.i2 + static_cast<int>(__float_as_uint(g.v2) & 3u);
+    const float va = __uint_as_float(__float_as_uint(g.s1) & ~3u);
+    const float vb = __uint_as_float(__float_as_uint(g.v2) & ~3u);
+    const bool b_first = ranks_before(vb, ib, va, ia);
+    val[1] = b_first ? vb : va;
+    ix[1] = b_first ? ib : ia;
+  }
+}
 
 template <typename T, int D, int K, int QT>
 __global__ void __launch_bounds__(256)
@@ -64,6 +128,11 @@ topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __
   for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
     for (int m = 0; m < K; ++m) { val[qt][m] = -INFINITY; ix[qt][m] = kIdxSentinel; }
+  // bf16, k <= 2: selection by lane group (group_insert)
+  constexpr bool GROUP = sizeof(T) == 2 && K <= 2;
+  GroupTop2 g[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) g[qt] = {-INFINITY, -INFINITY, -INFINITY, kIdxSentinel, kIdxSentinel};
 
   bool self_r[4];  // element r of a diagonal tile is this lane's self pair
 #pragma unroll
@@ -85,16 +154,41 @@ topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __
       const int kabs = c0 + kb0;
       f32x4 s[QT][BT];
       block_scores<F, QT, BT>(frag, Ks, kb0, LDK, lane, s);
-      prepare_block<QT, BT, POW2>(s, scale, self_r, q0, kabs, kend, grp);
-      rebase_list<QT, K>(ix, kabs - base);
-      base = kabs;
+      if constexpr (GROUP) {
+        if constexpr (!POW2) {
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt)
+          for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-        for (int t = 0; t < BT; ++t)
+            for (int t = 0; t < BT; ++t) s[qt][t] *= scale;
+        }
+        // finite mask: the row bits must not turn it into a NaN
+        mask_block<QT, BT>(s, self_r, q0, kabs, kend, grp, kMasked);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) topk_insert<K>(val[qt], ix[qt], s[qt][t][r], 16 * t + r);
+        for (int qt = 0; qt < QT; ++qt) {
+          g[qt].i1 -= kabs - base;
+          g[qt].i2 -= kabs - base;
+        }
+        base = kabs;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+          for (int t = 0; t < BT; ++t) group_insert<K>(g[qt], s[qt][t], 16 * t);
+      } else {
+        prepare_block<QT, BT, POW2>(s, scale, self_r, q0, kabs, kend, grp);
+        rebase_list<QT, K>(ix, kabs - base);
+        base = kabs;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+          for (int t = 0; t < BT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) topk_insert<K>(val[qt], ix[qt], s[qt][t][r], 16 * t + r);
+      }
     }
+  }
+  if constexpr (GROUP) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) group_to_list<K>(g[qt], val[qt], ix[qt]);
   }
   rebase_list<QT, K>(ix, -base);  // back to absolute key indices
   if (q0 >= N) return;
