@@ -12,9 +12,10 @@ aggregation). ``value`` is its device time per call in microseconds.
 Alongside, with the reference's protocol (interleaved event timing and graph
 replay, minimum over samples): the dense core, top-k at k=1/2/4, the fixed-set
 kernel given the exact top-k set (selection-time share), the streaming kernel
-at B=256 N=1024, the reference's masked-bisection and sort
+at B=256 N=512 and 1024, fp32 and bf16, the reference's masked-bisection and sort
 selection variants at the metric point, the Z-order select+attend at B=1024 N=512 k=2
-(configs[4]), the configs[2] bf16 grid (B = 1024, 4096), the configs[1] sweep
+(configs[4]), the configs[0] MPE n6 shape with the CPU oracle beside it, the
+configs[2] bf16 grid (B = 32 to 4096, k = 1, 2, 4), the configs[1] sweep
 over N, the pre-score selectors (radius / grid kNN, Morton window) and the
 launch floor. Streaming and Z-order are single launches here: their headline
 figures are eager event timings, with the graph replays alongside
@@ -43,7 +44,8 @@ KS = (1, 2, 4)
 VALUE_K = 2
 # The kernel the value call dispatches to at this shape (fp32, d=16, k=2,
 # N=256: the plain fp32 pass; the filter-and-verify kernel takes over at
-# N >= 512). Its launch is what rocprofv3 reports under this name.
+# k >= 3, or N >= 512 with large batches). Its launch is what rocprofv3
+# reports under this name.
 VALUE_KERNEL = "tarmac::topk_small_kernel<float, 16, 2, 2>"
 METRIC_FALLBACK = "µs/call attention core, top-k vs dense ratio, N=256 d=16 k=1,2,4; %HBM peak"
 
@@ -316,32 +318,39 @@ def main() -> int:
     detail["impls_B256_N384_d16_k2_us"] = {n: round(s["min_us"], 3) for n, s in si.items()}
     del fi, q7, k7, v7
 
-    # ---- streaming top-k, B=256, N=1024 ------------------------
-    b4, n4 = 256, 1024
-    g4 = np.random.default_rng(4242)
-    q4, k4, v4 = (torch.from_numpy(g4.standard_normal((b4, n4, D)).astype(np.float32)).to(dev)
-                  for _ in range(3))
+    # ---- streaming top-k, B=256, N in {512, 1024}, fp32 and bf16
     from tarmac.kernels import streaming_topk_attention
-    f4 = {"dense": lambda: fused_dense_attention(q4, k4, v4)}
-    for kk in KS:
-        # the API default key chunk (the largest that fits LDS), and the
-        # reference's 256-key tile
-        f4[f"stream_k{kk}"] = (lambda kk=kk: streaming_topk_attention(q4, k4, v4, kk))
-        f4[f"stream_k{kk}_chunk256"] = (lambda kk=kk: streaming_topk_attention(q4, k4, v4, kk,
-                                                                               block_n=256))
-    # each call is one launch: eager event timing is the device time of that
-    # launch; graph replay (kept for reference) adds a fixed cost on this stack
-    s4 = {n: harness.stats(s) for n, s in
-          harness.time_interleaved(f4, args.reps, 5, 2).items()}
-    s4g = {n: harness.stats(s) for n, s in
-           harness.time_interleaved(harness.as_graphs(f4), args.reps, 5, 2).items()}
-    detail["streaming_B256_N1024"] = {
-        n: round(s["min_us"], 3) for n, s in s4.items()}
-    detail["streaming_B256_N1024"].update(
-        {f"ratio_k{kk}": round(s4[f"stream_k{kk}"]["min_us"] / s4["dense"]["min_us"], 4)
-         for kk in KS})
-    detail["streaming_B256_N1024"]["graph_us"] = {n: round(s["min_us"], 3) for n, s in s4g.items()}
-    del q4, k4, v4, f4
+    b4 = 256
+    for n4 in (512, 1024):
+        g4 = np.random.default_rng(4242 if n4 == 1024 else 4242 + n4)
+        base4 = [torch.from_numpy(g4.standard_normal((b4, n4, D)).astype(np.float32)).to(dev)
+                 for _ in range(3)]
+        for dt in (torch.float32, torch.bfloat16):
+            q4, k4, v4 = (t.to(dt) for t in base4)
+            f4 = {"dense": lambda: fused_dense_attention(q4, k4, v4)}
+            for kk in KS:
+                # the API default key chunk (the largest that fits LDS), and
+                # (fp32) the reference's 256-key tile
+                f4[f"stream_k{kk}"] = (lambda kk=kk: streaming_topk_attention(q4, k4, v4, kk))
+                if dt == torch.float32:
+                    f4[f"stream_k{kk}_chunk256"] = (
+                        lambda kk=kk: streaming_topk_attention(q4, k4, v4, kk, block_n=256))
+            # each call is one launch: eager event timing is the device time of
+            # that launch; graph replay (kept for reference) adds a fixed cost
+            s4 = {n: harness.stats(s) for n, s in
+                  harness.time_interleaved(f4, args.reps, 5, 2).items()}
+            key = (f"streaming_B256_N{n4}" if dt == torch.float32
+                   else f"streaming_bf16_B256_N{n4}")
+            detail[key] = {n: round(s["min_us"], 3) for n, s in s4.items()}
+            detail[key].update(
+                {f"ratio_k{kk}": round(s4[f"stream_k{kk}"]["min_us"] / s4["dense"]["min_us"], 4)
+                 for kk in KS})
+            if dt == torch.float32 and n4 == 1024:
+                s4g = {n: harness.stats(s) for n, s in
+                       harness.time_interleaved(harness.as_graphs(f4), args.reps, 5, 2).items()}
+                detail[key]["graph_us"] = {n: round(s["min_us"], 3) for n, s in s4g.items()}
+            del q4, k4, v4, f4
+        del base4
 
     # ---- Z-order select+attend, B=1024, N=512, k=2, 16 bits ---
     b5, n5, k5 = 1024, 512, 2
@@ -384,18 +393,43 @@ def main() -> int:
         del q6, k6, v6, pos6
     detail["prescore_selectors_B256_d16_us"] = sel_rows
 
+    # ---- the MPE n6 shape (fp32, B=256, N=6, d=16, k=2), which
+    # the reference runs on its CPU path; the numpy oracle is timed beside it
+    # (one thread, the whole batch) unless --no-cpu
+    g0 = np.random.default_rng(1234 + 7 * 6 + D)
+    base0 = [g0.standard_normal((256, 6, D)).astype(np.float32) for _ in range(3)]
+    q0, k0, v0 = (torch.from_numpy(x).to(dev) for x in base0)
+    f0 = {"dense": bound.dense(q0, k0, v0), "topk_k2": bound.topk(q0, k0, v0, 2)}
+    s0 = {n: harness.stats(s)["min_us"] for n, s in
+          harness.time_interleaved(f0, args.reps, 5, 2).items()}
+    row0 = {f"{n}_us": round(t, 3) for n, t in s0.items()}
+    if not args.no_cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import tarmac_oracle as O
+        from threadpoolctl import threadpool_limits
+        with threadpool_limits(1):
+            O.topk_gather(*base0, 2)
+            t_cpu = []
+            for _ in range(30):
+                t1 = time.perf_counter()
+                O.topk_gather(*base0, 2)
+                t_cpu.append(time.perf_counter() - t1)
+        row0["cpu_oracle_topk_k2_us"] = round(min(t_cpu) * 1e6, 3)
+    detail["configs0_B256_N6_d16_k2"] = row0
+    del q0, k0, v0, f0, base0
+
     # ---- bf16 (inputs N(0,1) cast to bf16, fp32 accumulation),
-    # B in {1024, 4096}, N in {64, 256, 512}, d in {16, 32, 64}; dense on bf16
-    # MFMA with its HBM and MFMA fractions, top-k k = 1, 2 beside it
+    # B in {32, 256, 1024, 4096}, N in {64, 256, 512}, d in {16, 32, 64}; dense
+    # on bf16 MFMA with its HBM and MFMA fractions, top-k k = 1, 2, 4 beside it
     bf16_rows = {}
     for d3 in (16, 32, 64):
         for n3 in (64, 256, 512):
-            for b3 in (1024, 4096):
+            for b3 in (32, 256, 1024, 4096):
                 g3 = np.random.default_rng(77 + n3 + d3)
                 q3, k3, v3 = (torch.from_numpy(g3.standard_normal((b3, n3, d3)).astype(np.float32))
                               .to(dev).to(torch.bfloat16) for _ in range(3))
                 f3 = {"dense": bound.dense(q3, k3, v3)}
-                for kk in (1, 2):
+                for kk in KS:
                     f3[f"topk_k{kk}"] = bound.topk(q3, k3, v3, kk)
                 s3 = {n: harness.stats(s)["min_us"] for n, s in
                       harness.time_interleaved(f3, max(10, args.reps // 4), 3, 2).items()}

@@ -195,8 +195,11 @@ int tarmac_dense_bwd(const float* q, const float* k, const float* v, const float
  * MFMA, rescore k+1 candidates in the canonical fp32 order and prove the
  * result is the exact top k (16-query tiles where the proof fails recompute
  * in fp32). The result is identical either way; only the time differs.
- * mode: 0 = never, 1 = where it is faster (default: d = 16 with N >= 512,
- * or N >= 256 with topk >= 3), 2 = always.
+ * mode: 0 = never, 1 = where it is faster (default: d = 16 with N >= 256
+ * and topk >= 3, or N >= 512 and B * N >= 131072), 2 = always. bf16 inputs at d = 16 have the
+ * same kernel with one bf16 product per score (used from topk = 4 and
+ * N = 256 in mode 1); it selects the exact top k of the canonical fp32 scores of the inputs
+ * converted to fp32.
  * Process-wide. Returns the previous mode, or -1 (and sets the last error)
  * for an invalid mode. No counterpart in the reference (its kernels have one
  * path).

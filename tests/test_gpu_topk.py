@@ -6,7 +6,9 @@ for k <= 8; outputs within 1e-5 of max|ref| (normwise relative) against the
 float64 restatement of the reference's gather path wherever the k-th score is
 not a near-tie. bf16 bar: every retained set is admissible under the bf16-MFMA
 score error bound, and outputs are within 1e-2 of max|ref| against a float64
-evaluation over the kernel's own retained set.
+evaluation over the kernel's own retained set; where bf16 runs the
+filter-and-verify kernel (d = 16, k >= 4, or forced), retained indices are
+bit-exact against the canonical-order C oracle on the bf16-rounded inputs.
 """
 
 from __future__ import annotations
@@ -183,6 +185,53 @@ def test_topk_bf16(N, d, kk):
     ref = O.prescore_attention(qb.astype(np.float64), kb.astype(np.float64),
                                vb.astype(np.float64), idx.astype(np.int64))
     assert np.abs(out - ref).max() <= BF16_TOL * np.abs(ref).max()
+
+
+def run_topk_bf16(q, k, v, kk, chunk=None):
+    from tarmac.kernels import topk_attention
+    qd, kd, vd = dev(q, k, v, dtype=torch.bfloat16)
+    out, idx = topk_attention(qd, kd, vd, kk, return_indices=True, key_chunk=chunk)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy(), idx.cpu().numpy()
+
+
+def check_bf16_exact(q, k, v, kk, out, idx):
+    """The bf16 filter-and-verify path (d = 16) selects the exact top k of the
+    canonical fp32 scores of the inputs converted to fp32: indices bit-exact
+    against the C oracle on the bf16-rounded inputs, outputs within 1e-2."""
+    qb, kb, vb = (O.bf16_round(x) for x in (q, k, v))
+    out_c, idx_c = O.canon_topk(qb, kb, vb, kk)
+    assert np.array_equal(idx, idx_c), "bf16 retained indices differ from the canonical oracle"
+    assert np.abs(out - out_c).max() <= BF16_TOL * max(np.abs(out_c).max(), 1e-30)
+
+
+@pytest.mark.parametrize("N,kk,chunk", [(256, 4, None), (256, 8, None), (512, 5, None),
+                                        (1024, 4, None), (700, 6, 128), (1500, 4, 256)])
+def test_topk_bf16_filter_exact(N, kk, chunk):
+    """bf16, d = 16, k >= 4, N >= 256 runs filter-and-verify by default: exact."""
+    B = 4
+    q, k, v = qkv(91 + 3 * N + kk, B, N, 16)
+    out, idx = run_topk_bf16(q, k, v, kk, chunk)
+    check_bf16_exact(q, k, v, kk, out, idx)
+
+
+@pytest.mark.parametrize("N", [6, 64, 256, 1024])
+def test_topk_bf16_filter_forced_exact_with_ties(N, filter_always):
+    """Forced for every k at d = 16 (k <= 2 included), with duplicated keys,
+    zero and repeated queries and near-tied key clusters: still exact."""
+    B = 3
+    q, k, v = (O.bf16_round(x) for x in qkv(300 + N, B, N, 16))
+    k[:, 1::2] = k[:, 0::2]
+    q[:, :8] = 0.0
+    q[:, 8:16] = q[:, 8:9]
+    rng = np.random.default_rng(N)
+    for c0 in range(2, N - 20, 61):
+        k[:, c0 + 1:c0 + 12] = O.bf16_round(k[:, c0:c0 + 1] * (1.0 + 2.0 ** -7 *
+                                            rng.integers(-1, 2, (B, 11, 16))))
+    for kk in (1, 2, 4, 8):
+        if kk < N:
+            out, idx = run_topk_bf16(q, k, v, kk)
+            check_bf16_exact(q, k, v, kk, out, idx)
 
 
 @pytest.mark.parametrize("N,d,kk,chunk", [(256, 16, 1, None), (256, 16, 2, None), (384, 32, 4, None),

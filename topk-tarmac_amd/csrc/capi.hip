@@ -83,9 +83,9 @@ int topk_common(const void* q, const void* k, const void* v, void* out, int32_t*
   int kc;
   if (key_chunk <= 0) {
     kc = n64 < kmax ? n64 : kmax;
-    // bf16 always runs the register-list kernel: keep its key copy within
-    // 40 KiB so four workgroups share a CU (a whole 512-key row at d = 64
-    // would allow two, and measured 1.4x slower than 256-key chunks)
+    // bf16: keep the key copy within 40 KiB so four workgroups share a CU (a
+    // whole 512-key row at d = 64 would allow two, and measured 1.4x slower
+    // than 256-key chunks in the register-list kernel)
     if (dtype == tarmac::kBf16)
       while (kc > 64 && tarmac::topk_lds_bytes(dtype, d, kc) > kBf16TopkLds) kc -= 64;
   } else {

@@ -21,6 +21,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t bf16;  // raw bfloat16 storage
 
 constexpr int kWave = 64;
+constexpr int kCUs = 256;  // compute units of an MI355X (8 XCDs x 32)
 
 __device__ __forceinline__ float bf16_to_f32(bf16 h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);

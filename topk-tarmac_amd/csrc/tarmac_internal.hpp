@@ -141,7 +141,7 @@ int knn_grid_threads(int N);
 
 size_t topk_lds_bytes(int dtype, int d, int kc);
 size_t plain_lds_bytes(int dtype, int d, int kc);  // topk_small_kernel's key copy
-size_t topk_filter_lds_bytes(int d, int kc);
+size_t topk_filter_lds_bytes(int dtype, int d, int kc);
 size_t dense_lds_bytes(int dtype, int d, int kc);
 size_t zorder_lds_bytes(int N);
 size_t knn_radius_lds_bytes(int N);

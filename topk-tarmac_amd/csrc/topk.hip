@@ -728,14 +728,24 @@ static hipError_t dispatch_topk(const TopkArgs& a) {
 
 int g_topk_filter_mode = kFilterAuto;
 
-// Where the filter-and-verify kernel beats the plain fp32 pass (measured on
-// MI355X): at d = 16 its fixed per-query cost (split staging, merge, exact
-// rescoring) pays off once each query scans 512 keys, or 256 keys when the
-// plain pass's per-score selection cost grows with k >= 3. At d = 32 and 64
-// the six split products per score cost more than the selection they save
-// (N = 512: 1.2x to 1.7x slower than the plain pass), so it is not used.
+// Where the filter-and-verify kernel beats the plain pass (measured on
+// MI355X). fp32: at d = 16 its fixed per-query cost (split staging, merge,
+// exact rescoring) pays off once each query scans 512 keys, or 256 keys when
+// the plain pass's per-score selection cost grows with k >= 3; at d = 32 and
+// 64 the six split products per score cost more than the selection they save
+// (N = 512: 1.2x to 1.7x slower), so it is not used. bf16 (d = 16): from
+// k = 4 and N = 256, where the plain pass's per-score insertion (15
+// operations) costs more than the filter's overhead (N = 256 to 1024: 8 to
+// 37% faster; 14% slower at N = 64); k <= 2 keeps the plain pass's group
+// selection.
+// At k <= 2 the fp32 filter also needs a large batch: with few workgroups
+// its longer per-wave chain (merge, rescoring) is not hidden (N = 512, B = 64:
+// 18.4 vs 16.0 us; B = 256: 35.0 vs 38.9 us).
 static bool filter_pays(const TopkArgs& a) {
-  return a.d == 16 && (a.N >= 512 || (a.N >= 256 && a.topk >= 3));
+  if (a.dtype == kBf16) return a.topk >= 4 && a.N >= 256;
+  if (a.d != 16 || a.N < 256) return false;
+  if (a.topk >= 3) return true;
+  return a.N >= 512 && static_cast<long>(a.B) * a.N >= 131072;
 }
 
 hipError_t run_topk(const TopkArgs& a) {
@@ -768,8 +778,8 @@ size_t plain_lds_bytes(int dtype, int d, int kc) {
 
 size_t topk_lds_bytes(int dtype, int d, int kc) {
   const size_t plain = plain_lds_bytes(dtype, d, kc);
-  if (dtype != kF32 || d == 8) return plain;
-  const size_t filt = topk_filter_lds_bytes(d, kc);
+  if (!topk_filter_supported(dtype, d, 1)) return plain;
+  const size_t filt = topk_filter_lds_bytes(dtype, d, kc);
   return plain > filt ? plain : filt;
 }
 

@@ -1,16 +1,20 @@
-// Exact fp32 top-k attention by filter-and-verify.
+// Exact top-k attention by filter-and-verify.
 //
-// Same function as topk_small_kernel (scores in the canonical fp32 order,
-// top-k with ties to the lower index, k-softmax, gathered aggregation), but
-// the N-wide scoring pass runs on bf16 MFMA:
+// Same function as topk_small_kernel on fp32 inputs (scores in the canonical
+// fp32 order, top-k with ties to the lower index, k-softmax, gathered
+// aggregation). On bf16 inputs (d = 16) the scores are the canonical fp32
+// scores of the inputs converted to fp32 (the rule the large-k kernels also
+// follow), so the selection is exact there too. The N-wide scoring pass runs
+// on bf16 MFMA:
 //
-//  1. filter: every (query, key) dot is formed from three-way split operands
-//     x = x_hi + x_mid + x_lo (bf16 each) with the six products of size
-//     >= 2^-16, which approximates the fp32 dot to
+//  1. filter: fp32 inputs: every (query, key) dot is formed from three-way
+//     split operands x = x_hi + x_mid + x_lo (bf16 each) with the six
+//     products of size >= 2^-16, which approximates the fp32 dot to
 //     |a - q.k| <= 2^-21 sum_c |q_c k_c| (representation 2^-22, bf16 MFMA
-//     accumulation measured <= 2^-21.9 of the term magnitudes); the canonical
-//     fp32 dot is within d 2^-24 sum_c |q_c k_c| of q.k. Selection runs on
-//     packed values (the
+//     accumulation measured <= 2^-21.9 of the term magnitudes). bf16 inputs:
+//     one bf16 product (exact products, the same accumulation error). The
+//     canonical fp32 dot (d roundings) is within d 2^-24 sum_c |q_c k_c| of
+//     q.k. Selection runs on packed values (the
 //     filter score with the key's position in its low mantissa bits, see
 //     pack8): each lane keeps its k+2 largest with max / med3 only, and the
 //     four lane lists of a query merge into k+1 candidates plus the (k+2)-th
@@ -18,17 +22,16 @@
 //  2. verify: the k+1 candidates are rescored in the canonical fp32 order and
 //     their exact top k taken. Every other key's filter score is at most C,
 //     the largest value that truncates like the (k+2)-th entry. If C plus
-//     eps |q| max_j |k_j| (eps = filter_eps<d>(), at least the filter's error
-//     plus the canonical chain's d roundings, d 2^-24 sum_c |q_c k_c|, with
-//     margin; sum_c |q_c k_c| <= |q| |k_j|), scaled, is strictly below the
-//     k-th exact score, no other key can reach the top
+//     eps |q| max_j |k_j| (eps = filter_eps<d>(), >= the sum of the bounds
+//     above, with margin; sum_c |q_c k_c| <= |q| |k_j|), scaled, is strictly
+//     below the k-th exact score, no other key can reach the top
 //     k, so the result IS the exact top k. Rescoring one spare candidate
 //     settles near-ties between the k-th and (k+1)-th scores (duplicated keys
 //     included) without the fallback.
 //  3. fallback: a 16-query tile with any unproven query recomputes exactly
-//     (fp32 MFMA over all keys, rebuilt from the LDS copy when that holds
-//     them all), so the result never depends on the filter -- only the time
-//     does.
+//     (fp32 MFMA over all keys, read from the LDS copy when that holds them
+//     all exactly), so the result never depends on the filter -- only the
+//     time does.
 //
 // Reference behaviour: src/kernels/fused_topk_attention.py:211-333 and
 // src/kernels/streaming_topk_attention.py:66-258 (including the retained
@@ -243,39 +246,157 @@ __device__ __forceinline__ float stage_split(bf16* lds, const float* src, int ro
 }
 
 // ---------------------------------------------------------------------------
+// bf16 inputs: plain bf16 rows, one product per score
+// ---------------------------------------------------------------------------
+
+// Sum of squares of eight packed bf16 values.
+__device__ __forceinline__ float sumsq_bf16x8(const uint32_t (&w)[4]) {
+  float n2 = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xffff0000u);
+    n2 = fmaf(lo, lo, n2);
+    n2 = fmaf(hi, hi, n2);
+  }
+  return n2;
+}
+
+// The score fragment of topk_small_kernel's bf16 path, with the query left
+// unscaled (filter scores are compared unscaled) and |q|^2 for the bound.
+template <int D>
+struct Bf16FilterFrag : Frag<bf16, D> {
+  using Base = Frag<bf16, D>;
+  // Returns the sum of squares of the elements this lane loaded; the four
+  // lane groups together hold the whole row.
+  __device__ __forceinline__ float load_q(const bf16* qrow, int grp) {
+    Base::load_q(qrow, grp, 1.f);
+    if constexpr (D == 16) {
+      float n2 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = __uint_as_float(static_cast<uint32_t>(static_cast<uint16_t>(this->q[i])) << 16);
+        n2 = fmaf(x, x, n2);
+      }
+      return n2;
+    } else {
+      float n2 = 0.f;
+#pragma unroll
+      for (int h = 0; h < Base::NI; ++h) {
+        const auto w = __builtin_bit_cast(uint4, this->q[h]);
+        const uint32_t a[4] = {w.x, w.y, w.z, w.w};
+        n2 += sumsq_bf16x8(a);
+      }
+      return n2;
+    }
+  }
+  __device__ __forceinline__ static float row_norm2(float part) {
+    part += __shfl_xor(part, 16);
+    return part + __shfl_xor(part, 32);
+  }
+};
+
+// Stage `rows` bf16 key rows (zero rows up to rows_pad, a multiple of 64)
+// with row stride LDK and return this thread's max squared row norm.
+template <int D, int LDK>
+__device__ __forceinline__ float stage_bf16_norm(bf16* lds, const bf16* src, int rows, int rows_pad) {
+  constexpr int VPR = D / 8;  // 16-byte vectors per row; VPR consecutive threads share a row
+  constexpr int U = kStageBatch;
+  const char* base = reinterpret_cast<const char*>(src);
+  const int total = rows_pad * VPR;  // a multiple of 64: whole wavefronts agree on v < total
+  const int avail = rows * VPR;
+  float mx = 0.f;
+  for (int v0 = threadIdx.x; v0 < total; v0 += U * blockDim.x) {
+    uint4 x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int v = v0 + u * blockDim.x;
+      x[u] = make_uint4(0u, 0u, 0u, 0u);
+      if (v < avail) x[u] = *reinterpret_cast<const uint4*>(base + static_cast<uint32_t>(v) * 16u);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int v = v0 + u * blockDim.x, row = v / VPR, cv = v - row * VPR;
+      if (v >= total) break;
+      *reinterpret_cast<uint4*>(lds + row * LDK + cv * 8) = x[u];
+      const uint32_t w[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+      float n2 = sumsq_bf16x8(w);
+#pragma unroll
+      for (int o = 1; o < VPR; o <<= 1) n2 += __shfl_xor(n2, o);
+      mx = fmaxf(mx, n2);
+    }
+  }
+  return mx;
+}
+
+// Per input type: the filter fragment, the LDS key row and its staging.
+template <typename T, int D>
+struct FilterIn;
+
+template <int D>
+struct FilterIn<float, D> {
+  using SF = SplitFrag<D>;
+  static constexpr int LDK = SF::LDK;
+  __device__ __forceinline__ static float stage(bf16* lds, const float* src, int rows, int rows_pad,
+                                                bool& exact) {
+    return stage_split<D>(lds, src, rows, rows_pad, exact);
+  }
+  // E elements of a staged row, from element e0, rebuilt as fp32
+  template <int E>
+  __device__ __forceinline__ static void row_f32(float (&dst)[E], const bf16* r, int e0) {
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      dst[e] = (bf16_to_f32(r[SF::OFF_H + e0 + e]) + bf16_to_f32(r[SF::OFF_M + e0 + e])) +
+               bf16_to_f32(r[SF::OFF_L + e0 + e]);
+  }
+};
+
+template <int D>
+struct FilterIn<bf16, D> {
+  using SF = Bf16FilterFrag<D>;
+  static constexpr int LDK = SF::LDK;
+  __device__ __forceinline__ static float stage(bf16* lds, const bf16* src, int rows, int rows_pad,
+                                                bool&) {
+    return stage_bf16_norm<D, LDK>(lds, src, rows, rows_pad);
+  }
+  template <int E>
+  __device__ __forceinline__ static void row_f32(float (&dst)[E], const bf16* r, int e0) {
+    ld_bf16<E>(dst, r + e0);
+  }
+};
+
+// ---------------------------------------------------------------------------
 // exact fp32 pass for one query tile (fallback)
 // ---------------------------------------------------------------------------
 
 // The tile's exact top-k lists (merged over the four lanes of each query), in
-// the canonical fp32 order. from_lds (wave-uniform): key rows are rebuilt from
-// the split rows resident in LDS (all N keys, each rebuilt exactly);
-// otherwise they come from global memory.
-template <int D, int K>
-__device__ __forceinline__ void exact_tile(const float* __restrict__ Qb,
-                                           const float* __restrict__ Kb, const bf16* Ks,
-                                           bool from_lds, int N, int qbase, float scale, int lane,
-                                           float (&val)[K], int (&ix)[K]) {
+// the canonical fp32 order (fp32 MFMA on the inputs converted to fp32).
+// from_lds (wave-uniform): key rows are rebuilt from the rows resident in LDS
+// (all N keys, each rebuilt exactly); otherwise they come from global memory.
+template <typename T, int D, int K>
+__device__ __forceinline__ void exact_tile(const T* __restrict__ Qb, const T* __restrict__ Kb,
+                                           const bf16* Ks, bool from_lds, int N, int qbase,
+                                           float scale, int lane, float (&val)[K], int (&ix)[K]) {
   using F = Frag<float, D>;
   constexpr bool POW2 = pow2_scale<D>();
   constexpr int E = F::E;
-  constexpr int LDK = SplitFrag<D>::LDK;
+  constexpr int LDK = FilterIn<T, D>::LDK;
   const int col = lane & 15, grp = lane >> 4;
   const int self = qbase + col;
   F frag;
-  frag.load_q(Qb + static_cast<size_t>(min(self, N - 1)) * D, grp, POW2 ? scale : 1.f);
+  ld_row<T, E>(frag.q, Qb + static_cast<size_t>(min(self, N - 1)) * D + grp * E);
+  if constexpr (POW2) {
+#pragma unroll
+    for (int t = 0; t < E; ++t) frag.q[t] *= scale;
+  }
 #pragma unroll
   for (int m = 0; m < K; ++m) { val[m] = -INFINITY; ix[m] = kIdxSentinel; }
   for (int kb = 0; kb < N; kb += 16) {
     typename F::KF kf;
     if (from_lds) {
       // rows [N, 16 * ceil(N / 16)) are staged zero rows
-      const bf16* r = Ks + (kb + col) * LDK + grp * E;
-#pragma unroll
-      for (int e = 0; e < E; ++e)
-        kf.v[e] = (bf16_to_f32(r[SplitFrag<D>::OFF_H + e]) + bf16_to_f32(r[SplitFrag<D>::OFF_M + e])) +
-                  bf16_to_f32(r[SplitFrag<D>::OFF_L + e]);
+      FilterIn<T, D>::template row_f32<E>(kf.v, Ks + (kb + col) * LDK, grp * E);
     } else {
-      ld_f32<E>(kf.v, Kb + static_cast<size_t>(min(kb + col, N - 1)) * D + grp * E);
+      ld_row<T, E>(kf.v, Kb + static_cast<size_t>(min(kb + col, N - 1)) * D + grp * E);
     }
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -304,10 +425,10 @@ __device__ __forceinline__ void exact_tile(const float* __restrict__ Qb,
 
 // Canonical fp32 score of one (query row, key row) pair: fmaf chain with
 // element kk*(D/4)+t at step t, slot kk (the MFMA chain's order), then scaled.
+template <typename T, int D, bool POW2>
 // Four steps at a time (4-element runs of each quarter row), so at most 32
 // elements are live instead of both whole rows.
-template <int D, bool POW2>
-__device__ __forceinline__ float canon_pair(const float* qrow, const float* krow, float scale) {
+__device__ __forceinline__ float canon_pair(const T* qrow, const T* krow, float scale) {
   constexpr int QD = D / 4;
   float acc = 0.f;
 #pragma unroll
@@ -315,8 +436,8 @@ __device__ __forceinline__ float canon_pair(const float* qrow, const float* krow
     float q[4][4], k[4][4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      ld_f32<4>(q[kk], qrow + kk * QD + t0);
-      ld_f32<4>(k[kk], krow + kk * QD + t0);
+      ld_row<T, 4>(q[kk], qrow + kk * QD + t0);
+      ld_row<T, 4>(k[kk], krow + kk * QD + t0);
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -381,19 +502,20 @@ __device__ __forceinline__ void flush_segment(float (&pv)[QT][L], float (&rv)[QT
 // ONESEG: one chunk of at most one segment holds every key (kc >= N, N <= 1024),
 // so the lists stay packed until the merge.
 // Waves per SIMD the register budget is sized for: 5 (96 VGPRs); at d = 64
-// the split query and key fragments alone take 72 VGPRs, so 4 (128) there.
+// the key and query fragments alone need more, so 4 (128 VGPRs) there.
 template <int D>
 constexpr int filter_min_waves() {
   return D == 64 ? 4 : 5;
 }
 
-template <int D, int K, int QT, bool ONESEG>
+template <typename T, int D, int K, int QT, bool ONESEG>
 __global__ void __launch_bounds__(kFilterMaxWaves * 64, filter_min_waves<D>())
-topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
-                   const float* __restrict__ V, float* __restrict__ O, int32_t* __restrict__ Idx,
-                   int N, int n_qblk, int kc, float scale, int nblocks) {
-  using SF = SplitFrag<D>;
-  constexpr int LDK = SF::LDK;
+topk_filter_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
+                   T* __restrict__ O, int32_t* __restrict__ Idx, int N, int n_qblk, int kc,
+                   float scale, int nblocks) {
+  using FI = FilterIn<T, D>;
+  using SF = typename FI::SF;
+  constexpr int LDK = FI::LDK;
   constexpr int EO = D / 4;
   constexpr int BT = kFilterBlockTiles;
   constexpr int C = K + 1;  // candidates rescored exactly
@@ -411,8 +533,8 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   const int q0 = (qblk * nw + wave) * 16 * QT;  // wave-uniform
   const int col = lane & 15, grp = lane >> 4;
   const size_t boff = static_cast<size_t>(b) * N * D;
-  const float* Qb = Q + boff;
-  const float* Kb = Kx + boff;
+  const T* Qb = Q + boff;
+  const T* Kb = Kx + boff;
 
   SF frag[QT];
   int self[QT];
@@ -448,7 +570,7 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
       *inexact_slot = 0u;
     }
     bool exact = true;
-    const float mine = stage_split<D>(Ks, Kb + static_cast<size_t>(c0) * D, cn, cnb, exact);
+    const float mine = FI::stage(Ks, Kb + static_cast<size_t>(c0) * D, cn, cnb, exact);
     if (!exact) atomicOr(inexact_slot, 1u);
     __syncthreads();
     atomicMax(kmax_slot, __float_as_uint(mine));  // non-negative: bit order is value order
@@ -558,7 +680,7 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int qi = min(self[qt], N - 1);
-    const float* qrow = Qb + static_cast<size_t>(qi) * D;
+    const T* qrow = Qb + static_cast<size_t>(qi) * D;
     // lane group g rescores candidates g, g+4, ...
     float mine[(C + 3) / 4];
 #pragma unroll
@@ -569,7 +691,7 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
       for (int mm = 0; mm < C; ++mm)
         if (mm == m) c = cand[qt][mm];
       const int row = min(max(c, 0), N - 1);
-      const float e = canon_pair<D, POW2>(qrow, Kb + static_cast<size_t>(row) * D, scale);
+      const float e = canon_pair<T, D, POW2>(qrow, Kb + static_cast<size_t>(row) * D, scale);
       mine[u] = c < 0 ? -INFINITY : e;
     }
     // the exact top k of the candidates, in (score desc, index asc) order
@@ -587,7 +709,7 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     if (!__all(ok[qt]))
-      exact_tile<D, K>(Qb, Kb, Ks, lds_exact, N, q0 + 16 * qt, scale, lane, val[qt], ix[qt]);
+      exact_tile<T, D, K>(Qb, Kb, Ks, lds_exact, N, q0 + 16 * qt, scale, lane, val[qt], ix[qt]);
   }
 
   // ---- k-softmax and gathered aggregation --------------------------------
@@ -606,14 +728,14 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
       den += w;
       const int row = min(max(ix[qt][m], 0), N - 1);
       float vr[EO];
-      ld_f32<EO>(vr, V + boff + static_cast<size_t>(row) * D + grp * EO);
+      ld_row<T, EO>(vr, V + boff + static_cast<size_t>(row) * D + grp * EO);
 #pragma unroll
       for (int c = 0; c < EO; ++c) acc[c] = fmaf(w, vr[c], acc[c]);
     }
     const float inv = 1.f / den;
 #pragma unroll
     for (int c = 0; c < EO; ++c) acc[c] *= inv;
-    st_f32<EO>(O + boff + static_cast<size_t>(qi) * D + grp * EO, acc);
+    st_row<T, EO>(O + boff + static_cast<size_t>(qi) * D + grp * EO, acc);
     if (Idx != nullptr && grp == 0) {
       int32_t* dst = Idx + (static_cast<size_t>(b) * N + qi) * K;
 #pragma unroll
@@ -622,38 +744,43 @@ topk_filter_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   }
 }
 
-size_t topk_filter_lds_bytes(int d, int kc) {
+size_t topk_filter_lds_bytes(int dtype, int d, int kc) {
   const int kcb = (kc + kBlockKeys - 1) / kBlockKeys * kBlockKeys;
-  return 16 + static_cast<size_t>(kcb) * (3 * d + 8) * sizeof(bf16);
+  const int row = dtype == kF32 ? 3 * d + 8 : d + 8;  // bf16 elements per staged key row
+  return 16 + static_cast<size_t>(kcb) * row * sizeof(bf16);
 }
 
-template <int D>
+template <typename T, int D>
 static hipError_t launch_filter(const TopkArgs& a, int kc) {
   constexpr int QT = kTopkQueryTiles;
   const int per_wave = 16 * QT;
   const int waves = (a.N + per_wave - 1) / per_wave;
   // up to N = 256 the 28 KiB key copy is small: four-wave groups keep five
   // groups (20 waves) resident per CU; larger rows share one copy among eight
-  const int maxw = a.N <= 256 ? 4 : kFilterMaxWaves;
+  // waves, unless that leaves fewer than two workgroups per CU (small batches:
+  // B = 32, N = 512 runs 1.4x slower with eight-wave groups)
+  const long wide_groups = static_cast<long>(a.B) * ((a.N + 16 * QT * kFilterMaxWaves - 1) /
+                                                     (16 * QT * kFilterMaxWaves));
+  const int maxw = (a.N <= 256 || wide_groups < 2L * kCUs) ? 4 : kFilterMaxWaves;
   const int nw = waves >= maxw ? maxw : waves;
   const int qb = per_wave * nw;
   const int n_qblk = (a.N + qb - 1) / qb;
   const int nblocks = a.B * n_qblk;
-  const size_t lds = topk_filter_lds_bytes(D, kc);
-  const float* q = static_cast<const float*>(a.q);
-  const float* k = static_cast<const float*>(a.k);
-  const float* v = static_cast<const float*>(a.v);
-  float* o = static_cast<float*>(a.out);
+  const size_t lds = topk_filter_lds_bytes(a.dtype, D, kc);
+  const T* q = static_cast<const T*>(a.q);
+  const T* k = static_cast<const T*>(a.k);
+  const T* v = static_cast<const T*>(a.v);
+  T* o = static_cast<T*>(a.out);
   hipStream_t st = static_cast<hipStream_t>(a.stream);
   const bool oneseg = kc >= a.N && a.N <= kSegKeys;
-#define TARMAC_FILTER_CASE(KK)                                                                 \
-  case KK:                                                                                     \
-    if (oneseg)                                                                                \
-      hipLaunchKernelGGL((topk_filter_kernel<D, KK, QT, true>), dim3(nblocks), dim3(64 * nw), \
-                         lds, st, q, k, v, o, a.idx, a.N, n_qblk, kc, a.scale, nblocks);      \
-    else                                                                                       \
-      hipLaunchKernelGGL((topk_filter_kernel<D, KK, QT, false>), dim3(nblocks), dim3(64 * nw), \
-                         lds, st, q, k, v, o, a.idx, a.N, n_qblk, kc, a.scale, nblocks);      \
+#define TARMAC_FILTER_CASE(KK)                                                                    \
+  case KK:                                                                                        \
+    if (oneseg)                                                                                   \
+      hipLaunchKernelGGL((topk_filter_kernel<T, D, KK, QT, true>), dim3(nblocks), dim3(64 * nw),  \
+                         lds, st, q, k, v, o, a.idx, a.N, n_qblk, kc, a.scale, nblocks);         \
+    else                                                                                          \
+      hipLaunchKernelGGL((topk_filter_kernel<T, D, KK, QT, false>), dim3(nblocks), dim3(64 * nw), \
+                         lds, st, q, k, v, o, a.idx, a.N, n_qblk, kc, a.scale, nblocks);         \
     break;
   switch (a.topk) {
     TARMAC_FILTER_CASE(1)
@@ -671,15 +798,19 @@ static hipError_t launch_filter(const TopkArgs& a, int kc) {
   return hipGetLastError();
 }
 
+// fp32: d = 16, 32, 64. bf16: d = 16 only, where one bf16 product per score
+// makes the scan cheap (at d = 32 and 64 the plain bf16 pass is faster).
 bool topk_filter_supported(int dtype, int d, int topk) {
-  return dtype == kF32 && (d == 16 || d == 32 || d == 64) && topk >= 1 && topk <= kTopkSmallMax;
+  const bool shape = dtype == kF32 ? (d == 16 || d == 32 || d == 64) : (dtype == kBf16 && d == 16);
+  return shape && topk >= 1 && topk <= kTopkSmallMax;
 }
 
 hipError_t run_topk_filter(const TopkArgs& a) {
+  if (a.dtype == kBf16) return a.d == 16 ? launch_filter<bf16, 16>(a, a.key_chunk) : hipErrorInvalidValue;
   switch (a.d) {
-    case 16: return launch_filter<16>(a, a.key_chunk);
-    case 32: return launch_filter<32>(a, a.key_chunk);
-    case 64: return launch_filter<64>(a, a.key_chunk);
+    case 16: return launch_filter<float, 16>(a, a.key_chunk);
+    case 32: return launch_filter<float, 32>(a, a.key_chunk);
+    case 64: return launch_filter<float, 64>(a, a.key_chunk);
   }
   return hipErrorInvalidValue;
 }
