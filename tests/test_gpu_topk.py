@@ -205,6 +205,19 @@ def check_bf16_exact(q, k, v, kk, out, idx):
     assert np.abs(out - out_c).max() <= BF16_TOL * max(np.abs(out_c).max(), 1e-30)
 
 
+@pytest.mark.parametrize("N,d,kk,chunk", [(256, 16, 1, 64), (256, 16, 2, 16), (512, 32, 2, 128),
+                                          (1024, 64, 2, 256), (700, 16, 3, 128), (1500, 16, 4, 256)])
+def test_streaming_topk_bf16_matches_fused_bitwise(N, d, kk, chunk):
+    """bf16: the streamed kernel (key chunks) returns exactly the resident
+    kernel's indices and outputs, on every bf16 selection path."""
+    B = 3
+    q, k, v = qkv(5 * N + d + kk, B, N, d)
+    out_s, idx_s = run_topk_bf16(q, k, v, kk, chunk)
+    out_f, idx_f = run_topk_bf16(q, k, v, kk)
+    assert np.array_equal(idx_s, idx_f)
+    assert np.array_equal(out_s, out_f)
+
+
 @pytest.mark.parametrize("N,kk,chunk", [(256, 4, None), (256, 8, None), (512, 5, None),
                                         (1024, 4, None), (700, 6, 128), (1500, 4, 256)])
 def test_topk_bf16_filter_exact(N, kk, chunk):
