@@ -176,7 +176,7 @@ int tarmac_topk_variant_fwd(const void* q, const void* k, const void* v, void* o
   tarmac::TopkArgs a{q, k, v, out, idx_out, B, N, d, topk, dtype, 0, inv_sqrt(d), stream};
   a.select = variant == TARMAC_VARIANT_MASKED ? tarmac::kSelMasked : tarmac::kSelSort;
   a.bisect = bisect;
-  if (static_cast<long>(N + tarmac::wide_cap(a)) * 4 > kLdsBudget)
+  if (static_cast<size_t>(N + tarmac::wide_cap(a)) * 4 > kLdsBudget)
     return fail(TARMAC_ERR_UNSUPPORTED, "%s: N=%d too large for one score row in LDS", fn, N);
   return hip_status(tarmac::run_topk(a), fn);
 }

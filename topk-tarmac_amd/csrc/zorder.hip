@@ -38,6 +38,8 @@ constexpr int kZorderThreads = 256;
 // Longest padded row (next_pow2(N)) the selector sorts: four wavefronts with
 // runs of up to 1024 keys (16 per lane).
 constexpr int kZorderMaxP = 4096;
+static_assert(kZorderMaxP == (kZorderThreads / 64) * 64 * 16,
+              "the selector's longest row: every wavefront sorts 16 keys per lane");
 // Queries per quad per pass of the fused Z-order attention (peers from
 // global memory / from LDS).
 template <int D>
