@@ -104,8 +104,10 @@ def profile_one(args, q, k, v, dev) -> int:
     cover a single shape."""
     import numpy as np
     import torch
-    from tarmac import bound
+    from tarmac import _lib, bound
     name = args.profile_kernel
+    if args.topk_filter is not None:
+        _lib.LIB.tarmac_set_topk_filter(args.topk_filter)
     if name == "dense":
         fn = bound.dense(q, k, v)
     elif name.startswith("topk"):
@@ -159,6 +161,9 @@ def main() -> int:
                              "stream2"],
                     help="run only this kernel (headline shape; zorder/stream at their configs) "
                          "--warmup + --steps times, for profiler counter passes")
+    ap.add_argument("--topk-filter", type=int, default=None, choices=[0, 1, 2],
+                    help="top-k implementation for --profile-kernel runs (tarmac_set_topk_filter: "
+                         "0 plain, 1 automatic, 2 filter-and-verify)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 64 MiB device copy (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
