@@ -205,6 +205,36 @@ def check_bf16_exact(q, k, v, kk, out, idx):
     assert np.abs(out - out_c).max() <= BF16_TOL * max(np.abs(out_c).max(), 1e-30)
 
 
+@pytest.mark.parametrize("N,d", [(64, 16), (256, 32), (300, 64)])
+def test_topk_bf16_group_selection_with_ties(N, d):
+    """bf16 k <= 3 on the plain pass (group selection for k <= 2): duplicated
+    keys, zero and repeated queries give exact ties; every retained set stays
+    admissible, distinct and self-free, and outputs match float64 over it."""
+    from tarmac.kernels import topk_attention
+    B = 4
+    q, k, v = (O.bf16_round(x) for x in qkv(500 + N + d, B, N, d))
+    k[:, 1::2] = k[:, 0::2]
+    q[:, :5] = 0.0
+    q[:, 5:10] = q[:, 5:6]
+    qd, kd, vd = dev(q, k, v, dtype=torch.bfloat16)
+    for kk in (1, 2, 3):
+        out, idx = topk_attention(qd, kd, vd, kk, return_indices=True)
+        torch.cuda.synchronize()
+        out, idx = out.float().cpu().numpy(), idx.cpu().numpy()
+        assert not np.any(idx == np.arange(N)[None, :, None])
+        assert all(len(set(r)) == kk for r in idx.reshape(-1, kk).tolist())
+        s = O.scores(q.astype(np.float64), k.astype(np.float64))
+        eps = 2.0 * O.score_error_bound(q, k) + 1e-30
+        sel = np.zeros_like(s, dtype=bool)
+        np.put_along_axis(sel, idx.astype(np.int64), True, -1)
+        worst_sel = np.where(sel, s + eps, np.inf).min(-1)
+        best_out = np.where(sel | np.isneginf(s), -np.inf, s).max(-1)
+        assert np.all(best_out <= worst_sel)
+        ref = O.prescore_attention(q.astype(np.float64), k.astype(np.float64),
+                                   v.astype(np.float64), idx.astype(np.int64))
+        assert np.abs(out - ref).max() <= BF16_TOL * np.abs(ref).max()
+
+
 @pytest.mark.parametrize("N,d,kk,chunk", [(256, 16, 1, 64), (256, 16, 2, 16), (512, 32, 2, 128),
                                           (1024, 64, 2, 256), (700, 16, 3, 128), (1500, 16, 4, 256)])
 def test_streaming_topk_bf16_matches_fused_bitwise(N, d, kk, chunk):

@@ -91,6 +91,16 @@ __device__ __forceinline__ void group_to_list(const GroupTop2& g, float (&val)[K
     const bool b_first = ranks_before(vb, ib, va, ia);
     val[1] = b_first ? vb : va;
     ix[1] = b_first ? ib : ia;
+    // Cleared, equal values can arrive in descending index order (the row
+    // bits order ties by r); the lane merge needs (score desc, index asc)
+    // lists, or the four lanes of a query end with different lists.
+    const bool swap = ranks_before(val[1], ix[1], val[0], ix[0]);
+    const float v0 = val[0];
+    const int i0 = ix[0];
+    val[0] = swap ? val[1] : v0;
+    ix[0] = swap ? ix[1] : i0;
+    val[1] = swap ? v0 : val[1];
+    ix[1] = swap ? i0 : ix[1];
   }
 }
 
