@@ -12,7 +12,8 @@
  * path of the reference. Retained sets are the topk largest scores, ties to
  * the lower agent index. fp32 scores are formed in a fixed fmaf order
  * (element c = kk*(d/4) + t at step t, slot kk), so results are reproducible
- * bit for bit.
+ * bit for bit; bf16 inputs are ranked by that same fp32 score of the inputs
+ * converted to fp32 (the retained set is exact, not an approximation).
  *
  * Reference paths below are relative to the MHHamdan/TopK-TarMAC checkout.
  */
@@ -191,22 +192,30 @@ int tarmac_dense_bwd(const float* q, const float* k, const float* v, const float
                      int stats_ready, int B, int N, int d, void* stream);
 
 /*
- * fp32 top-k (d = 16, 32, 64; topk <= 8) can score all pairs on split-bf16
- * MFMA, rescore k+1 candidates in the canonical fp32 order and prove the
- * result is the exact top k (16-query tiles where the proof fails recompute
- * in fp32). The result is identical either way; only the time differs.
- * mode: 0 = never, 1 = where it is faster (default: d = 16 with N >= 256
- * and topk >= 3, or N >= 512 and B * N >= 131072), 2 = always. bf16 inputs at d = 16 have the
- * same kernel with one bf16 product per score (used from topk = 4 and
- * N = 256 in mode 1); it selects the exact top k of the canonical fp32 scores of the inputs
- * converted to fp32.
- * Process-wide. Returns the previous mode, or -1 (and sets the last error)
- * for an invalid mode. No counterpart in the reference (its kernels have one
- * path).
+ * Which of three equally exact implementations serves topk <= 8 (the result
+ * is identical whichever runs; only the time differs):
+ *   packed   -- scores with the key's position in their low mantissa bits,
+ *               lists of k+2 values kept with max / med3, a proof that the
+ *               truncation (fp32) or the bf16 score error bound (bf16) cannot
+ *               change the top k, exact canonical rescoring where it is needed,
+ *               and an exact recomputation of any 16-query tile left unproven;
+ *   filter   -- all pairs scored on split-bf16 MFMA (fp32 inputs) or bf16
+ *               MFMA (bf16, d = 16), k+1 candidates rescored in the canonical
+ *               fp32 order and proven against the bf16 error bound;
+ *   lists    -- fp32 MFMA scores and per-score (score, index) register lists.
+ * mode: 0 = packed always, 1 = automatic (default; the fastest measured on
+ * MI355X for the shape), 2 = filter where supported (fp32 d = 16, 32, 64;
+ * bf16 d = 16), 3 = lists for fp32 (bf16 runs packed). bf16 retained sets are
+ * always the exact top k of the canonical fp32 scores of the inputs converted
+ * to fp32. Process-wide (an atomic setting: concurrent calls stay safe and
+ * get identical results). Returns the previous mode, or -1 (and sets the last
+ * error) for an invalid mode. No counterpart in the reference (its kernels
+ * have one path).
  */
 #define TARMAC_FILTER_OFF 0
 #define TARMAC_FILTER_AUTO 1
 #define TARMAC_FILTER_ALWAYS 2
+#define TARMAC_FILTER_LISTS 3
 int tarmac_set_topk_filter(int mode);
 
 /* Writes 1.0f to *out: the launch-floor probe of scripts/launch_overhead.py:28-30. */

@@ -121,16 +121,17 @@ def test_python_wrappers_mirror_reference_asserts():
 
 
 def test_filter_mode_switch():
-    """tarmac_set_topk_filter: modes 0/1/2 return the previous mode; anything
+    """tarmac_set_topk_filter: modes 0/1/2/3 return the previous mode; anything
     else is refused with -1 and a message, leaving the mode unchanged."""
     from tarmac import _lib
     lib = _lib.LIB
     prev = lib.tarmac_set_topk_filter(1)
     try:
         assert lib.tarmac_set_topk_filter(2) == 1
-        assert lib.tarmac_set_topk_filter(0) == 2
+        assert lib.tarmac_set_topk_filter(3) == 2
+        assert lib.tarmac_set_topk_filter(0) == 3
         assert lib.tarmac_set_topk_filter(7) == -1
-        assert "mode must be 0, 1 or 2" in _lib.last_error()
+        assert "mode must be 0, 1, 2 or 3" in _lib.last_error()
         assert lib.tarmac_set_topk_filter(-1) == -1
         assert lib.tarmac_set_topk_filter(1) == 0
     finally:

@@ -58,7 +58,8 @@ def check_f32(q, k, v, kk, out, idx, exact_order=True):
 
 
 def _set_filter(mode: int) -> int:
-    """0 = plain fp32 pass, 1 = automatic, 2 = filter-and-verify wherever supported."""
+    """0 = packed exact pass, 1 = automatic, 2 = split-bf16 filter-and-verify
+    wherever supported, 3 = register-list pass (k <= 8)."""
     from tarmac import _lib
     return _lib.LIB.tarmac_set_topk_filter(mode)
 
@@ -79,7 +80,7 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("mode", [0, 2], ids=["plain", "filter"])
+@pytest.mark.parametrize("mode", [0, 2, 3], ids=["packed", "filter", "lists"])
 @pytest.mark.parametrize("N,d,kk", CASES)
 def test_fused_topk_f32_parity(N, d, kk, mode):
     B = max(2, min(16, 4096 // N))
@@ -174,14 +175,7 @@ def test_topk_bf16(N, d, kk):
     torch.cuda.synchronize()
     out = out.float().cpu().numpy()
     idx = idx.cpu().numpy()
-    s = O.scores(qb.astype(np.float64), kb.astype(np.float64))
-    # admissible: no unselected score beats a selected one by more than the bound
-    eps = 2.0 * O.score_error_bound(qb, kb) + 1e-30
-    sel = np.zeros_like(s, dtype=bool)
-    np.put_along_axis(sel, idx.astype(np.int64), True, -1)
-    worst_sel = np.where(sel, s + eps, np.inf).min(-1)
-    best_out = np.where(sel | np.isneginf(s), -np.inf, s).max(-1)
-    assert np.all(best_out <= worst_sel)
+    check_bf16_exact(q, k, v, kk, out, idx)
     ref = O.prescore_attention(qb.astype(np.float64), kb.astype(np.float64),
                                vb.astype(np.float64), idx.astype(np.int64))
     assert np.abs(out - ref).max() <= BF16_TOL * np.abs(ref).max()
@@ -196,43 +190,46 @@ def run_topk_bf16(q, k, v, kk, chunk=None):
 
 
 def check_bf16_exact(q, k, v, kk, out, idx):
-    """The bf16 filter-and-verify path (d = 16) selects the exact top k of the
-    canonical fp32 scores of the inputs converted to fp32: indices bit-exact
-    against the C oracle on the bf16-rounded inputs, outputs within 1e-2."""
+    """bf16 top-k selects the exact top k of the canonical fp32 scores of the
+    inputs converted to fp32: indices bit-exact against the C oracle on the
+    bf16-rounded inputs, outputs within 1e-2."""
     qb, kb, vb = (O.bf16_round(x) for x in (q, k, v))
     out_c, idx_c = O.canon_topk(qb, kb, vb, kk)
+    if kk > 8:  # the large-k kernels emit ascending index order
+        idx_c = np.sort(idx_c, -1)
     assert np.array_equal(idx, idx_c), "bf16 retained indices differ from the canonical oracle"
     assert np.abs(out - out_c).max() <= BF16_TOL * max(np.abs(out_c).max(), 1e-30)
 
 
 @pytest.mark.parametrize("N,d", [(64, 16), (256, 32), (300, 64)])
-def test_topk_bf16_group_selection_with_ties(N, d):
-    """bf16 k <= 3 on the plain pass (group selection for k <= 2): duplicated
-    keys, zero and repeated queries give exact ties; every retained set stays
-    admissible, distinct and self-free, and outputs match float64 over it."""
-    from tarmac.kernels import topk_attention
+def test_topk_bf16_exact_with_ties(N, d):
+    """bf16 with exact ties (duplicated keys, zero and repeated queries): the
+    retained set and its order are the canonical oracle's, ties to the lower
+    index, on every k <= 8."""
     B = 4
     q, k, v = (O.bf16_round(x) for x in qkv(500 + N + d, B, N, d))
     k[:, 1::2] = k[:, 0::2]
     q[:, :5] = 0.0
     q[:, 5:10] = q[:, 5:6]
-    qd, kd, vd = dev(q, k, v, dtype=torch.bfloat16)
-    for kk in (1, 2, 3):
-        out, idx = topk_attention(qd, kd, vd, kk, return_indices=True)
-        torch.cuda.synchronize()
-        out, idx = out.float().cpu().numpy(), idx.cpu().numpy()
-        assert not np.any(idx == np.arange(N)[None, :, None])
-        assert all(len(set(r)) == kk for r in idx.reshape(-1, kk).tolist())
-        s = O.scores(q.astype(np.float64), k.astype(np.float64))
-        eps = 2.0 * O.score_error_bound(q, k) + 1e-30
-        sel = np.zeros_like(s, dtype=bool)
-        np.put_along_axis(sel, idx.astype(np.int64), True, -1)
-        worst_sel = np.where(sel, s + eps, np.inf).min(-1)
-        best_out = np.where(sel | np.isneginf(s), -np.inf, s).max(-1)
-        assert np.all(best_out <= worst_sel)
-        ref = O.prescore_attention(q.astype(np.float64), k.astype(np.float64),
-                                   v.astype(np.float64), idx.astype(np.int64))
-        assert np.abs(out - ref).max() <= BF16_TOL * np.abs(ref).max()
+    for kk in (1, 2, 3, 4, 8):
+        out, idx = run_topk_bf16(q, k, v, kk)
+        check_bf16_exact(q, k, v, kk, out, idx)
+        # zero queries tie every peer at +0: the lowest indices win
+        assert idx[:, 0].tolist() == [list(range(1, kk + 1))] * B
+
+
+CONFIGS2 = [(N, d, kk) for N in (64, 256, 512) for d in (16, 32, 64) for kk in (1, 2, 4)]
+
+
+@pytest.mark.parametrize("N,d,kk", CONFIGS2)
+def test_topk_bf16_configs2_exact(N, d, kk):
+    """Every (N, d, k) cell of the bf16 grid: the retained set is the exact top
+    k of the canonical fp32 scores of the bf16 inputs (bit-exact indices and
+    order), outputs within 1e-2."""
+    B = 8
+    q, k, v = qkv(77 + N + d, B, N, d)
+    out, idx = run_topk_bf16(q, k, v, kk)
+    check_bf16_exact(q, k, v, kk, out, idx)
 
 
 @pytest.mark.parametrize("N,d,kk,chunk", [(256, 16, 1, 64), (256, 16, 2, 16), (512, 32, 2, 128),
@@ -296,8 +293,9 @@ def test_filter_path_matches_plain_fp32_path_bitwise(N, d, kk, chunk, filter_alw
     check_f32(q, k, v, kk, out_f, idx_f)
 
 
+@pytest.mark.parametrize("mode", [0, 2], ids=["packed", "filter"])
 @pytest.mark.parametrize("N,chunk", [(256, None), (700, 128), (2048, None)])
-def test_filter_fallback_on_ties(N, chunk, filter_always):
+def test_filter_fallback_on_ties(N, chunk, mode):
     """Duplicated keys and constant queries defeat the filter's proof; the
     fallback must still return the canonical answer (single-segment lists,
     chunked lists and lists spanning several 1024-key segments)."""
@@ -306,13 +304,18 @@ def test_filter_fallback_on_ties(N, chunk, filter_always):
     k[:, 1::2] = k[:, 0::2]
     q[:, :40] = 0.0
     q[:, 40:80] = q[:, 40:41]
-    for kk in (1, 2, 4, 8):
-        out, idx = run_topk(q, k, v, kk, chunk=chunk)
-        check_f32(q, k, v, kk, out, idx)
+    prev = _set_filter(mode)
+    try:
+        for kk in (1, 2, 4, 8):
+            out, idx = run_topk(q, k, v, kk, chunk=chunk)
+            check_f32(q, k, v, kk, out, idx)
+    finally:
+        _set_filter(prev)
 
 
+@pytest.mark.parametrize("mode", [0, 2], ids=["packed", "filter"])
 @pytest.mark.parametrize("N,kk,chunk", [(256, 2, None), (512, 8, None), (1500, 3, 256)])
-def test_filter_near_ties(N, kk, chunk, filter_always):
+def test_filter_near_ties(N, kk, chunk, mode):
     """Clusters of keys whose scores agree to ~1e-6 relative: candidates that
     share their truncated filter score, lists that must be re-sorted after
     repacking, and proofs that fail on purpose."""
@@ -321,7 +324,11 @@ def test_filter_near_ties(N, kk, chunk, filter_always):
     rng = np.random.default_rng(N)
     for c0 in range(0, N - 40, 97):
         k[:, c0 + 1:c0 + 40] = k[:, c0:c0 + 1] * 3.0 + 1e-6 * rng.standard_normal((B, 39, d))
-    out, idx = run_topk(q, k, v, kk, chunk=chunk)
+    prev = _set_filter(mode)
+    try:
+        out, idx = run_topk(q, k, v, kk, chunk=chunk)
+    finally:
+        _set_filter(prev)
     check_f32(q, k, v, kk, out, idx)
 
 

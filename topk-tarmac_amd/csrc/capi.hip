@@ -326,13 +326,11 @@ int tarmac_dense_bwd(const float* q, const float* k, const float* v, const float
 }
 
 int tarmac_set_topk_filter(int mode) {
-  if (mode < tarmac::kFilterOff || mode > tarmac::kFilterAlways) {
-    fail(TARMAC_ERR_INVALID, "tarmac_set_topk_filter: mode must be 0, 1 or 2 (got %d)", mode);
+  if (mode < tarmac::kFilterOff || mode > tarmac::kFilterLegacy) {
+    fail(TARMAC_ERR_INVALID, "tarmac_set_topk_filter: mode must be 0, 1, 2 or 3 (got %d)", mode);
     return -1;
   }
-  const int prev = tarmac::g_topk_filter_mode;
-  tarmac::g_topk_filter_mode = mode;
-  return prev;
+  return tarmac::set_topk_filter_mode(mode);
 }
 
 int tarmac_noop(float* out, void* stream) {

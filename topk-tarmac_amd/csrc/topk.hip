@@ -6,8 +6,8 @@
 // (fused_topk_attention_tiled) and src/kernels/streaming_topk_attention.py:
 // 66-258 (streaming_topk_attention, incl. the optional retained-index output).
 //
-// Small k (1..8), one launch shape for both the resident and the streamed
-// variants:
+// Small k (1..8), fp32 register-list pass (topk_small_kernel), one launch
+// shape for both the resident and the streamed variants:
 //   * workgroup = (batch row b, block of 16*nw queries), nw waves;
 //   * keys are staged through LDS in chunks of `kc` rows (kc >= N: the whole
 //     K[b] is resident; otherwise the chunks stream);
@@ -16,8 +16,7 @@
 //     see disjoint interleaved key subsets of one query, each in ascending key
 //     order;
 //   * every lane keeps a sorted (score desc, index asc) list of its best k in
-//     registers; strict '>' insertion keeps the lower index on ties (bf16
-//     inputs with k <= 2 select by lane group instead: group_insert);
+//     registers; strict '>' insertion keeps the lower index on ties;
 //   * two xor-shuffle merge steps (16, 32) combine the four lists, after which
 //     the 4 lanes of a query each compute d/4 output channels from the k
 //     gathered V rows.
@@ -25,84 +24,13 @@
 // Large k (> 8): one wave per query, the score row in LDS, an exact threshold
 // found by bisection on the order-preserving integer key, ties at the
 // threshold resolved to the lowest indices.
+#include <atomic>
+
 #include "frag.hpp"
 #include "select.hpp"
 #include "tarmac_internal.hpp"
 
 namespace tarmac {
-
-// bf16 inputs, k <= 2: selection by lane group. A lane's four scores of one
-// 16-key tile (rows r = 0..3) carry r in their low 2 mantissa bits (a
-// truncation of at most 2^-21 of the score, below the bf16 MFMA's own
-// accumulation error), so a tile's best (and second best) come from
-// max3 / min without index bookkeeping, and only whole groups enter the
-// running state: the best group's max and second, the second group's max,
-// and their tiles. The two best scores of everything seen are among those
-// three values. 2.25 (k = 1) and 4.75 (k = 2) VALU operations per score
-// instead of 3 and 7 for per-score insertion.
-struct GroupTop2 {
-  float v1, s1, v2;  // packed values
-  int i1, i2;        // tile offsets (16 t) of the best and second groups
-};
-
-__device__ __forceinline__ float pack_row(float s, uint32_t r) {
-  return __uint_as_float((__float_as_uint(s) & ~3u) | r);
-}
-
-template <int K>
-__device__ __forceinline__ void group_insert(GroupTop2& g, const f32x4& s, int tile_off) {
-  const float p0 = pack_row(s[0], 0u), p1 = pack_row(s[1], 1u);
-  const float p2 = pack_row(s[2], 2u), p3 = pack_row(s[3], 3u);
-  if constexpr (K == 1) {
-    const float m = vmax(vmax(p0, p1), vmax(p2, p3));
-    const bool c = m > g.v1;
-    g.v1 = vmax(g.v1, m);
-    g.i1 = c ? tile_off : g.i1;
-  } else {
-    const float hi_a = vmax(p0, p1), lo_a = vmin(p0, p1);
-    const float hi_b = vmax(p2, p3), lo_b = vmin(p2, p3);
-    const float m = vmax(hi_a, hi_b);
-    // second of the four: the middle of (hi_a, hi_b, max(lo_a, lo_b)), as
-    // that max never exceeds max(hi_a, hi_b)
-    const float sec = __builtin_amdgcn_fmed3f(vmax(lo_a, lo_b), hi_a, hi_b);
-    const bool c1 = m > g.v1, c2 = m > g.v2;
-    g.v2 = __builtin_amdgcn_fmed3f(g.v1, g.v2, m);
-    // two plain selects (a nested conditional compiles to a branch)
-    const int i2 = c2 ? tile_off : g.i2;
-    g.i2 = c1 ? g.i1 : i2;
-    g.v1 = vmax(g.v1, m);
-    g.i1 = c1 ? tile_off : g.i1;
-    g.s1 = c1 ? sec : g.s1;
-  }
-}
-
-// The lane's best K as (value, relative index) lists, values with the row
-// bits cleared.
-template <int K>
-__device__ __forceinline__ void group_to_list(const GroupTop2& g, float (&val)[K], int (&ix)[K]) {
-  const int r1 = static_cast<int>(__float_as_uint(g.v1) & 3u);
-  val[0] = __uint_as_float(__float_as_uint(g.v1) & ~3u);
-  ix[0] = g.i1 + r1;
-  if constexpr (K == 2) {
-    const int ia = g.i1 + static_cast<int>(__float_as_uint(g.s1) & 3u);
-    const int ib = g.i2 + static_cast<int>(__float_as_uint(g.v2) & 3u);
-    const float va = __uint_as_float(__float_as_uint(g.s1) & ~3u);
-    const float vb = __uint_as_float(__float_as_uint(g.v2) & ~3u);
-    const bool b_first = ranks_before(vb, ib, va, ia);
-    val[1] = b_first ? vb : va;
-    ix[1] = b_first ? ib : ia;
-    // Cleared, equal values can arrive in descending index order (the row
-    // bits order ties by r); the lane merge needs (score desc, index asc)
-    // lists, or the four lanes of a query end with different lists.
-    const bool swap = ranks_before(val[1], ix[1], val[0], ix[0]);
-    const float v0 = val[0];
-    const int i0 = ix[0];
-    val[0] = swap ? val[1] : v0;
-    ix[0] = swap ? ix[1] : i0;
-    val[1] = swap ? v0 : val[1];
-    ix[1] = swap ? i0 : ix[1];
-  }
-}
 
 template <typename T, int D, int K, int QT>
 __global__ void __launch_bounds__(256)
@@ -132,17 +60,13 @@ topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __
                     POW2 ? scale : 1.f);
   }
 
+  static_assert(sizeof(T) == 4, "the register-list pass selects on exact fp32 scores");
   float val[QT][K];
   int ix[QT][K];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
     for (int m = 0; m < K; ++m) { val[qt][m] = -INFINITY; ix[qt][m] = kIdxSentinel; }
-  // bf16, k <= 2: selection by lane group (group_insert)
-  constexpr bool GROUP = sizeof(T) == 2 && K <= 2;
-  GroupTop2 g[QT];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) g[qt] = {-INFINITY, -INFINITY, -INFINITY, kIdxSentinel, kIdxSentinel};
 
   bool self_r[4];  // element r of a diagonal tile is this lane's self pair
 #pragma unroll
@@ -164,41 +88,16 @@ topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __
       const int kabs = c0 + kb0;
       f32x4 s[QT][BT];
       block_scores<F, QT, BT>(frag, Ks, kb0, LDK, lane, s);
-      if constexpr (GROUP) {
-        if constexpr (!POW2) {
+      prepare_block<QT, BT, POW2>(s, scale, self_r, q0, kabs, kend, grp);
+      rebase_list<QT, K>(ix, kabs - base);
+      base = kabs;
 #pragma unroll
-          for (int qt = 0; qt < QT; ++qt)
+      for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-            for (int t = 0; t < BT; ++t) s[qt][t] *= scale;
-        }
-        // finite mask: the row bits must not turn it into a NaN
-        mask_block<QT, BT>(s, self_r, q0, kabs, kend, grp, kMasked);
+        for (int t = 0; t < BT; ++t)
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-          g[qt].i1 -= kabs - base;
-          g[qt].i2 -= kabs - base;
-        }
-        base = kabs;
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-          for (int t = 0; t < BT; ++t) group_insert<K>(g[qt], s[qt][t], 16 * t);
-      } else {
-        prepare_block<QT, BT, POW2>(s, scale, self_r, q0, kabs, kend, grp);
-        rebase_list<QT, K>(ix, kabs - base);
-        base = kabs;
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-          for (int t = 0; t < BT; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) topk_insert<K>(val[qt], ix[qt], s[qt][t][r], 16 * t + r);
-      }
+          for (int r = 0; r < 4; ++r) topk_insert<K>(val[qt], ix[qt], s[qt][t][r], 16 * t + r);
     }
-  }
-  if constexpr (GROUP) {
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) group_to_list<K>(g[qt], val[qt], ix[qt]);
   }
   rebase_list<QT, K>(ix, -base);  // back to absolute key indices
   if (q0 >= N) return;
@@ -733,49 +632,60 @@ static hipError_t launch_wide(const TopkArgs& a) {
 template <typename T, int D>
 static hipError_t dispatch_topk(const TopkArgs& a) {
   if (a.topk > kTopkSmallMax || a.select != kSelTopk) return launch_wide<T, D>(a);
-  return launch_small<T, D>(a, a.key_chunk);
+  if constexpr (sizeof(T) == 4) return launch_small<T, D>(a, a.key_chunk);
+  return hipErrorInvalidValue;  // bf16 k <= 8 runs the packed or filter kernels
 }
 
-int g_topk_filter_mode = kFilterAuto;
+// Process-wide choice between equally exact implementations (only the time
+// differs); atomic so that concurrent calls and a concurrent setter do not race.
+static std::atomic<int> g_topk_filter_mode{kFilterAuto};
 
-// Where the filter-and-verify kernel beats the plain pass (measured on
-// MI355X). fp32: at d = 16 its fixed per-query cost (split staging, merge,
-// exact rescoring) pays off once each query scans 512 keys, or 256 keys when
-// the plain pass's per-score selection cost grows with k >= 3; at d = 32 and
-// 64 the six split products per score cost more than the selection they save
-// (N = 512: 1.2x to 1.7x slower), so it is not used. bf16 (d = 16): from
-// k = 4 and N = 256, where the plain pass's per-score insertion (15
-// operations) costs more than the filter's overhead (N = 256 to 1024: 8 to
-// 37% faster; 14% slower at N = 64); k <= 2 keeps the plain pass's group
-// selection.
-// At k <= 2 the fp32 filter also needs a large batch: with few workgroups
-// its longer per-wave chain (merge, rescoring) is not hidden (N = 512, B = 64:
-// 18.4 vs 16.0 us; B = 256: 35.0 vs 38.9 us).
-static bool filter_pays(const TopkArgs& a) {
-  if (a.dtype == kBf16) return a.topk >= 4 && a.N >= 256;
-  if (a.d != 16 || a.N < 256) return false;
-  if (a.topk >= 3) return true;
-  return a.N >= 512 && static_cast<long>(a.B) * a.N >= 131072;
+int topk_filter_mode() { return g_topk_filter_mode.load(std::memory_order_relaxed); }
+int set_topk_filter_mode(int mode) { return g_topk_filter_mode.exchange(mode); }
+
+enum TopkPath { kPathPacked, kPathFilter, kPathLists };
+
+// The implementation for k <= 8 (all three return identical results). Automatic
+// choice from timings on MI355X at B = 1024 and the configs[2]
+// bf16 grid:
+//   fp32, d = 16: N >= 512: split-bf16 filter (N=512 k=2: 100 us vs 117 lists,
+//     121 packed); N = 256, k >= 3: filter (k=4: 43 vs 46 packed, 55 lists);
+//     k <= 2 below N = 512: register lists (N=256 k=2: 36 vs 36 filter, 38
+//     packed; N=64 k=1: 5.9 vs 6.7 packed, 9.9 filter); otherwise packed
+//     (N=384 k=4: 84 vs 102 filter, 110 lists; N=128 k=4: 18 vs 20 lists).
+//   fp32, d = 32, 64: register lists for k <= 2, packed above.
+//   bf16: packed, or the filter at d = 16 with k >= 4 and N >= 256 (k=4:
+//     35 vs 42 us); the register lists do not serve bf16 (their selection
+//     would run on the approximate bf16 scores).
+static TopkPath choose_path(const TopkArgs& a, int mode) {
+  const bool filt = topk_filter_supported(a.dtype, a.d, a.topk);
+  switch (mode) {
+    case kFilterOff: return kPathPacked;
+    case kFilterAlways: return filt ? kPathFilter : kPathPacked;
+    case kFilterLegacy: return a.dtype == kF32 ? kPathLists : kPathPacked;
+    default: break;
+  }
+  if (a.dtype == kBf16) return (filt && a.topk >= 4 && a.N >= 256) ? kPathFilter : kPathPacked;
+  if (a.d == 16 && filt && (a.N >= 512 || (a.N >= 256 && a.N < 384 && a.topk >= 3))) return kPathFilter;
+  return a.topk <= 2 ? kPathLists : kPathPacked;
 }
 
 hipError_t run_topk(const TopkArgs& a) {
-  if (a.select == kSelTopk && g_topk_filter_mode != kFilterOff &&
-      topk_filter_supported(a.dtype, a.d, a.topk) &&
-      (g_topk_filter_mode == kFilterAlways || filter_pays(a)))
-    return run_topk_filter(a);
-  if (a.dtype == kF32) {
-    switch (a.d) {
-      case 8: return dispatch_topk<float, 8>(a);
-      case 16: return dispatch_topk<float, 16>(a);
-      case 32: return dispatch_topk<float, 32>(a);
-      case 64: return dispatch_topk<float, 64>(a);
+  if (a.select == kSelTopk && a.topk <= kTopkSmallMax) {
+    switch (choose_path(a, topk_filter_mode())) {
+      case kPathPacked: return run_topk_packed(a);
+      case kPathFilter: return run_topk_filter(a);
+      case kPathLists: break;
     }
-  } else {
-    switch (a.d) {
-      case 16: return dispatch_topk<bf16, 16>(a);
-      case 32: return dispatch_topk<bf16, 32>(a);
-      case 64: return dispatch_topk<bf16, 64>(a);
-    }
+  }
+  switch (a.dtype == kF32 ? a.d : -a.d) {
+    case 8: return dispatch_topk<float, 8>(a);
+    case 16: return dispatch_topk<float, 16>(a);
+    case 32: return dispatch_topk<float, 32>(a);
+    case 64: return dispatch_topk<float, 64>(a);
+    case -16: return dispatch_topk<bf16, 16>(a);
+    case -32: return dispatch_topk<bf16, 32>(a);
+    case -64: return dispatch_topk<bf16, 64>(a);
   }
   return hipErrorInvalidValue;
 }
