@@ -161,7 +161,7 @@ def main() -> int:
                              "stream2"],
                     help="run only this kernel (headline shape; zorder/stream at their configs) "
                          "--warmup + --steps times, for profiler counter passes")
-    ap.add_argument("--topk-filter", type=int, default=None, choices=[0, 1, 2, 3],
+    ap.add_argument("--topk-filter", type=int, default=None, choices=[0, 1, 2, 3, 4],
                     help="top-k implementation for --profile-kernel runs (tarmac_set_topk_filter: "
                          "0 plain, 1 automatic, 2 filter-and-verify)")
     ap.add_argument("--copy-probe", action="store_true",

@@ -58,8 +58,9 @@ def check_f32(q, k, v, kk, out, idx, exact_order=True):
 
 
 def _set_filter(mode: int) -> int:
-    """0 = packed exact pass, 1 = automatic, 2 = split-bf16 filter-and-verify
-    wherever supported, 3 = register-list pass (k <= 8)."""
+    """0 = packed pass (fp32 MFMA scores), 1 = automatic, 2 = split-bf16
+    filter-and-verify wherever supported, 3 = register-list pass (fp32),
+    4 = packed pass on split-bf16 scores (fp32, d = 16)."""
     from tarmac import _lib
     return _lib.LIB.tarmac_set_topk_filter(mode)
 
@@ -80,7 +81,7 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("mode", [0, 2, 3], ids=["packed", "filter", "lists"])
+@pytest.mark.parametrize("mode", [0, 2, 3, 4], ids=["packed", "filter", "lists", "split"])
 @pytest.mark.parametrize("N,d,kk", CASES)
 def test_fused_topk_f32_parity(N, d, kk, mode):
     B = max(2, min(16, 4096 // N))
@@ -293,7 +294,7 @@ def test_filter_path_matches_plain_fp32_path_bitwise(N, d, kk, chunk, filter_alw
     check_f32(q, k, v, kk, out_f, idx_f)
 
 
-@pytest.mark.parametrize("mode", [0, 2], ids=["packed", "filter"])
+@pytest.mark.parametrize("mode", [0, 2, 4], ids=["packed", "filter", "split"])
 @pytest.mark.parametrize("N,chunk", [(256, None), (700, 128), (2048, None)])
 def test_filter_fallback_on_ties(N, chunk, mode):
     """Duplicated keys and constant queries defeat the filter's proof; the
@@ -313,7 +314,7 @@ def test_filter_fallback_on_ties(N, chunk, mode):
         _set_filter(prev)
 
 
-@pytest.mark.parametrize("mode", [0, 2], ids=["packed", "filter"])
+@pytest.mark.parametrize("mode", [0, 2, 4], ids=["packed", "filter", "split"])
 @pytest.mark.parametrize("N,kk,chunk", [(256, 2, None), (512, 8, None), (1500, 3, 256)])
 def test_filter_near_ties(N, kk, chunk, mode):
     """Clusters of keys whose scores agree to ~1e-6 relative: candidates that

@@ -124,10 +124,12 @@ struct KnnArgs {
 
 hipError_t run_topk(const TopkArgs& a);
 hipError_t run_topk_filter(const TopkArgs& a);
-hipError_t run_topk_packed(const TopkArgs& a);
+hipError_t run_topk_packed(const TopkArgs& a, bool split);
+bool packed_split_supported(int dtype, int d);
 bool topk_filter_supported(int dtype, int d, int topk);
 // tarmac_set_topk_filter modes
-constexpr int kFilterOff = 0, kFilterAuto = 1, kFilterAlways = 2, kFilterLegacy = 3;
+constexpr int kFilterOff = 0, kFilterAuto = 1, kFilterAlways = 2, kFilterLegacy = 3,
+              kFilterPackedSplit = 4;
 int topk_filter_mode();
 int set_topk_filter_mode(int mode);  // returns the previous mode
 hipError_t run_dense(const DenseArgs& a);
@@ -142,7 +144,7 @@ void grid_knn_shape(int N, int k, int* G, int* M);
 int knn_grid_threads(int N);
 
 size_t topk_lds_bytes(int dtype, int d, int kc);
-size_t packed_lds_bytes(int dtype, int d, int kc);  // topk_packed_kernel's key copy
+size_t packed_lds_bytes(int dtype, int d, int kc, bool split);  // topk_packed_kernel's key copy
 size_t plain_lds_bytes(int dtype, int d, int kc);  // topk_small_kernel's key copy
 size_t topk_filter_lds_bytes(int dtype, int d, int kc);
 size_t dense_lds_bytes(int dtype, int d, int kc);

@@ -643,37 +643,41 @@ static std::atomic<int> g_topk_filter_mode{kFilterAuto};
 int topk_filter_mode() { return g_topk_filter_mode.load(std::memory_order_relaxed); }
 int set_topk_filter_mode(int mode) { return g_topk_filter_mode.exchange(mode); }
 
-enum TopkPath { kPathPacked, kPathFilter, kPathLists };
+enum TopkPath { kPathPacked, kPathPackedSplit, kPathFilter, kPathLists };
 
-// The implementation for k <= 8 (all three return identical results). Automatic
-// choice from timings on MI355X at B = 1024 and the configs[2]
-// bf16 grid:
-//   fp32, d = 16: N >= 512: split-bf16 filter (N=512 k=2: 100 us vs 117 lists,
-//     121 packed); N = 256, k >= 3: filter (k=4: 43 vs 46 packed, 55 lists);
-//     k <= 2 below N = 512: register lists (N=256 k=2: 36 vs 36 filter, 38
-//     packed; N=64 k=1: 5.9 vs 6.7 packed, 9.9 filter); otherwise packed
-//     (N=384 k=4: 84 vs 102 filter, 110 lists; N=128 k=4: 18 vs 20 lists).
-//   fp32, d = 32, 64: register lists for k <= 2, packed above.
-//   bf16: packed, or the filter at d = 16 with k >= 4 and N >= 256 (k=4:
-//     35 vs 42 us); the register lists do not serve bf16 (their selection
-//     would run on the approximate bf16 scores).
+// The implementation for k <= 8 (all return identical results). Automatic
+// choice from interleaved timings on MI355X (B = 1024 for fp32 d = 16, the
+// configs[1] sweep; the configs[2] bf16 grid), us:
+//   fp32, d = 16: the packed pass on split-bf16 scores from N = 256 (N=256
+//     k=2: 33.5 vs lists 35.6, filter 34.5; k=4: 41.4 vs 44.1 filter, 55.9
+//     lists; N=512 k=2: 90.5 vs 96.2 filter, 117.7 lists), except k = 1 below
+//     N = 512 (lists: 28.6 vs 30.8 at N=256); below N = 256 the register
+//     lists for k <= 2 (N=64 k=1: 5.9 vs 6.7 packed, 9.2 split) and the
+//     fp32-MFMA packed pass above (N=128 k=4: 17.9 vs 19.9 lists).
+//   fp32, d = 8, 32, 64: register lists for k <= 2, packed above.
+//   bf16: packed, or the bf16 filter at d = 16 with k >= 4 and N >= 256
+//     (B=1024 N=256 k=4: 35.1 vs 40.4); the register lists do not serve bf16
+//     (their selection would run on the approximate bf16 scores).
 static TopkPath choose_path(const TopkArgs& a, int mode) {
   const bool filt = topk_filter_supported(a.dtype, a.d, a.topk);
+  const bool split = packed_split_supported(a.dtype, a.d);
   switch (mode) {
     case kFilterOff: return kPathPacked;
     case kFilterAlways: return filt ? kPathFilter : kPathPacked;
     case kFilterLegacy: return a.dtype == kF32 ? kPathLists : kPathPacked;
+    case kFilterPackedSplit: return split ? kPathPackedSplit : kPathPacked;
     default: break;
   }
   if (a.dtype == kBf16) return (filt && a.topk >= 4 && a.N >= 256) ? kPathFilter : kPathPacked;
-  if (a.d == 16 && filt && (a.N >= 512 || (a.N >= 256 && a.N < 384 && a.topk >= 3))) return kPathFilter;
+  if (split && a.N >= 256 && (a.topk >= 2 || a.N >= 512)) return kPathPackedSplit;
   return a.topk <= 2 ? kPathLists : kPathPacked;
 }
 
 hipError_t run_topk(const TopkArgs& a) {
   if (a.select == kSelTopk && a.topk <= kTopkSmallMax) {
     switch (choose_path(a, topk_filter_mode())) {
-      case kPathPacked: return run_topk_packed(a);
+      case kPathPacked: return run_topk_packed(a, false);
+      case kPathPackedSplit: return run_topk_packed(a, true);
       case kPathFilter: return run_topk_filter(a);
       case kPathLists: break;
     }

@@ -41,6 +41,7 @@
 #include "exact.hpp"
 #include "frag.hpp"
 #include "select.hpp"
+#include "split.hpp"
 #include "tarmac_internal.hpp"
 
 namespace tarmac {
@@ -111,6 +112,32 @@ __device__ __forceinline__ void flush_packed(float (&pv)[QT][NS][L], float (&rv)
       }
 }
 
+// Scoring per input: the query fragment, the LDS key row (element type and
+// stride) and its staging. fp32: exact fp32 MFMA scores from plain rows, or
+// (SPLIT) bf16 MFMA on three-way split operands (x = hi + mid + lo), which
+// approximates the fp32 dot to 2^-21 sum_c |q_c k_c| at a third of the MFMA
+// cycles; bf16: bf16 MFMA on the plain rows.
+template <typename T, int D, bool SPLIT>
+struct PackedIn;
+template <int D>
+struct PackedIn<float, D, false> {
+  using F = Frag<float, D>;
+  using R = float;
+  static constexpr int LDK = F::LDK;
+};
+template <int D>
+struct PackedIn<float, D, true> {
+  using F = SplitFrag<D>;
+  using R = bf16;
+  static constexpr int LDK = SplitFrag<D>::LDK;
+};
+template <int D>
+struct PackedIn<bf16, D, false> {
+  using F = Frag<bf16, D>;
+  using R = bf16;
+  static constexpr int LDK = F::LDK;
+};
+
 // k-softmax over a query's K retained scores (score desc) and the gathered
 // aggregation of their value rows; this lane writes channels grp*D/4 .. of
 // query qi, and lane row 0 the retained indices.
@@ -147,24 +174,27 @@ __device__ __forceinline__ void finish_tile(const T* __restrict__ V, T* __restri
   }
 }
 
-template <typename T, int D, int K, int QT, int NS, int FB, bool ONESEG>
-__global__ void __launch_bounds__(256)
+template <typename T, int D, int K, int QT, int NS, int FB, bool ONESEG, bool SPLIT>
+__global__ void __launch_bounds__(512)
 topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
                    T* __restrict__ O, int32_t* __restrict__ Idx, int N, int n_qblk, int kc,
                    float scale, int nblocks) {
-  using F = Frag<T, D>;
-  constexpr int LDK = F::LDK;
+  using PI = PackedIn<T, D, SPLIT>;
+  using F = typename PI::F;
+  using R = typename PI::R;  // LDS key row element
+  constexpr int LDK = PI::LDK;
   constexpr int BT = kPackedBlockTiles;     // 16-key tiles per scan block
   constexpr int BK = 16 * BT;
   constexpr int C = K + 1;                   // candidates rescored when needed
   constexpr int L = K + 2;                   // list entries: the candidates and the (K+2)-th
-  constexpr bool EXACT = sizeof(T) == 4;     // fp32 MFMA scores are the canonical scores
+  constexpr bool EXACT = sizeof(T) == 4 && !SPLIT;  // fp32 MFMA scores are the canonical scores
+  constexpr bool RESCORE = sizeof(T) == 4;  // fp32 softmax needs the canonical scores
   constexpr bool POW2 = pow2_scale<D>();
   constexpr uint32_t FM = (1u << FB) - 1u;
   constexpr int SEGK = seg_keys<FB>();
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  unsigned* kmax_slot = reinterpret_cast<unsigned*>(smem_raw);  // bf16: max |k|^2 of the row
-  T* Ks = reinterpret_cast<T*>(smem_raw + 16);
+  unsigned* kmax_slot = reinterpret_cast<unsigned*>(smem_raw);  // approximate scores: max |k|^2
+  R* Ks = reinterpret_cast<R*>(smem_raw + 16);
 
   const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -183,9 +213,13 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
     const int qi = min(q0 + 16 * qt + col, N - 1);
     // fp32: a power-of-two scale folds into q exactly (canonical order);
     // bf16: raw scores (the bound is scaled instead)
-    frag[qt].load_q(Qb + static_cast<size_t>(qi) * D, grp, (EXACT && POW2) ? scale : 1.f);
-    if constexpr (!EXACT) qn2[qt] = bf16_frag_norm2<D>(frag[qt]);
-    else qn2[qt] = 0.f;
+    if constexpr (SPLIT) {
+      qn2[qt] = F::row_norm2(frag[qt].load_q(Qb + static_cast<size_t>(qi) * D, grp));
+    } else {
+      frag[qt].load_q(Qb + static_cast<size_t>(qi) * D, grp, (EXACT && POW2) ? scale : 1.f);
+      if constexpr (!EXACT) qn2[qt] = bf16_frag_norm2<D>(frag[qt]);
+      else qn2[qt] = 0.f;
+    }
   }
   bool self_r[4];  // element r of a diagonal tile is this lane's self pair
 #pragma unroll
@@ -219,10 +253,15 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
       __syncthreads();
     } else {
       if (threadIdx.x == 0) *kmax_slot = 0u;
-      const float mine = stage_bf16_norm<D, LDK>(reinterpret_cast<bf16*>(Ks),
-                                                 reinterpret_cast<const bf16*>(Kb) +
-                                                     static_cast<size_t>(c0) * D,
-                                                 cn, cnb);
+      float mine;
+      if constexpr (SPLIT) {
+        bool exact_split = true;  // only the LDS rebuild needs it; the fallback reads global rows
+        mine = stage_split<D>(Ks, Kb + static_cast<size_t>(c0) * D, cn, cnb, exact_split);
+      } else {
+        mine = stage_bf16_norm<D, LDK>(reinterpret_cast<bf16*>(Ks),
+                                       reinterpret_cast<const bf16*>(Kb) + static_cast<size_t>(c0) * D,
+                                       cn, cnb);
+      }
       __syncthreads();
       atomicMax(kmax_slot, __float_as_uint(mine));  // non-negative: bit order is value order
     }
@@ -373,7 +412,7 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
 #pragma unroll
       for (int m = 0; m + 1 < K; ++m) ordered = ordered && sep[m];
       const bool normal = nprod < kPackedNormLimit;
-      fast = self >= N || (normal && ordered && sep[K - 1]);
+      fast = !SPLIT && (self >= N || (normal && ordered && sep[K - 1]));
       ok[qt] = self >= N || (normal && (sep[K - 1] || sep[K]));
 #pragma unroll
       for (int m = 0; m < K; ++m) {
@@ -381,7 +420,7 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
         ix[qt][m] = cand[qt][m];
       }
     }
-    if (EXACT || !__all(fast)) {
+    if (RESCORE || !__all(fast)) {
       float cv[C];
 #pragma unroll
       for (int u = 0; u < (C + 3) / 4; ++u) {
@@ -391,8 +430,13 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
         for (int mm = 0; mm < C; ++mm)
           if (mm == m) c = cand[qt][mm];
         const int row = min(max(c, 0), N - 1);
-        const float e = lds_all ? canon_from_frag<T, D, POW2>(frag[qt], Ks + row * LDK, scale)
-                                : canon_from_frag<T, D, POW2>(frag[qt], Kb + static_cast<size_t>(row) * D, scale);
+        float e;
+        if constexpr (SPLIT)
+          e = canon_pair<T, D, POW2>(Qb + static_cast<size_t>(min(self, N - 1)) * D,
+                                     Kb + static_cast<size_t>(row) * D, scale);
+        else
+          e = lds_all ? canon_from_frag<T, D, POW2>(frag[qt], Ks + row * LDK, scale)
+                      : canon_from_frag<T, D, POW2>(frag[qt], Kb + static_cast<size_t>(row) * D, scale);
         uint32_t g4[4];
         gather_rows(__float_as_uint(c < 0 ? -INFINITY : e), g4);
 #pragma unroll
@@ -403,6 +447,13 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
 #pragma unroll
       for (int m = 0; m < C; ++m) ci[m] = cand[qt][m];
       sort_lex<C>(cv, ci);
+      if constexpr (SPLIT) {
+        // every key outside the candidates scores at most the (K+2)-th
+        // entry's ceiling plus the split error
+        const float nprod = sqrtf(qn2[qt]) * kmax;
+        const float bound = (trunc_ceiling(pl[qt][K + 1], FM) + packed_eps<D>() * nprod) * scale;
+        ok[qt] = self >= N || (nprod < kPackedNormLimit && bound < cv[K - 1]);
+      }
       if (!fast) {
 #pragma unroll
         for (int m = 0; m < K; ++m) {
@@ -424,7 +475,9 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
     if (!__all(ok[qt])) {
       float ev[K];
       int ei[K];
-      exact_tile_plain<T, D, K, LDK>(Qb, Kb, Ks, lds_all, N, q0 + 16 * qt, scale, lane, ev, ei);
+      // split rows in LDS do not serve the exact pass: it reads global rows then
+      exact_tile_plain<T, D, K, LDK>(Qb, Kb, reinterpret_cast<const T*>(Ks), lds_all && !SPLIT, N,
+                                     q0 + 16 * qt, scale, lane, ev, ei);
       finish_tile<T, D, K>(V, O, Idx, b, N, q0 + 16 * qt + col, grp, ev, ei);
     }
   }
@@ -439,76 +492,86 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
 // bound by the insertion chains' latency.
 constexpr int kPackedSubLists = 1;
 
-size_t packed_lds_bytes(int dtype, int d, int kc) {
-  const int row = dtype == kF32 ? (d + 4) * 4 : (d + 8) * 2;
+size_t packed_lds_bytes(int dtype, int d, int kc, bool split) {
+  const int row = dtype == kF32 ? (split ? (3 * d + 8) * 2 : (d + 4) * 4) : (d + 8) * 2;
   const int kcb = (kc + kBlockKeys - 1) / kBlockKeys * kBlockKeys;
   return 16 + static_cast<size_t>(kcb) * row;
 }
 
-template <typename T, int D, int K, int QT, int NS, int FB, bool ONESEG>
+template <typename T, int D, int K, int QT, int NS, int FB, bool ONESEG, bool SPLIT>
 static void launch_packed_k(const TopkArgs& a, int kc, int nblocks, int n_qblk, int nw, size_t lds) {
-  hipLaunchKernelGGL((topk_packed_kernel<T, D, K, QT, NS, FB, ONESEG>), dim3(nblocks), dim3(64 * nw),
-                     lds, static_cast<hipStream_t>(a.stream), static_cast<const T*>(a.q),
-                     static_cast<const T*>(a.k), static_cast<const T*>(a.v),
-                     static_cast<T*>(a.out), a.idx, a.N, n_qblk, kc, a.scale, nblocks);
+  hipLaunchKernelGGL((topk_packed_kernel<T, D, K, QT, NS, FB, ONESEG, SPLIT>), dim3(nblocks),
+                     dim3(64 * nw), lds, static_cast<hipStream_t>(a.stream),
+                     static_cast<const T*>(a.q), static_cast<const T*>(a.k),
+                     static_cast<const T*>(a.v), static_cast<T*>(a.out), a.idx, a.N, n_qblk, kc,
+                     a.scale, nblocks);
 }
 
-template <typename T, int D, int K>
+template <typename T, int D, int K, bool SPLIT>
 static hipError_t launch_packed_shape(const TopkArgs& a) {
   constexpr int QT = kTopkQueryTiles;
+  constexpr int NS = kPackedSubLists;
   const int per_wave = 16 * QT;
   const int waves = (a.N + per_wave - 1) / per_wave;
-  const int nw = waves >= 4 ? 4 : waves;
+  // rows of 512 keys and more: eight waves share one staged key copy (half
+  // the staging, and a 57 KB split copy at N = 512 leaves eight waves per CU
+  // either way), unless that leaves fewer than two workgroups per CU
+  const long wide_groups = static_cast<long>(a.B) * ((a.N + 8 * per_wave - 1) / (8 * per_wave));
+  const int maxw = (a.N >= 512 && wide_groups >= 2L * kCUs) ? 8 : 4;
+  const int nw = waves >= maxw ? maxw : waves;
   const int qb = per_wave * nw;
   const int n_qblk = (a.N + qb - 1) / qb;
   const int nblocks = a.B * n_qblk;
   const int kc = a.key_chunk;
-  const size_t lds = packed_lds_bytes(a.dtype, D, kc);
+  const size_t lds = packed_lds_bytes(a.dtype, D, kc, SPLIT);
   // one segment when a single chunk holds the whole row: 8 field bits up to
   // N = 256 (a truncation of 2^-15 of the score), 10 up to 1024. bf16 always
   // packs 10 bits: its softmax runs on the truncated scores, which must not
   // depend on whether the row is streamed.
   if constexpr (sizeof(T) == 4) {
     if (kc >= a.N && a.N <= 256) {
-      launch_packed_k<T, D, K, QT, kPackedSubLists, 8, true>(a, kc, nblocks, n_qblk, nw, lds);
+      launch_packed_k<T, D, K, QT, NS, 8, true, SPLIT>(a, kc, nblocks, n_qblk, nw, lds);
       return hipGetLastError();
     }
   }
   if (kc >= a.N && a.N <= 1024)
-    launch_packed_k<T, D, K, QT, kPackedSubLists, 10, true>(a, kc, nblocks, n_qblk, nw, lds);
+    launch_packed_k<T, D, K, QT, NS, 10, true, SPLIT>(a, kc, nblocks, n_qblk, nw, lds);
   else
-    launch_packed_k<T, D, K, QT, kPackedSubLists, 10, false>(a, kc, nblocks, n_qblk, nw, lds);
+    launch_packed_k<T, D, K, QT, NS, 10, false, SPLIT>(a, kc, nblocks, n_qblk, nw, lds);
   return hipGetLastError();
 }
 
-template <typename T, int D>
+template <typename T, int D, bool SPLIT>
 static hipError_t launch_packed(const TopkArgs& a) {
   switch (a.topk) {
-    case 1: return launch_packed_shape<T, D, 1>(a);
-    case 2: return launch_packed_shape<T, D, 2>(a);
-    case 3: return launch_packed_shape<T, D, 3>(a);
-    case 4: return launch_packed_shape<T, D, 4>(a);
-    case 5: return launch_packed_shape<T, D, 5>(a);
-    case 6: return launch_packed_shape<T, D, 6>(a);
-    case 7: return launch_packed_shape<T, D, 7>(a);
-    case 8: return launch_packed_shape<T, D, 8>(a);
+    case 1: return launch_packed_shape<T, D, 1, SPLIT>(a);
+    case 2: return launch_packed_shape<T, D, 2, SPLIT>(a);
+    case 3: return launch_packed_shape<T, D, 3, SPLIT>(a);
+    case 4: return launch_packed_shape<T, D, 4, SPLIT>(a);
+    case 5: return launch_packed_shape<T, D, 5, SPLIT>(a);
+    case 6: return launch_packed_shape<T, D, 6, SPLIT>(a);
+    case 7: return launch_packed_shape<T, D, 7, SPLIT>(a);
+    case 8: return launch_packed_shape<T, D, 8, SPLIT>(a);
   }
   return hipErrorInvalidValue;
 }
 
-hipError_t run_topk_packed(const TopkArgs& a) {
+bool packed_split_supported(int dtype, int d) { return dtype == kF32 && d == 16; }
+
+hipError_t run_topk_packed(const TopkArgs& a, bool split) {
   if (a.dtype == kF32) {
+    if (split) return a.d == 16 ? launch_packed<float, 16, true>(a) : hipErrorInvalidValue;
     switch (a.d) {
-      case 8: return launch_packed<float, 8>(a);
-      case 16: return launch_packed<float, 16>(a);
-      case 32: return launch_packed<float, 32>(a);
-      case 64: return launch_packed<float, 64>(a);
+      case 8: return launch_packed<float, 8, false>(a);
+      case 16: return launch_packed<float, 16, false>(a);
+      case 32: return launch_packed<float, 32, false>(a);
+      case 64: return launch_packed<float, 64, false>(a);
     }
   } else {
     switch (a.d) {
-      case 16: return launch_packed<bf16, 16>(a);
-      case 32: return launch_packed<bf16, 32>(a);
-      case 64: return launch_packed<bf16, 64>(a);
+      case 16: return launch_packed<bf16, 16, false>(a);
+      case 32: return launch_packed<bf16, 32, false>(a);
+      case 64: return launch_packed<bf16, 64, false>(a);
     }
   }
   return hipErrorInvalidValue;
