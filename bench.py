@@ -43,10 +43,9 @@ B, N, D = 1024, 256, 16
 KS = (1, 2, 4)
 VALUE_K = 2
 # The kernel the value call dispatches to at this shape (fp32, d=16, k=2,
-# N=256: the plain fp32 pass; the filter-and-verify kernel takes over at
-# k >= 3, or N >= 512 with large batches). Its launch is what rocprofv3
-# reports under this name.
-VALUE_KERNEL = "tarmac::topk_small_kernel<float, 16, 2, 2>"
+# N=256: the packed selection pass on split-bf16 scores). Its launch is what
+# rocprofv3 reports under this name.
+VALUE_KERNEL = "tarmac::topk_packed_kernel<float, 16, 2, 2, 1, 8, true, true>"
 METRIC_FALLBACK = "µs/call attention core, top-k vs dense ratio, N=256 d=16 k=1,2,4; %HBM peak"
 
 

@@ -649,11 +649,11 @@ enum TopkPath { kPathPacked, kPathPackedSplit, kPathFilter, kPathLists };
 // choice from interleaved timings on MI355X (B = 1024 for fp32 d = 16, the
 // configs[1] sweep; the configs[2] bf16 grid), us:
 //   fp32, d = 16: the packed pass on split-bf16 scores from N = 256 (N=256
-//     k=2: 33.5 vs lists 35.6, filter 34.5; k=4: 41.4 vs 44.1 filter, 55.9
-//     lists; N=512 k=2: 90.5 vs 96.2 filter, 117.7 lists), except k = 1 below
-//     N = 512 (lists: 28.6 vs 30.8 at N=256); below N = 256 the register
-//     lists for k <= 2 (N=64 k=1: 5.9 vs 6.7 packed, 9.2 split) and the
-//     fp32-MFMA packed pass above (N=128 k=4: 17.9 vs 19.9 lists).
+//     k=1: 28.4 vs lists 30.4; k=2: 31.1 vs 37.1 lists, 34.5 filter; k=4:
+//     38.1 vs 44.1 filter, 56.5 lists; N=512 k=2: 83.5 vs 96.2 filter, 117.4
+//     lists); below N = 256 the register lists for k <= 2 (N=64 k=1: 5.9 vs
+//     6.7 packed, 9.2 split) and the fp32-MFMA packed pass above (N=128 k=4:
+//     17.9 vs 19.9 lists).
 //   fp32, d = 8, 32, 64: register lists for k <= 2, packed above.
 //   bf16: packed, or the bf16 filter at d = 16 with k >= 4 and N >= 256
 //     (B=1024 N=256 k=4: 35.1 vs 40.4); the register lists do not serve bf16
@@ -669,7 +669,7 @@ static TopkPath choose_path(const TopkArgs& a, int mode) {
     default: break;
   }
   if (a.dtype == kBf16) return (filt && a.topk >= 4 && a.N >= 256) ? kPathFilter : kPathPacked;
-  if (split && a.N >= 256 && (a.topk >= 2 || a.N >= 512)) return kPathPackedSplit;
+  if (split && a.N >= 256) return kPathPackedSplit;
   return a.topk <= 2 ? kPathLists : kPathPacked;
 }
 

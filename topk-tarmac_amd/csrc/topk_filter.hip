@@ -295,9 +295,15 @@ topk_filter_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
     }
     bool exact = true;
     const float mine = FI::stage(Ks, Kb + static_cast<size_t>(c0) * D, cn, cnb, exact);
-    if (!exact) atomicOr(inexact_slot, 1u);
+    // one LDS atomic per wave (a per-lane atomic compiles to a 64-step
+    // readlane loop); non-negative floats order like their bits
+    const float wmax = wave_max_rows(mine);
+    const bool wexact = __all(exact);
     __syncthreads();
-    atomicMax(kmax_slot, __float_as_uint(mine));  // non-negative: bit order is value order
+    if (lane == 0) {
+      atomicMax(kmax_slot, __float_as_uint(wmax));
+      if (!wexact) atomicOr(inexact_slot, 1u);
+    }
     if (q0 < N) {
       const int kend = c0 + cn;
       for (int kb0 = 0; kb0 < cnb; kb0 += 16 * BT) {

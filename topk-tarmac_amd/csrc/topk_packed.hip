@@ -262,8 +262,11 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
                                        reinterpret_cast<const bf16*>(Kb) + static_cast<size_t>(c0) * D,
                                        cn, cnb);
       }
+      // one LDS atomic per wave (a per-lane atomic compiles to a 64-step
+      // readlane loop); non-negative floats order like their bits
+      const float wmax = wave_max_rows(mine);
       __syncthreads();
-      atomicMax(kmax_slot, __float_as_uint(mine));  // non-negative: bit order is value order
+      if (lane == 0) atomicMax(kmax_slot, __float_as_uint(wmax));
     }
     if (q0 < N) {
       const int kend = c0 + cn;  // rows past the chunk end are zero padding
