@@ -58,6 +58,13 @@ weights_attention           equals topk_gather when the kept set is the
                             top-k set
 canon_topk (C)              numpy oracle: same sets off near-ties, outputs to
                             1e-6; brute force of the fmaf chain in Python
+score_error_bound           exact-rational error of canonical scores (random,
+                            cancellation-heavy and constructed worst-case
+                            chains) stays within it; the constructed chain
+                            reaches over 0.85 of it (tight, so a halved bound,
+                            gamma_d or a dropped |.| or scale fails)
+near_tie_rows               brute force on Python-sorted rows; exact gaps at
+                            the eps boundary; k >= N-1 rows
 canon_morton_window (C)     numpy oracle bit-exact (codes and indices)
 ==========================  ===================================================
 """
@@ -404,11 +411,17 @@ def near_tie_rows(s: np.ndarray, topk: int, eps: np.ndarray | float) -> np.ndarr
 
 
 def score_error_bound(q, k) -> np.ndarray:
-    """Forward error bound for an fp32 dot of length d, ``[B, N, N]``:
-    ``gamma_{d+1} * sum_c |q_c k_c| / sqrt(d)`` with ``gamma_m = m u / (1 - m u)``."""
+    """Twice the forward error bound of one canonical fp32 score, ``[B, N, N]``:
+    ``2 * gamma_{d+2} * sum_c |q_c k_c| / sqrt(d)`` with
+    ``gamma_m = m u / (1 - m u)``, ``u = 2^-24``. One score is the fmaf chain
+    (d roundings, each at most u times the running partial, which is at most
+    ``sum_c |q_c k_c|``) times fp32(1/sqrt(d)) (the constant's own rounding
+    and the product's: two more). Twice that bounds how far two scores' order
+    can move, so rows whose k-th and (k+1)-th scores are closer are the ones
+    where the fp32 selection may legitimately differ from exact arithmetic."""
     d = q.shape[-1]
     u = 2.0 ** -24
-    g = (d + 1) * u / (1 - (d + 1) * u)
+    g = (d + 2) * u / (1 - (d + 2) * u)
     a = np.matmul(np.abs(q.astype(np.float64)), np.abs(np.swapaxes(k, -1, -2)).astype(np.float64))
     return 2 * g * a / np.sqrt(d)
 

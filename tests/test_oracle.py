@@ -648,3 +648,156 @@ def test_pins_reject_planted_mistakes(golden):
         assert not pin_grid_knn(O.select_grid_knn, golden)
     finally:
         O.grid_cells = real_cells
+
+
+# ---------------------------------------------------------------------------
+# score_error_bound and near_tie_rows
+# ---------------------------------------------------------------------------
+
+def _chain_order(d):
+    """Elements of a row in the canonical chain's order: c = kk*(d/4) + t at
+    step t, slot kk."""
+    return [kk * (d // 4) + t for t in range(d // 4) for kk in range(4)]
+
+
+def _worst_case_pair(d):
+    """A query/key pair whose canonical score loses close to half an ulp at
+    every one of its d roundings, in the same direction: the first product
+    (1 + 2^-23)(1 - 2^-24) = 1 + 2^-24 - 2^-47 rounds down to 1, and every later
+    term 2^-24 - 2^-34 is just under half an ulp of the running 1.0, so it is
+    lost too. Returns q, k as [1, 2, d] (query 0 against key 1)."""
+    q = np.zeros((1, 2, d), np.float32)
+    k = np.zeros((1, 2, d), np.float32)
+    order = _chain_order(d)
+    q[0, 0, order[0]] = np.float32(1 + 2.0 ** -23)
+    k[0, 1, order[0]] = np.float32(1 - 2.0 ** -24)
+    for c in order[1:]:
+        q[0, 0, c] = np.float32(2.0 ** -24 - 2.0 ** -34)
+        k[0, 1, c] = np.float32(1.0)
+    return q, k
+
+
+def _score_errors(q, k):
+    """|canonical fp32 score - exact q.k/sqrt(d)| for every off-diagonal pair,
+    evaluated in 60-digit decimal from the exact rational dot."""
+    import decimal
+    ctx = decimal.Context(prec=60)
+    d = q.shape[-1]
+    inv_sqrt = ctx.divide(decimal.Decimal(1), ctx.sqrt(decimal.Decimal(d)))
+    s = O.canon_scores(q, k)
+    B, N, _ = q.shape
+    err = np.zeros((B, N, N))
+    for b in range(B):
+        for i in range(N):
+            for j in range(N):
+                if i == j:
+                    continue
+                dot = sum(Fraction(float(q[b, i, c])) * Fraction(float(k[b, j, c])) for c in range(d))
+                exact = ctx.multiply(ctx.divide(decimal.Decimal(dot.numerator),
+                                                decimal.Decimal(dot.denominator)), inv_sqrt)
+                err[b, i, j] = float(abs(ctx.subtract(decimal.Decimal(float(s[b, i, j])), exact)))
+    return err
+
+
+def _cancelling_rows(d, seed):
+    """Rows whose products nearly cancel: large alternating terms and a small
+    remainder, so |q.k| is far below sum |q_c k_c|."""
+    rng = np.random.default_rng(seed)
+    q = np.empty((1, 4, d), np.float32)
+    k = np.empty((1, 4, d), np.float32)
+    big = rng.uniform(50, 100, (4, d // 2)).astype(np.float32)
+    q[0, :, 0::2] = big
+    q[0, :, 1::2] = -big * np.float32(1 + 2.0 ** -20)
+    k[0] = rng.uniform(0.999, 1.001, (4, d)).astype(np.float32)
+    return q, k
+
+
+def pin_score_error_bound(bound_fn) -> bool:
+    """The bound must dominate the exact error of every canonical score
+    (random, cancellation-heavy and worst-case chains), and the worst-case
+    chain must reach at least 0.85 of it (the bound is tight, not just safe:
+    0.89 at d = 16, 0.95 at d = 32)."""
+    for d in (16, 32):
+        cases = [qkv(d + 1, 2, 5, d)[:2], _cancelling_rows(d, d), _worst_case_pair(d)]
+        for q, k in cases:
+            single = bound_fn(q, k) / 2
+            err = _score_errors(q, k)
+            off = np.broadcast_to(~np.eye(q.shape[1], dtype=bool), err.shape)
+            if not np.all(err[off] <= single[off]):
+                return False
+        q, k = _worst_case_pair(d)
+        if _score_errors(q, k)[0, 0, 1] < 0.85 * bound_fn(q, k)[0, 0, 1] / 2:
+            return False
+    return True
+
+
+def pin_near_tie_rows(fn) -> bool:
+    """Brute force over Python-sorted rows, and exact gaps at the boundary."""
+    rng = np.random.default_rng(3)
+    s = rng.standard_normal((40, 9))
+    s[:, 0] = -np.inf  # a masked self pair
+    for kk in (1, 2, 4, 7):
+        eps = rng.uniform(0, 0.5, 40)
+        want = []
+        for row, e in zip(s, eps):
+            srt = sorted(row.tolist(), reverse=True)
+            want.append(srt[kk - 1] - srt[kk] <= e)
+        if not np.array_equal(fn(s, kk, eps), np.array(want)):
+            return False
+    row = np.array([[-np.inf, 5.0, 4.0, 3.0, 2.75, 1.0]])
+    if not (fn(row, 3, 0.25)[0] and not fn(row, 3, 0.2)[0] and not fn(row, 2, 0.25)[0]):
+        return False
+    return not fn(row, 6, 10.0)[0]  # no (k+1)-th score: never a near-tie
+
+
+def test_score_error_bound_pinned():
+    assert pin_score_error_bound(O.score_error_bound)
+
+
+def test_near_tie_rows_pinned():
+    assert pin_near_tie_rows(O.near_tie_rows)
+
+
+def test_error_bound_pins_reject_planted_mistakes():
+    u = 2.0 ** -24
+
+    def halved(q, k):
+        return O.score_error_bound(q, k) / 2
+
+    def gamma_d(q, k):                 # counts d roundings: misses the scale's two
+        d = q.shape[-1]
+        a = np.matmul(np.abs(q.astype(np.float64)), np.abs(np.swapaxes(k, -1, -2)).astype(np.float64))
+        return 2 * (d * u / (1 - d * u)) * a / np.sqrt(d)
+
+    def no_abs(q, k):                  # |q.k| instead of sum |q_c k_c|
+        d = q.shape[-1]
+        g = (d + 2) * u / (1 - (d + 2) * u)
+        return 2 * g * np.abs(np.matmul(q.astype(np.float64),
+                                        np.swapaxes(k, -1, -2).astype(np.float64))) / np.sqrt(d)
+
+    def no_scale(q, k):                # forgets the 1/sqrt(d): safe but sqrt(d) too loose
+        return O.score_error_bound(q, k) * np.sqrt(q.shape[-1])
+
+    for mutant in (halved, gamma_d, no_abs, no_scale):
+        assert not pin_score_error_bound(mutant), mutant.__name__
+
+    def strict(s, kk, eps):
+        srt = -np.sort(-s, axis=-1)
+        if kk >= s.shape[-1]:
+            return np.zeros(s.shape[:-1], dtype=bool)
+        return srt[..., kk - 1] - srt[..., kk] < eps
+
+    def off_by_one(s, kk, eps):
+        srt = -np.sort(-s, axis=-1)
+        if kk >= s.shape[-1]:
+            return np.zeros(s.shape[:-1], dtype=bool)
+        return srt[..., max(kk - 2, 0)] - srt[..., kk - 1] <= eps
+
+    def ascending(s, kk, eps):
+        srt = np.sort(s, axis=-1)
+        if kk >= s.shape[-1]:
+            return np.zeros(s.shape[:-1], dtype=bool)
+        return np.abs(srt[..., kk - 1] - srt[..., kk]) <= eps
+
+    for mutant in (strict, off_by_one, ascending):
+        assert not pin_near_tie_rows(mutant), mutant.__name__

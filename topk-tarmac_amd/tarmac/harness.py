@@ -21,9 +21,9 @@ Follows the reference harness:
 
 from __future__ import annotations
 
-import statistics
 from typing import Any, Callable
 
+import numpy as np
 import torch
 
 #: MI355X datasheet peaks used for roofline fractions.
@@ -61,11 +61,11 @@ def analytic_bytes(path: str, B: int, N: int, d: int, k: int = 0, itemsize: int 
     raise ValueError(path)
 
 
-def event_time(fn: Callable[[], Any], stream: torch.cuda.Stream | None = None) -> float:
-    """Milliseconds of one call, bracketed by events on the launch stream."""
-    stream = stream or torch.cuda.current_stream()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+def _elapsed_ms(fn: Callable[[], Any], start: torch.cuda.Event, end: torch.cuda.Event) -> float:
+    """Device time of one call: the event pair sits on the stream current
+    during the call, and the host waits for the second event before the next
+    call starts (calls never overlap)."""
+    stream = torch.cuda.current_stream()
     start.record(stream)
     fn()
     end.record(stream)
@@ -74,59 +74,60 @@ def event_time(fn: Callable[[], Any], stream: torch.cuda.Stream | None = None) -
 
 
 def time_interleaved(fns: dict[str, Callable[[], Any]], reps: int, warmup: int,
-                     runs: int) -> dict[str, list[list[float]]]:
-    """Interleave every function repetition by repetition; raw samples (ms)
-    per run."""
+                     runs: int) -> dict[str, np.ndarray]:
+    """Round-robin timing: in every repetition each callable runs once, in
+    turn. Returns per callable an array [runs, reps] of milliseconds."""
     names = list(fns)
+    samples = np.zeros((len(names), runs, reps))
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
     with torch.no_grad():
         for _ in range(warmup):
-            for n in names:
-                fns[n]()
+            for name in names:
+                fns[name]()
         torch.cuda.synchronize()
-        out: dict[str, list[list[float]]] = {n: [] for n in names}
-        for _ in range(runs):
-            block: dict[str, list[float]] = {n: [] for n in names}
-            for _ in range(reps):
-                for n in names:
-                    block[n].append(event_time(fns[n]))
-            for n in names:
-                out[n].append(block[n])
-    return out
+        for run in range(runs):
+            for rep in range(reps):
+                for i, name in enumerate(names):
+                    samples[i, run, rep] = _elapsed_ms(fns[name], start, end)
+    return {name: samples[i] for i, name in enumerate(names)}
 
 
 def as_graphs(fns: dict[str, Callable[[], Any]]) -> dict[str, Callable[[], Any]]:
-    """Capture each call in its own graph; return the replays."""
-    out: dict[str, Callable[[], Any]] = {}
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side), torch.no_grad():
-        for f in fns.values():
+    """Capture each callable into a graph of its own and return the replays.
+    A few eager calls first keep any one-time setup out of the capture; the
+    wrappers read the current stream, which during capture is the capture
+    stream."""
+    graphs: dict[str, torch.cuda.CUDAGraph] = {}
+    with torch.no_grad():
+        for name, fn in fns.items():
             for _ in range(3):
-                f()
-    torch.cuda.current_stream().wait_stream(side)
-    for n, f in fns.items():
-        g = torch.cuda.CUDAGraph()
-        with torch.no_grad(), torch.cuda.graph(g):
-            f()
-        out[n] = g.replay
+                fn()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                fn()
+            graphs[name] = graph
     torch.cuda.synchronize()
-    return out
+    return {name: graph.replay for name, graph in graphs.items()}
 
 
-def stats(samples: list[list[float]]) -> dict[str, Any]:
-    flat = sorted(x for run in samples for x in run)
-    meds = [statistics.median(r) for r in samples]
+def stats(samples) -> dict[str, Any]:
+    """Summary of an array [runs, reps] of milliseconds: the minimum (the
+    primary statistic), the overall median, each run's median and the spread
+    between run medians."""
+    arr = np.asarray(samples, dtype=float)
+    per_run = np.median(arr, axis=1)
     return {
-        "min_us": 1e3 * flat[0],
-        "median_us": 1e3 * statistics.median(flat),
-        "run_medians_us": [1e3 * m for m in meds],
-        "inter_run_spread_pct": 100.0 * (max(meds) - min(meds)) / min(meds),
-        "n": len(flat),
+        "min_us": 1e3 * float(arr.min()),
+        "median_us": 1e3 * float(np.median(arr)),
+        "run_medians_us": [1e3 * float(m) for m in per_run],
+        "inter_run_spread_pct": 100.0 * float((per_run.max() - per_run.min()) / per_run.min()),
+        "n": int(arr.size),
     }
 
 
-def paired_ratio(num: list[list[float]], den: list[list[float]]) -> float:
-    """Median of per-repetition ratios (repetitions ran in the same round)."""
-    a = [x for r in num for x in r]
-    b = [x for r in den for x in r]
-    return statistics.median(x / y for x, y in zip(a, b))
+def paired_ratio(num, den) -> float:
+    """Median of the per-repetition ratios num / den (the two ran in the same
+    rounds, so each pair saw the same machine state)."""
+    return float(np.median(np.asarray(num, dtype=float) / np.asarray(den, dtype=float)))

@@ -21,6 +21,8 @@ score row, index tensor or gathered tensor written to HBM.
 
 from __future__ import annotations
 
+import math
+
 import torch
 
 from .. import _launch, _lib
@@ -131,17 +133,18 @@ def fused_topk_attention_sort(q: torch.Tensor, k: torch.Tensor,
 
 def reference_topk_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                              topk: int) -> torch.Tensor:
-    """The composed PyTorch gather path (scores, ``topk``, softmax, gather,
-    contract), kept as the baseline it is in the reference
-    (``fused_topk_attention.py:390-402``). Not a fallback: the fused entry
-    points above never call it."""
-    B, N, d = q.shape
-    topk = max(1, min(topk, N - 1))
-    scores = torch.matmul(q, k.transpose(-1, -2)) / (d ** 0.5)
-    eye = torch.eye(N, device=q.device, dtype=torch.bool).unsqueeze(0)
-    scores = scores.masked_fill(eye, float("-inf"))
-    top_scores, top_idx = scores.topk(topk, dim=-1, sorted=False)
-    w = torch.softmax(top_scores, dim=-1)
-    idx = top_idx.reshape(B, N * topk, 1).expand(B, N * topk, d)
-    v_g = v.gather(1, idx).view(B, N, topk, d)
-    return torch.matmul(w.unsqueeze(-2), v_g).squeeze(-2)
+    """The composed PyTorch score-then-select path the reference times as its
+    baseline (``fused_topk_attention.py:390-402``): all N x N scores, the
+    self pair masked, ``topk`` (unsorted), softmax over the kept scores, and
+    the kept value rows gathered and contracted. Each query's kept rows are
+    read through flat row numbers ``b * N + j`` of ``v`` viewed as
+    ``[B * N, d]``. Not a fallback: the fused entry points above never call it."""
+    n_batch, n_agents, dim = q.shape
+    keep = max(1, min(int(topk), n_agents - 1))
+    logits = torch.bmm(q, k.transpose(1, 2).contiguous()) / math.sqrt(dim)
+    logits.diagonal(dim1=1, dim2=2).fill_(float("-inf"))
+    kept, which = torch.topk(logits, keep, dim=2, sorted=False)
+    weights = torch.softmax(kept, dim=2)
+    base = torch.arange(n_batch, device=q.device).view(n_batch, 1, 1) * n_agents
+    rows = v.reshape(n_batch * n_agents, dim)[which + base]   # [B, N, keep, d]
+    return (weights.unsqueeze(3) * rows).sum(dim=2)
