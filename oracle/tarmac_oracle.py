@@ -65,6 +65,12 @@ score_error_bound           exact-rational error of canonical scores (random,
                             gamma_d or a dropped |.| or scale fails)
 near_tie_rows               brute force on Python-sorted rows; exact gaps at
                             the eps boundary; k >= N-1 rows
+entmax_bisect               entmax15_exact (closed form) to 1e-6 at alpha=1.5;
+                            alpha -> 2 equals sparsemax's closed form; rows sum
+                            to 1, the self pair gets 0
+entmax15_exact              its own definition: weights sum to 1 and
+                            (z_j - tau)_+^2 with one tau; brute force over all
+                            supports on small rows
 canon_morton_window (C)     numpy oracle bit-exact (codes and indices)
 ==========================  ===================================================
 """
@@ -408,6 +414,48 @@ def near_tie_rows(s: np.ndarray, topk: int, eps: np.ndarray | float) -> np.ndarr
         return np.zeros(s.shape[:-1], dtype=bool)
     gap = srt[..., topk - 1] - srt[..., topk]
     return gap <= eps
+
+
+def entmax_bisect(s: np.ndarray, alpha: float, iters: int = 24) -> np.ndarray:
+    """alpha-entmax weights over the last axis by threshold bisection, the
+    reference's ``_forward_entmax`` (``src/agents/mappo.py:294-330``): z =
+    (alpha - 1) s, tau bracketed in [max z - 1, max z] and halved ``iters``
+    times on sum_j [z_j - tau]_+^(1/(alpha-1)) > 1, then the weights at the
+    midpoint, renormalised. -inf scores (the self pair) get weight 0."""
+    z = np.where(np.isneginf(s), -np.inf, s * (alpha - 1.0))
+    power = 1.0 / (alpha - 1.0)
+    hi = z.max(-1, keepdims=True)
+    lo = hi - 1.0
+    for _ in range(iters):
+        mid = 0.5 * (lo + hi)
+        above = (np.maximum(z - mid, 0.0) ** power).sum(-1, keepdims=True) > 1.0
+        lo = np.where(above, mid, lo)
+        hi = np.where(above, hi, mid)
+    p = np.maximum(z - 0.5 * (lo + hi), 0.0) ** power
+    return p / np.maximum(p.sum(-1, keepdims=True), 1e-8)
+
+
+def entmax15_exact(s: np.ndarray) -> np.ndarray:
+    """Exact 1.5-entmax over the last axis (sort-based closed form; Peters,
+    Niculae and Martins, 2019): with z = s / 2 sorted descending, the support
+    is the largest k whose threshold tau_k = mean_k - sqrt(mean_k^2 -
+    (sumsq_k - 1) / k) stays at or below z_(k); weights [z - tau]_+^2."""
+    z = np.where(np.isneginf(s), -np.inf, s / 2.0)
+    out = np.zeros_like(z, dtype=np.float64)
+    flat_z = z.reshape(-1, z.shape[-1])
+    flat_o = out.reshape(-1, z.shape[-1])
+    for r in range(flat_z.shape[0]):
+        zs = np.sort(flat_z[r][np.isfinite(flat_z[r])])[::-1]
+        tau = None
+        for k in range(1, len(zs) + 1):
+            m = zs[:k].mean()
+            disc = m * m - ((zs[:k] ** 2).sum() - 1.0) / k
+            t = m - np.sqrt(max(disc, 0.0))
+            if t <= zs[k - 1]:
+                tau = t
+        flat_o[r] = np.maximum(flat_z[r] - tau, 0.0) ** 2
+        flat_o[r][~np.isfinite(flat_z[r])] = 0.0
+    return out
 
 
 def score_error_bound(q, k) -> np.ndarray:

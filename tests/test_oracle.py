@@ -801,3 +801,87 @@ def test_error_bound_pins_reject_planted_mistakes():
 
     for mutant in (strict, off_by_one, ascending):
         assert not pin_near_tie_rows(mutant), mutant.__name__
+
+
+# ---------------------------------------------------------------------------
+# entmax (the reference's training-study arm, src/agents/mappo.py:294-330)
+# ---------------------------------------------------------------------------
+
+def _sparsemax(s):
+    """Closed-form sparsemax (alpha = 2 entmax) per row."""
+    out = np.zeros_like(s)
+    for idx in np.ndindex(s.shape[:-1]):
+        row = s[idx]
+        fin = np.isfinite(row)
+        zs = np.sort(row[fin])[::-1]
+        cs = np.cumsum(zs)
+        ks = np.arange(1, len(zs) + 1)
+        k = ks[1 + ks * zs > cs].max()
+        tau = (cs[k - 1] - 1) / k
+        out[idx] = np.where(fin, np.maximum(row - tau, 0.0), 0.0)
+    return out
+
+
+def _entmax15_brute(row):
+    """Every support of a small row: the one whose weights are consistent."""
+    fin = [j for j in range(len(row)) if np.isfinite(row[j])]
+    z = row / 2.0
+    for r in range(1, len(fin) + 1):
+        for sup in itertools.combinations(fin, r):
+            zs = z[list(sup)]
+            m = zs.mean()
+            disc = m * m - ((zs ** 2).sum() - 1.0) / r
+            if disc < 0:
+                continue
+            tau = m - np.sqrt(disc)
+            p = np.where(np.isfinite(z), np.maximum(z - tau, 0.0) ** 2, 0.0)
+            if set(np.flatnonzero(p > 0)) == set(sup) and abs(p.sum() - 1) < 1e-9:
+                return p
+    raise AssertionError("no consistent support")
+
+
+def pin_entmax(fn) -> bool:
+    rng = np.random.default_rng(11)
+    s = rng.standard_normal((3, 6, 6)) * 2.0
+    for i in range(6):
+        s[:, i, i] = -np.inf
+    p = fn(s, 1.5)
+    if not np.allclose(p.sum(-1), 1.0, atol=1e-9) or np.any(p[:, range(6), range(6)] != 0):
+        return False
+    if np.abs(p - O.entmax15_exact(s)).max() > 1e-6:
+        return False
+    return np.abs(fn(s, 2.0) - _sparsemax(s)).max() <= 1e-6
+
+
+def test_entmax15_exact_matches_brute_force():
+    rng = np.random.default_rng(5)
+    s = rng.standard_normal((4, 5)) * 3.0
+    s[0, 2] = -np.inf
+    want = np.stack([_entmax15_brute(r) for r in s])
+    assert np.abs(O.entmax15_exact(s) - want).max() <= 1e-12
+
+
+def test_entmax_bisect_pinned():
+    assert pin_entmax(O.entmax_bisect)
+
+
+def test_entmax_pin_rejects_planted_mistakes():
+    def wrong_power(s, alpha):          # squares the weights for every alpha
+        z = np.where(np.isneginf(s), -np.inf, s * (alpha - 1.0))
+        hi = z.max(-1, keepdims=True)
+        lo = hi - 1.0
+        for _ in range(24):
+            mid = 0.5 * (lo + hi)
+            above = (np.maximum(z - mid, 0.0) ** 2).sum(-1, keepdims=True) > 1.0
+            lo, hi = np.where(above, mid, lo), np.where(above, hi, mid)
+        p = np.maximum(z - 0.5 * (lo + hi), 0.0) ** 2
+        return p / p.sum(-1, keepdims=True)
+
+    def few_steps(s, alpha):            # 6 halvings instead of 24
+        return O.entmax_bisect(s, alpha, iters=6)
+
+    def softmax_instead(s, alpha):
+        return O.softmax(s)
+
+    for mutant in (wrong_power, few_steps, softmax_instead):
+        assert not pin_entmax(mutant), mutant.__name__

@@ -17,10 +17,21 @@ topk           ``tarmac_topk_fused_fwd`` (masked top-k is the same function
                as the gathered one, ``mappo.py:374-382``)
 topk_gather    ``tarmac_topk_fused_fwd``
 zorder_k       ``tarmac_zorder_fwd`` (selector + attend in one launch)
+random_k       k peers drawn uniformly without the self pair, exactly as
+               ``mappo.py:233-263`` draws them (the same ``torch.rand``
+               call), then ``tarmac_fixedset_fwd`` over that set
+entmax         alpha-entmax over all peers by the reference's 24-step
+               threshold bisection (``mappo.py:294-330``), dense torch ops
+adaptive_topk  the Gumbel-softmax k gate over dense weights
+               (``mappo.py:383-414``), dense torch ops
 =============  ==========================================================
 
-The training-study arms ``random_k``, ``entmax`` and ``adaptive_topk`` are
-not part of the timed core and are not provided here.
+``entmax`` and ``adaptive_topk`` are training-study arms outside the timed
+core; their dense (B, N, N) formulations run as torch operations on the
+device, as in the reference. Any ``msg_dim`` up to 64 works: heads whose
+width the kernels do not take (fp32: 8, 16, 32, 64; bf16: 16, 32, 64) are
+zero-padded to the next width, with q pre-scaled by sqrt(width / msg_dim) so
+that scores keep the 1/sqrt(msg_dim) scale.
 
 The reference's Triton kernels are forward-only
 (``scripts/bench_attention_core.py:172-176``) and its training differentiates
@@ -32,6 +43,7 @@ dense core.
 
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass
 
 import numpy as np
@@ -42,6 +54,7 @@ import torch.nn.functional as F
 from ..kernels.backward import (dense_attention_backward, dense_attention_forward_stats,
                                 fixedset_attention_backward)
 from ..kernels.fused_dense_attention import fused_dense_attention
+from ..kernels.fused_prescore_attention import fused_prescore_attention
 from ..kernels.fused_topk_attention import topk_attention
 from ..kernels.prescore_selection import zorder_attention
 
@@ -49,8 +62,11 @@ from ..kernels.prescore_selection import zorder_attention
 #: default, ``src/kernels/prescore_selection.py:62``).
 ZORDER_BITS = 10
 
-HIP_MODES = ("dense", "dense_sdpa", "topk", "topk_gather", "zorder_k")
-REFERENCE_ONLY_MODES = ("random_k", "entmax", "adaptive_topk")
+HIP_MODES = ("dense", "dense_sdpa", "topk", "topk_gather", "zorder_k", "random_k")
+TORCH_MODES = ("entmax", "adaptive_topk")
+
+#: Head widths the HIP kernels take, per dtype.
+_WIDTHS = {torch.float32: (8, 16, 32, 64), torch.bfloat16: (16, 32, 64)}
 
 
 @dataclass
@@ -116,6 +132,35 @@ def _tracks_grad(*ts: torch.Tensor) -> bool:
     return torch.is_grad_enabled() and any(t.requires_grad for t in ts)
 
 
+def _kernel_width(d: int, dtype: torch.dtype) -> int:
+    for w in _WIDTHS.get(dtype, ()):
+        if w >= d:
+            return w
+    raise NotImplementedError(
+        f"msg_dim={d} ({dtype}): the HIP attention core takes head widths up to 64")
+
+
+def _to_width(q, k, v):
+    """Zero-pad the heads to a width the kernels take; q is scaled so that
+    q'.k' / sqrt(width) = q.k / sqrt(d). Returns (q', k', v', d)."""
+    d = q.shape[-1]
+    w = _kernel_width(d, q.dtype)
+    if w == d:
+        return q, k, v, d
+    pad = (0, w - d)
+    return (F.pad(q * math.sqrt(w / d), pad), F.pad(k, pad), F.pad(v, pad), d)
+
+
+def _random_peers(B: int, N: int, kk: int, device) -> torch.Tensor:
+    """k peers per agent uniformly without replacement, self excluded: the
+    reference ranks uniform noise with self pushed to +inf and keeps the k
+    smallest (``mappo.py:250-255``); the same draw gives the same sets."""
+    noise = torch.rand(B, N, N, device=device)
+    eye = torch.eye(N, device=device, dtype=torch.bool).unsqueeze(0)
+    noise = noise.masked_fill(eye, float("inf"))
+    return noise.topk(kk, dim=-1, largest=False, sorted=False).indices
+
+
 def _entropy(w: torch.Tensor) -> float:
     w = w.clamp_min(1e-12)
     return float((-(w * w.log()).sum(-1)).mean().item())
@@ -161,6 +206,62 @@ class AttentionComm(nn.Module):
         s = torch.matmul(q.float().unsqueeze(-2), kg.transpose(-1, -2)).squeeze(-2) / d ** 0.5
         return torch.softmax(s, -1)
 
+    # -- the torch-composed arms (outside the timed core) ---------------------
+    def _entmax(self, q, k, v, N: int) -> tuple[torch.Tensor, dict]:
+        """alpha-entmax over all peers (``mappo.py:294-330``): threshold tau
+        found by 24 bisection steps on sum_j [(alpha-1) s_j - tau]_+^(1/(alpha-1)) = 1,
+        starting from [max - 1, max]; the self pair sits far below any threshold."""
+        alpha = self.cfg.entmax_alpha
+        z = (torch.matmul(q, k.transpose(-1, -2).contiguous()) / math.sqrt(q.shape[-1])) * (alpha - 1.0)
+        z.diagonal(dim1=-2, dim2=-1).fill_(torch.finfo(z.dtype).min / 4)
+        power = 1.0 / (alpha - 1.0)
+        hi = z.amax(dim=-1, keepdim=True)
+        lo = hi - 1.0
+        for _ in range(24):
+            mid = 0.5 * (lo + hi)
+            above = (z - mid).clamp_min(0).pow(power).sum(-1, keepdim=True) > 1.0
+            lo = torch.where(above, mid, lo)
+            hi = torch.where(above, hi, mid)
+        p = (z - 0.5 * (lo + hi)).clamp_min(0).pow(power)
+        p = p / p.sum(-1, keepdim=True).clamp_min(1e-8)
+        info: dict = {}
+        if self.collect_info:
+            info["effective_k"] = float((p > 0).sum(-1).float().mean().item())
+        return torch.matmul(p, v), info
+
+    def _adaptive_topk(self, x, q, k, v, N: int) -> tuple[torch.Tensor, dict]:
+        """Per-agent k from a hard Gumbel-softmax gate over k = 1..N-1, applied
+        to the dense weights (``mappo.py:383-414``): the weights outside each
+        row's chosen top k are zeroed and the rest renormalised; ``expected_k``
+        stays a differentiable tensor."""
+        w = self._dense_weights_like(q, k)
+        info: dict = {}
+        if self.collect_info:
+            info["mean_attn_entropy"] = _entropy(w)
+        gate = F.gumbel_softmax(self.k_gate(x), tau=1.0, hard=True)          # (B, N, K)
+        ranked, order = w.sort(dim=-1, descending=True)
+        # prefix[m, j] = 1 when rank j is within the first m + 1 ranks
+        ranks = torch.arange(N, device=x.device)
+        prefix = (ranks.view(1, N) <= torch.arange(self.k_bins, device=x.device).view(-1, 1))
+        keep_ranked = torch.matmul(gate, prefix.to(w.dtype))                  # (B, N, N)
+        keep = torch.zeros_like(w).scatter_(-1, order, keep_ranked)
+        attn = w * keep
+        attn = attn / attn.sum(-1, keepdim=True).clamp_min(1e-8)
+        ks = torch.arange(1, self.k_bins + 1, device=x.device, dtype=gate.dtype)
+        info["expected_k"] = (gate * ks).sum(-1).mean()
+        if self.collect_info:
+            info["mean_k"] = float(info["expected_k"].item())
+        return torch.matmul(attn, v), info
+
+    @staticmethod
+    def _dense_weights_like(q, k) -> torch.Tensor:
+        """softmax(q k^T / sqrt(d)) with the self pair masked, in q's dtype."""
+        N = q.shape[1]
+        s = torch.matmul(q, k.transpose(-1, -2).contiguous()) / math.sqrt(q.shape[-1])
+        s = s.masked_fill(torch.eye(N, device=q.device, dtype=torch.bool).unsqueeze(0),
+                          float("-inf"))
+        return torch.softmax(s, -1)
+
     # -- forward -------------------------------------------------------------
     def forward(self, x: torch.Tensor,
                 pos: torch.Tensor | None = None) -> tuple[torch.Tensor, dict]:
@@ -168,53 +269,74 @@ class AttentionComm(nn.Module):
         mode = self.cfg.attn_mode
         qkv = self.qkv(x)
         q, k, v = (t.contiguous() for t in qkv.chunk(3, dim=-1))
-        info: dict = {}
 
+        if mode == "entmax":
+            msg, info = self._entmax(q, k, v, N)
+            return self.proj(F.gelu(msg)), info
+        if mode == "adaptive_topk":
+            msg, info = self._adaptive_topk(x, q, k, v, N)
+            return self.proj(F.gelu(msg)), info
+        if mode not in HIP_MODES:
+            raise ValueError(f"unknown attn_mode {mode!r}")
+        if mode == "zorder_k" and pos is None:
+            raise ValueError("attn_mode='zorder_k' needs agent positions")
+        qw, kw, vw, d = _to_width(q, k, v)
+        msg, info = self._core(mode, q, k, qw, kw, vw, pos, B, N)
+        return self.proj(F.gelu(msg[..., :d])), info
+
+    def _core(self, mode, q, k, qw, kw, vw, pos, B: int, N: int) -> tuple[torch.Tensor, dict]:
+        """The HIP core on kernel-width heads (qw, kw, vw); q, k are the
+        unpadded heads for the diagnostics."""
+        info: dict = {}
+        grad = _tracks_grad(qw, kw, vw)
         if mode == "zorder_k":
-            if pos is None:
-                raise ValueError("attn_mode='zorder_k' needs agent positions")
             kk = self._k_eff(N)
-            if _tracks_grad(q, k, v):
+            if grad:
                 msg, idx = _SetCore.apply(
                     lambda a, b, c, p: zorder_attention(a, b, c, p, kk, ZORDER_BITS,
                                                         return_indices=True),
-                    q, k, v, pos)
+                    qw, kw, vw, pos)
             else:
-                res = zorder_attention(q, k, v, pos, kk, ZORDER_BITS,
+                res = zorder_attention(qw, kw, vw, pos, kk, ZORDER_BITS,
                                        return_indices=self.collect_info)
                 msg, idx = res if self.collect_info else (res, None)
             info["effective_k"] = float(kk)
             if self.collect_info:
                 info["mean_attn_entropy"] = _entropy(self._set_weights(q, k, idx))
-            return self.proj(F.gelu(msg)), info
+            return msg, info
+
+        if mode == "random_k":
+            kk = self._k_eff(N)
+            peers = _random_peers(B, N, kk, qw.device)
+            if grad:
+                msg, _ = _SetCore.apply(
+                    lambda a, b, c, ix: (fused_prescore_attention(a, b, c, ix), ix),
+                    qw, kw, vw, peers)
+            else:
+                msg = fused_prescore_attention(qw, kw, vw, peers)
+            info["effective_k"] = float(kk)
+            return msg, info
 
         if mode in ("dense", "dense_sdpa"):
-            msg = (_DenseCore.apply(q, k, v) if _tracks_grad(q, k, v)
-                   else fused_dense_attention(q, k, v))
+            msg = _DenseCore.apply(qw, kw, vw) if grad else fused_dense_attention(qw, kw, vw)
             if mode == "dense" and self.collect_info:
                 info["mean_attn_entropy"] = _entropy(self._dense_weights(q, k))
-            return self.proj(F.gelu(msg)), info
+            return msg, info
 
-        if mode in ("topk", "topk_gather"):
-            kk = self._k_eff(N)
-            if _tracks_grad(q, k, v):
-                msg, idx = _SetCore.apply(
-                    lambda a, b, c: topk_attention(a, b, c, kk, return_indices=True), q, k, v)
-            else:
-                want_idx = self.collect_info and mode == "topk_gather"
-                res = topk_attention(q, k, v, kk, return_indices=want_idx)
-                msg, idx = res if want_idx else (res, None)
-            if mode == "topk":
-                if self.collect_info:
-                    info["mean_attn_entropy"] = _entropy(self._dense_weights(q, k))
+        kk = self._k_eff(N)  # topk, topk_gather
+        if grad:
+            msg, idx = _SetCore.apply(
+                lambda a, b, c: topk_attention(a, b, c, kk, return_indices=True), qw, kw, vw)
+        else:
+            want_idx = self.collect_info and mode == "topk_gather"
+            res = topk_attention(qw, kw, vw, kk, return_indices=want_idx)
+            msg, idx = res if want_idx else (res, None)
+        if mode == "topk":
+            if self.collect_info:
+                info["mean_attn_entropy"] = _entropy(self._dense_weights(q, k))
+            info["effective_k"] = float(kk)
+        else:
+            if self.collect_info:
                 info["effective_k"] = float(kk)
-            else:
-                if self.collect_info:
-                    info["effective_k"] = float(kk)
-                    info["mean_attn_entropy"] = _entropy(self._set_weights(q, k, idx))
-            return self.proj(F.gelu(msg)), info
-
-        if mode in REFERENCE_ONLY_MODES:
-            raise NotImplementedError(
-                f"attn_mode={mode!r} is a training-study arm outside the HIP attention core")
-        raise ValueError(f"unknown attn_mode {mode!r}")
+                info["mean_attn_entropy"] = _entropy(self._set_weights(q, k, idx))
+        return msg, info
