@@ -12,14 +12,21 @@ aggregation). ``value`` is its device time per call in microseconds.
 Alongside, with the reference's protocol (interleaved event timing and graph
 replay, minimum over samples): the dense core, top-k at k=1/2/4, the fixed-set
 kernel given the exact top-k set (selection-time share), the streaming kernel
-at B=256 N=512 and 1024, fp32 and bf16, the reference's masked-bisection and sort
-selection variants at the metric point, the Z-order select+attend at B=1024 N=512 k=2
-(configs[4]), the configs[0] MPE n6 shape with the CPU oracle beside it, the
-configs[2] bf16 grid (B = 32 to 4096, k = 1, 2, 4), the configs[1] sweep
-over N, the pre-score selectors (radius / grid kNN, Morton window) and the
-launch floor. Streaming and Z-order are single launches here: their headline
-figures are eager event timings, with the graph replays alongside
-(``graph_us``), which add a fixed cost per replay on this software stack.
+at B=256 N=512 and 1024, fp32 and bf16, the reference's
+masked-bisection and sort selection variants at the metric point, the Z-order
+select+attend at B=1024 N=512 k=2, the configs[0] MPE n6 shape,
+the configs[2] bf16 grid (B = 32 to 4096, k = 1, 2, 4), the configs[1] sweep
+over N, the pre-score selectors (radius / grid kNN, Morton window), the
+module forward and forward+backward, and the backward kernels. Launches per
+call are counted as the nodes of each call's captured graph; the fixed cost of
+a timed call is broken down (event pair, launch, back-to-back gap, graph
+replay); the device's sustained copy bandwidth and library GEMM rates are
+probed beside the datasheet peaks.
+
+``cpu_baseline``: the reference's CPU path (a torch-CPU restatement of its
+compositions) timed on this host with all cores of the affinity mask and the
+reference's CPU protocol, at the full metric shape, with configs[0] and
+configs[4] beside it (--no-cpu skips it).
 
 Prints ONE JSON line. Exits non-zero (with a message) for --gpus > 1: this
 build measures one GPU.
@@ -65,37 +72,56 @@ def _traffic_from_profiles(kernel_tag: str):
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(seconds_budget: float = 15.0) -> dict:
-    """The numpy oracle's top-k gather path (k=2) on a bounded sample of the
-    workload, single thread, scaled to the full batch."""
+def cpu_baseline() -> dict:
+    """The reference's CPU path, timed on this host's own cores beside the GPU
+    numbers: the torch-CPU restatement of its compositions (oracle/
+    cpu_reference.py) at full config sizes, with the reference's CPU protocol
+    (perf_counter around one call, warm-up 10, reps 30, runs 5; minimum,
+    per-run medians, spread) and torch using every core of the affinity mask.
+    The value is configs[1]'s metric point (topk_gather, k=2, B=1024, N=256,
+    d=16, fp32); dense at the same point, configs[0] (B=256, N=6, k=2) and
+    configs[4] (Z-order, B=1024, N=512, k=2, 16 bits) beside it. Inputs come
+    from the same seeded CPU generator as the GPU run."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import numpy as np
-    import tarmac_oracle as O
+    import torch
+    import cpu_reference as C
+    cores = len(os.sched_getaffinity(0))
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(cores)
     try:
-        from threadpoolctl import threadpool_limits
-    except Exception:  # pragma: no cover
-        threadpool_limits = None
-    bs = 64
-    rng = np.random.default_rng(1234 + 7 * N + D)
-    q, k, v = (rng.standard_normal((bs, N, D)).astype(np.float32) for _ in range(3))
-    ctx = threadpool_limits(1) if threadpool_limits else None
-    times = []
-    try:
-        if ctx:
-            ctx.__enter__()
-        O.topk_gather(q, k, v, VALUE_K)  # warm-up
-        t_end = time.perf_counter() + seconds_budget
-        while time.perf_counter() < t_end and len(times) < 30:
-            t0 = time.perf_counter()
-            O.topk_gather(q, k, v, VALUE_K)
-            times.append(time.perf_counter() - t0)
+        def tensors(seed, b, n, d):
+            g = np.random.default_rng(seed)
+            return [torch.from_numpy(g.standard_normal((b, n, d)).astype(np.float32)) for _ in range(3)]
+
+        q, k, v = tensors(1234 + 7 * N + D, B, N, D)
+        value = C.time_protocol(lambda: C.topk_gather(q, k, v, VALUE_K))
+        # dense beside it on a shorter protocol (its calls cost as much as the
+        # value's and add nothing to the metric)
+        dense = C.time_protocol(lambda: C.dense_unfused(q, k, v), warmup=3, reps=10, runs=3)
+        q0, k0, v0 = tensors(1234 + 7 * 6 + D, 256, 6, D)
+        c1 = C.time_protocol(lambda: C.topk_gather(q0, k0, v0, 2))
+        g5 = np.random.default_rng(4242 + 512)
+        q5, k5, v5 = (torch.from_numpy(g5.standard_normal((1024, 512, D)).astype(np.float32))
+                      for _ in range(3))
+        pos5 = torch.from_numpy(g5.random((1024, 512, 2)).astype(np.float32))
+        c5 = C.time_protocol(lambda: C.zorder(q5, k5, v5, pos5, 2, 16))
+        host = C.host_report()
     finally:
-        if ctx:
-            ctx.__exit__(None, None, None)
-    per_call_us = min(times) * (B / bs) * 1e6
-    return {"value": per_call_us, "unit": "µs/call", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle topk_gather (fp32, k={VALUE_K}) on {bs} of {B} batch rows "
-                      f"(N={N}, d={D}), min of {len(times)} calls, x{B // bs} to the full batch"}
+        torch.set_num_threads(prev_threads)
+    r = lambda t: {kk: (round(vv, 3) if isinstance(vv, float) else
+                        ([round(x, 3) for x in vv] if isinstance(vv, list) else vv))
+                   for kk, vv in t.items()}
+    return {"value": round(value["min_us"], 3), "unit": "µs/call", "cores": cores,
+            "kind": "port",
+            "sample": (f"torch-CPU restatement of the reference's topk_gather (k={VALUE_K}) on the "
+                       f"full configs[1] batch (B={B}, N={N}, d={D}, fp32), {cores} threads; "
+                       "warm-up 10, 5 runs x 30 reps, minimum"),
+            "protocol": r(value),
+            "dense_unfused_B1024_N256_d16": r(dense),
+            "configs0_topk_gather_B256_N6_d16_k2": r(c1),
+            "configs4_zorder_B1024_N512_d16_k2": r(c5),
+            "host": host}
 
 
 def profile_one(args, q, k, v, dev) -> int:
@@ -119,6 +145,12 @@ def profile_one(args, q, k, v, dev) -> int:
         # configs[2] point where bf16 dense is HBM-bound: B=4096, N=64, d=64
         g = np.random.default_rng(77 + 64 + 64)
         qb, kb, vb = (torch.from_numpy(g.standard_normal((4096, 64, 64)).astype(np.float32))
+                      .to(dev).to(torch.bfloat16) for _ in range(3))
+        fn = bound.dense(qb, kb, vb)
+    elif name == "dense_bf16_d16":
+        # configs[2] bf16 dense at d=16: B=4096, N=256
+        g = np.random.default_rng(77 + 256 + 16)
+        qb, kb, vb = (torch.from_numpy(g.standard_normal((4096, 256, 16)).astype(np.float32))
                       .to(dev).to(torch.bfloat16) for _ in range(3))
         fn = bound.dense(qb, kb, vb)
     elif name == "stream2":
@@ -148,21 +180,24 @@ def profile_one(args, q, k, v, dev) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    # the device needs some tens of milliseconds of sustained load to reach its
+    # working clock (a cold start reads ~20% slow): 3000 untimed calls (~0.1 s)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=3000)
     ap.add_argument("--reps", type=int, default=40, help="interleaved repetitions per run")
     ap.add_argument("--runs", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--value-only", action="store_true",
                     help="time only the value kernel (for profiler runs)")
     ap.add_argument("--profile-kernel", default=None,
-                    choices=["dense", "dense_bf16", "topk1", "topk2", "topk4", "fixedset2", "zorder",
+                    choices=["dense", "dense_bf16", "dense_bf16_d16", "topk1", "topk2", "topk4", "fixedset2", "zorder",
                              "stream2"],
                     help="run only this kernel (headline shape; zorder/stream at their configs) "
                          "--warmup + --steps times, for profiler counter passes")
     ap.add_argument("--topk-filter", type=int, default=None, choices=[0, 1, 2, 3, 4],
                     help="top-k implementation for --profile-kernel runs (tarmac_set_topk_filter: "
-                         "0 plain, 1 automatic, 2 filter-and-verify)")
+                         "0 packed, 1 automatic, 2 filter-and-verify, 3 register lists, "
+                         "4 packed on split-bf16 scores)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 64 MiB device copy (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -296,6 +331,15 @@ def main() -> int:
         "graph": {n: {kk: round(vv, 3) for kk, vv in s.items() if kk in ("min_us", "median_us")}
                   for n, s in gst.items()},
     }
+    # launches per call, counted as the nodes of the captured graph
+    detail["graph_nodes_per_call"] = {n: harness.graph_node_counts(f) for n, f in gfns.items()}
+    # where a timed call's fixed cost goes (event pair, launch, graph replay)
+    from tarmac import _launch, _lib
+    flag = torch.zeros(1, device=dev)
+    detail["launch_overheads_us"] = harness.launch_overheads(
+        fns["noop"], fns[f"topk_k{VALUE_K}"],
+        lambda: _lib.LIB.tarmac_noop(_launch.ptr(flag), _launch.stream(flag)),
+        gfns[f"topk_k{VALUE_K}"], reps=max(20, args.reps))
     del fns, gfns
 
     # ---- the reference's fused implementations (scripts/bench_attention_core.py:160-170)
@@ -353,6 +397,7 @@ def main() -> int:
                 s4g = {n: harness.stats(s) for n, s in
                        harness.time_interleaved(harness.as_graphs(f4), args.reps, 5, 2).items()}
                 detail[key]["graph_us"] = {n: round(s["min_us"], 3) for n, s in s4g.items()}
+                detail[key]["graph_nodes_per_call"] = harness.graph_node_counts(f4["stream_k2"])
             del q4, k4, v4, f4
         del base4
 
@@ -374,7 +419,8 @@ def main() -> int:
         "ratio_vs_dense": round(tz / s5["dense"]["min_us"], 4),
         "hbm_frac": round(harness.analytic_bytes("zorder", b5, n5, D, k5)
                           / (tz * 1e-6) / harness.PEAK_HBM_BYTES_PER_S, 4),
-        "graph_us": {n: round(s["min_us"], 3) for n, s in s5g.items()}}
+        "graph_us": {n: round(s["min_us"], 3) for n, s in s5g.items()},
+        "graph_nodes_per_call": harness.graph_node_counts(f5["zorder_total"])}
     del q5, k5t, v5, pos5, f5
 
     # ---- pre-score selectors (scripts/bench_prescore.py: B=256, d=16) -------
@@ -398,8 +444,7 @@ def main() -> int:
     detail["prescore_selectors_B256_d16_us"] = sel_rows
 
     # ---- the MPE n6 shape (fp32, B=256, N=6, d=16, k=2), which
-    # the reference runs on its CPU path; the numpy oracle is timed beside it
-    # (one thread, the whole batch) unless --no-cpu
+    # the reference runs on its CPU path (timed in cpu_baseline, all cores)
     g0 = np.random.default_rng(1234 + 7 * 6 + D)
     base0 = [g0.standard_normal((256, 6, D)).astype(np.float32) for _ in range(3)]
     q0, k0, v0 = (torch.from_numpy(x).to(dev) for x in base0)
@@ -408,17 +453,7 @@ def main() -> int:
           harness.time_interleaved(f0, args.reps, 5, 2).items()}
     row0 = {f"{n}_us": round(t, 3) for n, t in s0.items()}
     if not args.no_cpu:
-        sys.path.insert(0, str(ROOT / "oracle"))
-        import tarmac_oracle as O
-        from threadpoolctl import threadpool_limits
-        with threadpool_limits(1):
-            O.topk_gather(*base0, 2)
-            t_cpu = []
-            for _ in range(30):
-                t1 = time.perf_counter()
-                O.topk_gather(*base0, 2)
-                t_cpu.append(time.perf_counter() - t1)
-        row0["cpu_oracle_topk_k2_us"] = round(min(t_cpu) * 1e6, 3)
+        row0["cpu_reference_topk_k2_us"] = "see cpu_baseline.configs0_topk_gather_B256_N6_d16_k2"
     detail["configs0_B256_N6_d16_k2"] = row0
     del q0, k0, v0, f0, base0
 
@@ -550,7 +585,8 @@ def main() -> int:
               harness.time_interleaved(harness.as_graphs(fg), args.reps, 5, 2).items()}
         small[f"N{n}"] = {"eager_us": {k_: round(v_, 3) for k_, v_ in se.items()},
                           "graph_us": {k_: round(v_, 3) for k_, v_ in sg.items()},
-                          "launches_per_call": 1}
+                          "graph_nodes_per_call": {k_: harness.graph_node_counts(f)
+                                                   for k_, f in fg.items()}}
     detail["small_n_B1024_d16"] = small
 
     # ---- configs[1] sweep: B=1024, d=16, N in {32..512}, k in {1,2,4} ------
@@ -576,6 +612,7 @@ def main() -> int:
     detail["sweep_B1024_d16_us"] = sweep
 
     line["detail"] = detail
+    line["device_probes"] = harness.device_probes(dev)
     line["device"] = torch.cuda.get_device_name(dev)
     line["host"] = {"cpu": platform.processor() or platform.machine(),
                     "affinity_cores": len(os.sched_getaffinity(0))}

@@ -131,3 +131,135 @@ def paired_ratio(num, den) -> float:
     """Median of the per-repetition ratios num / den (the two ran in the same
     rounds, so each pair saw the same machine state)."""
     return float(np.median(np.asarray(num, dtype=float) / np.asarray(den, dtype=float)))
+
+
+# hipGraphNodeType values (hip_runtime_api.h)
+_NODE_TYPES = {0: "kernel", 1: "memcpy", 2: "memset", 3: "host", 4: "graph", 5: "empty",
+               6: "wait_event", 7: "event_record"}
+
+
+def _hip_runtime():
+    """The HIP runtime this process already runs on (loaded by torch; the
+    soname resolves to that same instance)."""
+    import ctypes
+    lib = ctypes.CDLL("libamdhip64.so.7")
+    lib.hipGraphGetNodes.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_size_t)]
+    lib.hipGraphNodeGetType.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]
+    return lib
+
+
+def graph_node_counts(fn: Callable[[], Any]) -> dict[str, int]:
+    """Capture one call of ``fn`` and count the captured graph's nodes by
+    type: the number of kernel launches (and copies, fills) the call makes."""
+    import ctypes
+    with torch.no_grad():
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph(keep_graph=True)
+        with torch.cuda.graph(graph):
+            fn()
+    handle = ctypes.c_void_p(graph.raw_cuda_graph())
+    hip = _hip_runtime()
+    count = ctypes.c_size_t(0)
+    if hip.hipGraphGetNodes(handle, None, ctypes.byref(count)) != 0:
+        raise RuntimeError("hipGraphGetNodes failed")
+    nodes = (ctypes.c_void_p * max(1, count.value))()
+    if hip.hipGraphGetNodes(handle, nodes, ctypes.byref(count)) != 0:
+        raise RuntimeError("hipGraphGetNodes failed")
+    out: dict[str, int] = {}
+    for i in range(count.value):
+        kind = ctypes.c_int(-1)
+        if hip.hipGraphNodeGetType(ctypes.c_void_p(nodes[i]), ctypes.byref(kind)) != 0:
+            raise RuntimeError("hipGraphNodeGetType failed")
+        name = _NODE_TYPES.get(kind.value, f"type{kind.value}")
+        out[name] = out.get(name, 0) + 1
+    del graph
+    return out
+
+
+def _pair_us(fn: Callable[[], Any], reps: int) -> float:
+    """Minimum over ``reps`` of one event pair around one call of ``fn``."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    return 1e3 * min(_elapsed_ms(fn, start, end) for _ in range(reps))
+
+
+def launch_overheads(noop: Callable[[], Any], kernel: Callable[[], Any],
+                     noop_capturable: Callable[[], Any], kernel_capturable: Callable[[], Any],
+                     reps: int = 50, batch: int = 100) -> dict[str, float]:
+    """Where the fixed cost of one timed call goes, in microseconds (minima).
+
+    * ``event_pair_empty``: two events recorded back to back, nothing between;
+    * ``noop_single``: one 1-wave kernel between the events;
+    * ``noop_back_to_back``: per-launch time of ``batch`` noops under one pair
+      (the launch-to-launch gap of a stream kept busy);
+    * ``noop_graph_single``: one replay of a graph holding one noop;
+      ``noop_graph_back_to_back``: per replay, ``batch`` replays under one
+      pair; ``noop_graph_batched``: per node, one replay of a graph holding
+      ``batch`` noops;
+    * ``kernel_*``: the same for ``kernel``.
+
+    ``noop`` and ``kernel`` may be pre-bound to a stream; the ``_capturable``
+    forms must launch on the current stream (they are captured)."""
+    def back_to_back(fn):
+        def many():
+            for _ in range(batch):
+                fn()
+        return _pair_us(many, max(5, reps // 10)) / batch
+
+    def graph_of(fn, count):
+        with torch.no_grad():
+            for _ in range(2):
+                fn()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(count):
+                    fn()
+        torch.cuda.synchronize()
+        return g
+
+    res = {}
+    with torch.no_grad():
+        for _ in range(10):
+            noop()
+            kernel()
+        torch.cuda.synchronize()
+        res["event_pair_empty"] = _pair_us(lambda: None, reps)
+        for name, eager, capturable in (("noop", noop, noop_capturable),
+                                        ("kernel", kernel, kernel_capturable)):
+            res[f"{name}_single"] = _pair_us(eager, reps)
+            res[f"{name}_back_to_back"] = back_to_back(eager)
+            g1 = graph_of(capturable, 1)
+            res[f"{name}_graph_single"] = _pair_us(g1.replay, reps)
+            res[f"{name}_graph_back_to_back"] = back_to_back(g1.replay)
+            gb = graph_of(capturable, batch)
+            res[f"{name}_graph_batched"] = _pair_us(gb.replay, max(5, reps // 10)) / batch
+            del g1, gb
+    torch.cuda.synchronize()
+    return {k: round(v, 3) for k, v in res.items()}
+
+
+def device_probes(device, reps: int = 20) -> dict[str, float]:
+    """What this device sustains on plain library work, beside the datasheet
+    peaks: a 1 GiB device-to-device copy (read + write bytes per second) and
+    square 8192^3 GEMMs (torch.mm on hipBLASLt) in fp32 and bf16."""
+    res = {}
+    src = torch.ones(256 << 20, device=device)          # 1 GiB of fp32
+    dst = torch.empty_like(src)
+    t = _pair_us(lambda: dst.copy_(src), reps) * 1e-6
+    res["copy_1GiB_GBps"] = round(2 * src.numel() * 4 / t / 1e9, 1)
+    del src, dst
+    n = 8192
+    for name, dt in (("gemm_fp32_TFLOPs", torch.float32), ("gemm_bf16_TFLOPs", torch.bfloat16)):
+        a = torch.randn(n, n, device=device).to(dt)
+        b = torch.randn(n, n, device=device).to(dt)
+        c = torch.empty(n, n, device=device, dtype=dt)
+        for _ in range(3):
+            torch.mm(a, b, out=c)
+        t = _pair_us(lambda: torch.mm(a, b, out=c), max(5, reps // 2)) * 1e-6
+        res[name] = round(2 * n ** 3 / t / 1e12, 1)
+        del a, b, c
+    torch.cuda.synchronize()
+    return res
