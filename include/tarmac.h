@@ -192,6 +192,20 @@ int tarmac_dense_bwd(const float* q, const float* k, const float* v, const float
                      int stats_ready, int B, int N, int d, void* stream);
 
 /*
+ * tarmac_dense_bwd (stats_ready = 0) that allocates nothing: its [B, 2, N]
+ * statistics live in a library-held device array of 8 MiB per GPU (so
+ * B * N <= 1048576; larger calls return TARMAC_ERR_UNSUPPORTED), resident
+ * until the process ends. Calls no hipMalloc or allocating routine. Every
+ * call on one GPU shares that array: calls that overlap on one GPU (two
+ * streams, two threads) race and must be serialised by the caller. No
+ * counterpart in the reference; for callers that cannot allocate device
+ * memory (code under graph capture, serving loops that forbid hipMalloc).
+ */
+int tarmac_dense_bwd_noalloc(const float* q, const float* k, const float* v, const float* out,
+                             const float* dout, float* dq, float* dk, float* dv, int B, int N,
+                             int d, void* stream);
+
+/*
  * Which of three equally exact implementations serves topk <= 8 (the result
  * is identical whichever runs; only the time differs):
  *   packed   -- scores with the key's position in their low mantissa bits,

@@ -325,6 +325,31 @@ int tarmac_dense_bwd(const float* q, const float* k, const float* v, const float
   return hip_status(tarmac::run_dense_bwd(a), fn);
 }
 
+int tarmac_dense_bwd_noalloc(const float* q, const float* k, const float* v, const float* out,
+                             const float* dout, float* dq, float* dk, float* dv, int B, int N,
+                             int d, void* stream) {
+  const char* fn = "tarmac_dense_bwd_noalloc";
+  int rc = check_core(q, k, v, out, B, N, d, TARMAC_DTYPE_F32, fn);
+  if (rc) return rc;
+  if (!dout || !dq || !dk || !dv) return fail(TARMAC_ERR_INVALID, "%s: null pointer", fn);
+  if (!aligned(dout, 16) || !aligned(dq, 16) || !aligned(dk, 16) || !aligned(dv, 16))
+    return fail(TARMAC_ERR_INVALID, "%s: misaligned buffer", fn);
+  const size_t need = size_t(2) * size_t(B) * size_t(N) * sizeof(float);
+  if (need > tarmac::kScratchBytes)
+    return fail(TARMAC_ERR_UNSUPPORTED,
+                "%s: the [B, 2, N] statistics need %zu bytes, more than the library's %zu-byte "
+                "scratch (B * N <= %zu); use tarmac_dense_bwd with a caller workspace",
+                fn, need, tarmac::kScratchBytes, tarmac::kScratchBytes / (2 * sizeof(float)));
+  void* ws = nullptr;
+  hipError_t e = tarmac::scratch_address(&ws);
+  if (e != hipSuccess) return hip_status(e, fn);
+  // every statistic is written by the first pass before the second reads it:
+  // nothing in the scratch needs clearing
+  tarmac::DenseBwdArgs a{q, k, v, out, dout, dq, dk, dv, static_cast<float*>(ws), 0, B, N, d,
+                         inv_sqrt(d), stream};
+  return hip_status(tarmac::run_dense_bwd(a), fn);
+}
+
 int tarmac_set_topk_filter(int mode) {
   if (mode < tarmac::kFilterOff || mode > tarmac::kFilterPackedSplit) {
     fail(TARMAC_ERR_INVALID, "tarmac_set_topk_filter: mode must be 0 to 4 (got %d)", mode);

@@ -139,6 +139,10 @@ hipError_t run_zorder(const ZorderArgs& a);
 hipError_t run_noop(float* out, void* stream);
 hipError_t run_fixedset_bwd(const FixedsetBwdArgs& a);
 hipError_t run_dense_bwd(const DenseBwdArgs& a);
+// Library-held device workspace (one per GPU, kScratchBytes): the current
+// device's address of it, looked up on the first call on that device.
+constexpr size_t kScratchBytes = size_t(8) << 20;
+hipError_t scratch_address(void** out);
 hipError_t run_knn(const KnnArgs& a);
 void grid_knn_shape(int N, int k, int* G, int* M);
 int knn_grid_threads(int N);

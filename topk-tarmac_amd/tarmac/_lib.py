@@ -43,6 +43,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tarmac_fixedset_bwd": ([_P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I, _P], _I),
     "tarmac_dense_fwd_stats": ([_P, _P, _P, _P, _P, _I, _I, _I, _P], _I),
     "tarmac_dense_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P], _I),
+    "tarmac_dense_bwd_noalloc": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P], _I),
     "tarmac_knn_radius": ([_P, _P, _I, _I, _I, _I, _P], _I),
     "tarmac_knn_grid": ([_P, _P, _I, _I, _I, _I, _P], _I),
     "tarmac_grid_knn_shape": ([_I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)], _I),
