@@ -159,9 +159,12 @@ int tarmac_zorder_fwd(const void* q, const void* k, const void* v, const float* 
  * gradients of the top-k core with the set its forward retained (gradients
  * flow only through the retained scores and value rows, as for torch.topk's
  * gather), of the Z-order core with its selector's set, and of prescore
- * attention. dq, dk and dv are written (dk, dv are summed over the queries
- * that retain each key with fp32 atomics, so their low bits depend on the
- * order the adds land in). No kernel counterpart in the reference (its Triton kernels are
+ * attention. dq, dk and dv are written. Each key's dk, dv are summed over
+ * the queries that retain it in ascending query order, so they are bitwise
+ * reproducible, except in a batch row whose sets name a peer twice, or when N is too large for the
+ * row's N x N bitmask in LDS (N above about 1100 at d = 16): there they are
+ * summed with fp32 atomics, whose low bits depend on the order the adds land
+ * in. No kernel counterpart in the reference (its Triton kernels are
  * forward-only, scripts/bench_attention_core.py:172-176); replaces autograd
  * through src/agents/mappo.py:192-231 in src/training/train_mappo.py:366.
  */

@@ -16,9 +16,12 @@
 //   s_j = c q_i.k_j, w = softmax(s over S_i), dw_j = dO_i.v_j,
 //   D_i = sum_j w_j dw_j, ds_j = w_j (dw_j - D_i),
 //   dq_i = c sum_j ds_j k_j,  dk_j += c ds_j q_i,  dv_j += w_j dO_i.
-// dk and dv collect contributions from every query that retained j, with
-// fp32 atomic adds (accumulation order is not fixed): in LDS, one workgroup
-// per batch row, when the row's dK and dV fit 64 KiB; else in global memory.
+// dk and dv collect contributions from every query that retained j. The
+// mask kernel (one workgroup per batch row, while the row's N x N bitmask
+// fits LDS) sums them per key in ascending query order, with no float
+// atomics; beyond that, or for sets that repeat a peer, they are summed with
+// fp32 atomic adds in no fixed order: per-entry lists in LDS (gather form),
+// accumulators in LDS, or global memory, whichever fits.
 //
 // Dense, self pair excluded: P = softmax(c Q K^T), D_i = dO_i.O_i,
 //   dS = P o (dO V^T - D 1^T),  dQ = c dS K,  dK = c dS^T Q,  dV = P^T dO.
@@ -55,15 +58,21 @@ __device__ __forceinline__ void atomic_add_row(float* dst, const float (&x)[E], 
 // fixed peer set
 // ---------------------------------------------------------------------------
 
-// One query (a quad of lanes): dq is written; the dk / dv rows of its peers
-// receive atomic adds (global memory or LDS). Peers are taken U at a time
-// with their index, K and V loads in flight together; when the set fits one
-// batch (kk <= U) the second pass reuses the rows from registers. Kb / Vb are
-// the batch row's keys and values, in LDS or global memory. For each valid
-// peer, sink(j, p, q, g, ds, w) receives the query's contribution to dk_p
-// (scale * ds * q) and dv_p (w * g); every lane of the quad calls it.
+// A query's softmax statistics over its set: the max m of its exp2-domain
+// scores, 1 / sum 2^(s - m), and D = sum_j w_j dw_j.
+struct RowStats {
+  float m, inv_l, dsum;
+};
+
+// One query (a quad of lanes): dq is written and the statistics returned.
+// Peers are taken U at a time with their index, K and V loads in flight
+// together; when the set fits one batch (kk <= U) the second pass reuses the
+// rows from registers. Kb / Vb are the batch row's keys and values, in LDS or
+// global memory. For each valid peer, sink(j, p, q, g, ds, w) receives the
+// query's contribution to dk_p (scale * ds * q) and dv_p (w * g); every lane
+// of the quad calls it.
 template <int D, typename I, typename Sink>
-__device__ __forceinline__ void fixedset_bwd_row(const float* __restrict__ qrow,
+__device__ __forceinline__ RowStats fixedset_bwd_row(const float* __restrict__ qrow,
                                                  const float* __restrict__ grow,
                                                  const float* Kb, const float* Vb,
                                                  const I* __restrict__ ir, float* __restrict__ dqrow,
@@ -136,6 +145,7 @@ __device__ __forceinline__ void fixedset_bwd_row(const float* __restrict__ qrow,
 #pragma unroll
   for (int c = 0; c < E; ++c) dq[c] = bad ? __int_as_float(0x7fc00000) : dq[c] * scale;
   st_f32<E>(dqrow + sub * E, dq);
+  return RowStats{m, inv_l, Dq};
 }
 
 // The scatter of a peer's contribution with fp32 atomic adds (global memory
@@ -354,6 +364,151 @@ fixedset_bwd_gather_kernel(const float* __restrict__ Q, const float* __restrict_
     for (int c = 0; c < E; ++c) dk[c] *= scale;
     st_f32<E>(dK + boff + static_cast<size_t>(j) * D + sub * E, dk);
     st_f32<E>(dV + boff + static_cast<size_t>(j) * D + sub * E, dv);
+  }
+}
+
+// Mask form (no float atomics, sums in ascending query order), one workgroup
+// per batch row:
+//   1. each query (a quad) writes dq, keeps its statistics in LDS and sets
+//      bit i of row p of an N x N bitmask for every peer p (integer LDS
+//      atomics; an OR lands the same whatever the order);
+//   2. each key p (a quad) walks the set bits of its row in ascending query
+//      order and, for every query i that retains it, recomputes s, w, dw and
+//      ds from the saved statistics (the same operations on the same lanes
+//      as step 1) and sums dk = scale * sum ds q_i, dv = sum w g_i, written
+//      once. LDS holds N statistics and N^2 bits, plus (STAGE) the row's K
+//      and V, then Q and dO.
+// A set that names one peer twice does not fit a bitmask: a batch row where
+// step 1 finds a repeated peer is summed with global fp32 atomics instead
+// (its dK, dV rows zeroed first), in no fixed order.
+struct MaskSink {
+  unsigned* mask;
+  int* repeated;
+  int words;  // per mask row
+  int i;
+  int sub;
+  template <int E>
+  __device__ __forceinline__ void operator()(int, int p, const float (&)[E], const float (&)[E],
+                                             float, float) const {
+    if (sub == 0) {
+      const unsigned bit = 1u << (i & 31);
+      if (atomicOr(mask + static_cast<size_t>(p) * words + (i >> 5), bit) & bit) *repeated = 1;
+    }
+  }
+};
+
+size_t fixedset_mask_lds_bytes(int N, int D, bool stage) {
+  const size_t words = (static_cast<size_t>(N) + 31) / 32;
+  return (stage ? 8 * static_cast<size_t>(N) * D : 0) + 16 * static_cast<size_t>(N) +
+         4 * static_cast<size_t>(N) * words + 16;
+}
+
+template <int D, typename I, bool STAGE>
+__global__ void __launch_bounds__(1024)
+fixedset_bwd_mask_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
+                         const float* __restrict__ V, const float* __restrict__ dO,
+                         const I* __restrict__ Idx, float* __restrict__ dQ,
+                         float* __restrict__ dK, float* __restrict__ dV, int N, int kk,
+                         float scale) {
+  constexpr int E = D / 4;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int nd = N * D, words = (N + 31) >> 5;
+  float* rows = reinterpret_cast<float*>(smem_raw);  // STAGE: K, V, then Q, dO
+  float4* stats = reinterpret_cast<float4*>(smem_raw + (STAGE ? 8 * static_cast<size_t>(nd) : 0));
+  unsigned* mask = reinterpret_cast<unsigned*>(stats + N);  // [N keys][words]
+  int* repeated = reinterpret_cast<int*>(mask + static_cast<size_t>(N) * words);
+  const int b = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
+  const size_t boff = static_cast<size_t>(b) * nd;
+  const int sub = tid & 3, quads = nt >> 2;
+
+  for (int t = tid; t < N * words; t += nt) mask[t] = 0u;
+  if (tid == 0) *repeated = 0;
+  const float* Kb = Kx + boff;
+  const float* Vb = V + boff;
+  if constexpr (STAGE) {
+    for (int t = tid; t < nd / 4; t += nt) {
+      reinterpret_cast<float4*>(rows)[t] = reinterpret_cast<const float4*>(Kb)[t];
+      reinterpret_cast<float4*>(rows + nd)[t] = reinterpret_cast<const float4*>(Vb)[t];
+    }
+    Kb = rows;
+    Vb = rows + nd;
+  }
+  __syncthreads();
+  // 1. per query
+  for (int i0 = 0; i0 < N; i0 += quads) {
+    const int i = i0 + (tid >> 2);
+    if (i < N) {  // whole quads agree
+      const size_t row = static_cast<size_t>(b) * N + i;
+      const RowStats r = fixedset_bwd_row<D, I>(Q + row * D, dO + row * D, Kb, Vb, Idx + row * kk,
+                                                dQ + row * D, N, kk, scale, sub,
+                                                MaskSink{mask, repeated, words, i, sub});
+      if (sub == 0) stats[i] = make_float4(r.m, r.inv_l, r.dsum, 0.f);
+    }
+  }
+  __syncthreads();
+  if (*repeated) {  // uniform over the workgroup
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int t = tid; t < nd / 4; t += nt) {
+      reinterpret_cast<float4*>(dK + boff)[t] = z;
+      reinterpret_cast<float4*>(dV + boff)[t] = z;
+    }
+    __syncthreads();
+    for (int i0 = 0; i0 < N; i0 += quads) {
+      const int i = i0 + (tid >> 2);
+      if (i < N) {
+        const size_t row = static_cast<size_t>(b) * N + i;
+        fixedset_bwd_row<D, I>(Q + row * D, dO + row * D, Kb, Vb, Idx + row * kk, dQ + row * D, N,
+                               kk, scale, sub, AtomicSink<D>{dK + boff, dV + boff, sub, scale});
+      }
+    }
+    return;
+  }
+  const float* Qb = Q + boff;
+  const float* Gb = dO + boff;
+  if constexpr (STAGE) {  // K, V are read from global memory below
+    for (int t = tid; t < nd / 4; t += nt) {
+      reinterpret_cast<float4*>(rows)[t] = reinterpret_cast<const float4*>(Qb)[t];
+      reinterpret_cast<float4*>(rows + nd)[t] = reinterpret_cast<const float4*>(Gb)[t];
+    }
+    Qb = rows;
+    Gb = rows + nd;
+    __syncthreads();
+  }
+  // 2. per key
+  const float c2 = scale * kLog2eF;
+  for (int p0 = 0; p0 < N; p0 += quads) {
+    const int p = p0 + (tid >> 2);
+    if (p >= N) break;  // whole quads agree; no barrier follows
+    float kr[E], vr[E], dk[E], dv[E];
+    ld_f32<E>(kr, Kx + boff + static_cast<size_t>(p) * D + sub * E);
+    ld_f32<E>(vr, V + boff + static_cast<size_t>(p) * D + sub * E);
+#pragma unroll
+    for (int c = 0; c < E; ++c) dk[c] = dv[c] = 0.f;
+    const unsigned* mrow = mask + static_cast<size_t>(p) * words;
+    for (int w = 0; w < words; ++w) {
+      unsigned bits = mrow[w];
+      while (bits) {  // the same bits on the quad's four lanes
+        const int i = (w << 5) + __builtin_ctz(bits);
+        bits &= bits - 1u;
+        float q[E], g[E];
+        ld_f32<E>(q, Qb + static_cast<size_t>(i) * D + sub * E);
+        ld_f32<E>(g, Gb + static_cast<size_t>(i) * D + sub * E);
+        const float4 st = stats[i];
+        const float sc = quad_dot<E>(q, kr) * c2;
+        const float dw = quad_dot<E>(g, vr);
+        const float wgt = fast_exp2(sc - st.x) * st.y;
+        const float ds = wgt * (dw - st.z);
+#pragma unroll
+        for (int c = 0; c < E; ++c) {
+          dk[c] = fmaf(ds, q[c], dk[c]);
+          dv[c] = fmaf(wgt, g[c], dv[c]);
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < E; ++c) dk[c] *= scale;
+    st_f32<E>(dK + boff + static_cast<size_t>(p) * D + sub * E, dk);
+    st_f32<E>(dV + boff + static_cast<size_t>(p) * D + sub * E, dv);
   }
 }
 
@@ -677,12 +832,26 @@ constexpr size_t dkv_lds_bytes(int c) {
 // ---------------------------------------------------------------------------
 
 constexpr size_t kBwdLdsBudget = 65536;
+// the mask kernel runs one 1024-thread workgroup per CU whatever its LDS
+constexpr size_t kMaskLdsBudget = 160 * 1024;
 
 template <int D, typename I>
 static hipError_t launch_fixedset_bwd_t(const FixedsetBwdArgs& a) {
   hipStream_t st = static_cast<hipStream_t>(a.stream);
   const I* idx = static_cast<const I*>(a.idx);
   const size_t row_bytes = static_cast<size_t>(a.N) * D * sizeof(float);
+  const size_t mask_stage = fixedset_mask_lds_bytes(a.N, D, true);
+  const size_t mask_plain = fixedset_mask_lds_bytes(a.N, D, false);
+  if (mask_stage <= kMaskLdsBudget) {  // statistics, bitmask and the row's K, V fit LDS
+    hipLaunchKernelGGL((fixedset_bwd_mask_kernel<D, I, true>), dim3(a.B), dim3(1024), mask_stage,
+                       st, a.q, a.k, a.v, a.dout, idx, a.dq, a.dk, a.dv, a.N, a.kk, a.scale);
+    return hipGetLastError();
+  }
+  if (mask_plain <= kMaskLdsBudget) {  // statistics and bitmask fit LDS
+    hipLaunchKernelGGL((fixedset_bwd_mask_kernel<D, I, false>), dim3(a.B), dim3(1024), mask_plain,
+                       st, a.q, a.k, a.v, a.dout, idx, a.dq, a.dk, a.dv, a.N, a.kk, a.scale);
+    return hipGetLastError();
+  }
   const size_t gather_lds = fixedset_gather_lds_bytes(a.N, D, a.kk);
   if (gather_lds <= kBwdLdsBudget) {  // rows and per-entry lists fit LDS
     hipLaunchKernelGGL((fixedset_bwd_gather_kernel<D, I>), dim3(a.B), dim3(1024), gather_lds, st,

@@ -68,8 +68,8 @@ struct FixedsetBwdArgs {
   const void* idx;
   int idx_is_i64;
   float* dq;        // written
-  float* dk;        // accumulated (zero on entry)
-  float* dv;        // accumulated (zero on entry)
+  float* dk;        // written
+  float* dv;        // written
   int B, N, d, kk;
   float scale;
   void* stream;
