@@ -135,7 +135,7 @@ def profile_one(args, q, k, v, dev) -> int:
         _lib.LIB.tarmac_set_topk_filter(args.topk_filter)
     if name == "dense":
         fn = bound.dense(q, k, v)
-    elif name.startswith("topk"):
+    elif name in ("topk1", "topk2", "topk4"):
         fn = bound.topk(q, k, v, int(name[4:]))
     elif name == "fixedset2":
         idx = bound.topk(q, k, v, 2, with_idx=True)
@@ -153,6 +153,12 @@ def profile_one(args, q, k, v, dev) -> int:
         qb, kb, vb = (torch.from_numpy(g.standard_normal((4096, 256, 16)).astype(np.float32))
                       .to(dev).to(torch.bfloat16) for _ in range(3))
         fn = bound.dense(qb, kb, vb)
+    elif name == "topk95":
+        # the module benchmark's large-k core: B=256, N=384, d=16, k=95
+        g = np.random.default_rng(1234 + 7 * 384 + D)
+        q7, k7, v7 = (torch.from_numpy(g.standard_normal((256, 384, D)).astype(np.float32)).to(dev)
+                      for _ in range(3))
+        fn = bound.topk(q7, k7, v7, 95)
     elif name == "stream2":
         g = np.random.default_rng(4242)
         q4, k4, v4 = (torch.from_numpy(g.standard_normal((256, 1024, D)).astype(np.float32)).to(dev)
@@ -190,7 +196,7 @@ def main() -> int:
     ap.add_argument("--value-only", action="store_true",
                     help="time only the value kernel (for profiler runs)")
     ap.add_argument("--profile-kernel", default=None,
-                    choices=["dense", "dense_bf16", "dense_bf16_d16", "topk1", "topk2", "topk4", "fixedset2", "zorder",
+                    choices=["dense", "dense_bf16", "dense_bf16_d16", "topk1", "topk95", "topk2", "topk4", "fixedset2", "zorder",
                              "stream2"],
                     help="run only this kernel (headline shape; zorder/stream at their configs) "
                          "--warmup + --steps times, for profiler counter passes")

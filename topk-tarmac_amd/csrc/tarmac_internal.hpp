@@ -125,6 +125,8 @@ struct KnnArgs {
 hipError_t run_topk(const TopkArgs& a);
 hipError_t run_topk_filter(const TopkArgs& a);
 hipError_t run_topk_packed(const TopkArgs& a, bool split);
+bool topk_hist_supported(const TopkArgs& a);  // fp32, d = 16, k > 8, N <= 512
+hipError_t run_topk_hist(const TopkArgs& a);
 bool packed_split_supported(int dtype, int d);
 bool topk_filter_supported(int dtype, int d, int topk);
 // tarmac_set_topk_filter modes

@@ -682,6 +682,7 @@ hipError_t run_topk(const TopkArgs& a) {
       case kPathLists: break;
     }
   }
+  if (topk_hist_supported(a)) return run_topk_hist(a);
   switch (a.dtype == kF32 ? a.d : -a.d) {
     case 8: return dispatch_topk<float, 8>(a);
     case 16: return dispatch_topk<float, 16>(a);

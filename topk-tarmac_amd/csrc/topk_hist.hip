@@ -1,0 +1,674 @@
+// Exact top-k attention for large k (fp32, d = 16, N <= 512): every score of
+// a query stays in registers, a histogram of them locates the k-th largest,
+// and the kept keys' softmax weights drive the MFMA aggregation of the dense
+// kernel (every other key weighs 0).
+//
+// Reference behaviour: the top-k core (src/agents/mappo.py:192-231 topk_gather,
+// src/kernels/fused_topk_attention.py:296-355) at the module's k = 0.25 (N - 1)
+// (scripts/microbenchmark_comm.py), ties to the lower index
+// (src/kernels/streaming_topk_attention.py:37-44); the retained indices come
+// out in ascending order.
+//
+// Layout: workgroup = (batch row b, 64 queries), four waves of 16 queries;
+// lane l owns query l % 16 and, in 16-key tile t, keys 16 t + 4 (l / 16) + r.
+//  1. scores: fp32 MFMA on the key rows staged in LDS, q pre-multiplied by the
+//     power-of-two scale: these ARE the canonical fp32 scores (the MFMA chain
+//     rounds like the canonical fmaf chain, in its order).
+//  2. histogram: kHistBins bins spanning [min, max] of a query's scores,
+//     counted with LDS atomics; a scan from the top finds the bin tb that
+//     holds the k-th largest.
+//  3. select: scores above tb's upper edge (plus the binning's rounding
+//     slack) are kept, scores below its lower edge are dropped; the scores in
+//     between -- bin tb, every tie at the k-th score among them -- go to
+//     per-lane lists and are ranked by (score desc, index asc); the best
+//     k - |kept| join.
+//  4. aggregate: P = 2^((s - max) log2 e) on the kept keys (0 elsewhere) in
+//     the fp32 MFMA P V product of the dense kernel, plus the joining keys'
+//     value rows; out = acc / sum.
+//  fallback: a wave with a query whose band could overflow the lists (ties,
+//     rows of nearly equal scores) or with non-finite inputs or scores takes
+//     the queries one at a time over the whole wave: the k-th largest 32-bit
+//     ordered key by bisection, ties to the lower index.
+#include <type_traits>
+
+#include "exact.hpp"
+#include "frag.hpp"
+#include "tarmac_internal.hpp"
+
+namespace tarmac {
+
+namespace {
+
+constexpr int kHistBins = 128;   // per query
+constexpr int kHistLane = 16;    // listed keys per lane (fast path); 4 lanes per query
+constexpr int kHistWaves = 4;    // 16-query waves per workgroup
+constexpr int kHistSel = 16;     // selection bitmask words per query (N <= 512)
+constexpr int kHistQWords = kHistBins + kHistSel;  // scratch words per query
+constexpr unsigned kHistMaskedBits = 0xffffffffu;  // a NaN; its ordered key is INT_MIN
+constexpr unsigned kListUpper = 0x80000000u;       // listed key lies in a bin above tb
+
+__device__ __forceinline__ float masked_score() { return __uint_as_float(kHistMaskedBits); }
+
+// Monotone fp32 -> int32 (NaN above +inf, kHistMaskedBits -> INT_MIN).
+__device__ __forceinline__ int ordered_key(float x) {
+  const int i = __float_as_int(x);
+  return i ^ ((i >> 31) & 0x7fffffff);
+}
+
+// v_cvt_u32_f32 (NaN, y < 0 -> 0).
+__device__ __forceinline__ unsigned cvt_u32(float y) {
+  unsigned u;
+  asm("v_cvt_u32_f32 %0, %1" : "=v"(u) : "v"(y));
+  return u;
+}
+
+// Histogram bin of a score (NaN -> 0); monotone in x. The clamp matters only
+// when |min| dwarfs the range, where the rounding of c0 can reach bin
+// kHistBins (such rows also fail the fast path's margin test).
+__device__ __forceinline__ unsigned bin_of(float x, float inv, float c0) {
+  return min(cvt_u32(fmaf(x, inv, c0)), static_cast<unsigned>(kHistBins - 1));
+}
+
+// x, as a value the compiler cannot relate to other expressions: key
+// indices recomputed in a later phase then cost an add instead of keeping
+// one register per score live from an earlier phase.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Within one wavefront: LDS writes issued before are seen by reads issued after.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Sum over the four lane rows (lanes l, l ^ 16, l ^ 32, l ^ 48).
+__device__ __forceinline__ unsigned rows_sum(unsigned x) {
+  const LanePair p = swap_rows16(x);
+  const LanePair q = swap_rows32(p.a + p.b);
+  return q.a + q.b;
+}
+__device__ __forceinline__ float rows_sum(float x) {
+  const LanePair p = swap_rows16(__float_as_uint(x));
+  const float s = __uint_as_float(p.a) + __uint_as_float(p.b);
+  const LanePair q = swap_rows32(__float_as_uint(s));
+  return __uint_as_float(q.a) + __uint_as_float(q.b);
+}
+__device__ __forceinline__ float rows_max(float x) {
+  const LanePair p = swap_rows16(__float_as_uint(x));
+  const float s = fmaxf(__uint_as_float(p.a), __uint_as_float(p.b));
+  const LanePair q = swap_rows32(__float_as_uint(s));
+  return fmaxf(__uint_as_float(q.a), __uint_as_float(q.b));
+}
+__device__ __forceinline__ float rows_min(float x) {
+  const LanePair p = swap_rows16(__float_as_uint(x));
+  const float s = fminf(__uint_as_float(p.a), __uint_as_float(p.b));
+  const LanePair q = swap_rows32(__float_as_uint(s));
+  return fminf(__uint_as_float(q.a), __uint_as_float(q.b));
+}
+
+// Canonical fp32 score (the order of canon_pair<float, 16, true>) from the
+// query row pre-multiplied by the power-of-two scale, held in registers.
+__device__ __forceinline__ float canon_row16(const float (&qs)[16], const float* krow) {
+  float k[16];
+  ld_f32<16>(k, krow);
+  float acc = 0.f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) acc = fmaf(qs[kk * 4 + t], k[kk * 4 + t], acc);
+  return acc;
+}
+
+template <int NT>
+constexpr size_t hist_scratch_bytes() {
+  return static_cast<size_t>(kHistWaves) * 16 * kHistQWords * 4 + kHistWaves * 32 * 4;
+}
+
+template <int NT>
+constexpr size_t hist_region_a_bytes() {
+  const size_t ks = static_cast<size_t>(16 * NT) * Frag<float, 16>::LDK * sizeof(float);
+  const size_t sc = hist_scratch_bytes<NT>();
+  return ks > sc ? ks : sc;
+}
+
+template <int NT>
+constexpr size_t hist_lds_bytes() {
+  return 16 + hist_region_a_bytes<NT>() + static_cast<size_t>(16) * (16 * NT + 4) * sizeof(float);
+}
+
+// Sums and maximum over the whole wave (DPP row reductions, then row swaps).
+__device__ __forceinline__ unsigned wave_sum(unsigned x) {
+  const int r = row16_reduce(static_cast<int>(x), [](int a, int b) { return a + b; });
+  return rows_sum(static_cast<unsigned>(r));
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  return rows_sum(row16_reduce(x, [](float a, float b) { return a + b; }));
+}
+
+// The fallback of a wave: its queries one at a time over all 64 lanes (keys
+// j = lane + 64 i), canonical fp32 scores, the k-th largest ordered key by
+// bisection over the 32-bit range, ties at it to the lowest indices (a
+// ballot prefix in ascending key order), the kept value rows summed across
+// the wave. Writes out (and the ascending indices) itself.
+template <int NT>
+__device__ __forceinline__ void hist_fallback_wave(const float* Qb, const float* Kb,
+                                                   const float* Vb, float* Ob, int32_t* Ib,
+                                                   int N, int q0, int topk, float scale,
+                                                   int lane) {
+  constexpr int NI = (16 * NT + 63) / 64;  // keys per lane
+  const unsigned kq = static_cast<unsigned>(topk);
+  const uint64_t below = (1ull << lane) - 1ull;
+  for (int qq = 0; qq < 16; ++qq) {
+    const int qi = q0 + qq;
+    if (qi >= N) break;  // uniform
+    float qs[16];
+    ld_f32<16>(qs, Qb + static_cast<size_t>(qi) * 16);
+#pragma unroll
+    for (int c = 0; c < 16; ++c) qs[c] *= scale;
+    int key[NI];
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int j = lane + 64 * i;
+      const bool valid = j < N && j != qi;
+      const float c = valid ? canon_row16(qs, Kb + static_cast<size_t>(j) * 16) : masked_score();
+      mloc = fmaxf(mloc, c);
+      key[i] = ordered_key(c);
+    }
+    const float mq = wave_max_rows(mloc);
+    long lo = -2147483647L, hi = 2147483647L;  // INT_MIN (masked) never counts
+    for (int it = 0; it < 32; ++it) {
+      const long mid = lo + (hi - lo + 1) / 2;
+      unsigned c = 0u;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) c += key[i] >= mid ? 1u : 0u;
+      c = wave_sum(c);
+      if (c >= kq) lo = mid;
+      else hi = mid - 1;
+      if (c == kq) break;  // uniform: exactly k keys at or above lo
+    }
+    const int thr = static_cast<int>(lo);
+    unsigned gt = 0u;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) gt += key[i] > thr ? 1u : 0u;
+    const unsigned need_ties = kq - wave_sum(gt);
+    unsigned ties = 0u, base = 0u;
+    float acc[16], lsum = 0.f;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) acc[c] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int j = lane + 64 * i;
+      const bool tie = key[i] == thr;
+      const uint64_t tmask = __ballot(tie);
+      const bool sel = key[i] > thr || (tie && ties + __popcll(tmask & below) < need_ties);
+      const uint64_t smask = __ballot(sel);
+      if (sel) {
+        // the ordered key maps back to the score by the same xor
+        const float c = __int_as_float(ordered_key(__int_as_float(key[i])));
+        const float p = fast_exp2((c - mq) * kLog2eF);  // subtract first: exact near the max
+        lsum += p;
+        float vr[16];
+        ld_f32<16>(vr, Vb + static_cast<size_t>(j) * 16);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = fmaf(p, vr[e], acc[e]);
+        if (Ib != nullptr) {
+          const unsigned pos = base + static_cast<unsigned>(__popcll(smask & below));
+          if (pos < kq) Ib[static_cast<size_t>(qi) * topk + pos] = j;
+        }
+      }
+      ties += static_cast<unsigned>(__popcll(tmask));
+      base += static_cast<unsigned>(__popcll(smask));
+    }
+    const float il = 1.f / wave_sum(lsum);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = wave_sum(acc[e]);
+    if (lane < 4) {
+      f32x4 o;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (e == 4 * lane + r) v = acc[e];
+        o[r] = v * il;
+      }
+      *reinterpret_cast<f32x4*>(Ob + static_cast<size_t>(qi) * 16 + 4 * lane) = o;
+    }
+  }
+}
+
+}  // namespace
+
+// Waves per SIMD the register budget is held to (the scores of a query tile
+// take NT x 4 registers); without the cap the compiler parks a second copy
+// of them in AGPRs and drops to one wave.
+template <int NT>
+constexpr int hist_waves_per_eu() {
+  return NT <= 8 ? 4 : (NT <= 16 ? 3 : 2);
+}
+
+template <int NT, bool WITH_IDX>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(hist_waves_per_eu<NT>(), hist_waves_per_eu<NT>())))
+topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
+                 const float* __restrict__ V, float* __restrict__ O, int32_t* __restrict__ Idx,
+                 int N, int n_qblk, int topk, float scale, int nblocks) {
+  using F = Frag<float, 16>;
+  constexpr int D = 16, LDK = F::LDK, NP = 16 * NT, LDV = NP + 4;
+  constexpr int BT = 4;  // tiles per score block
+  static_assert(NT % BT == 0 && NP <= 32 * kHistSel, "tile count");
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  unsigned* flags = reinterpret_cast<unsigned*>(smem_raw);  // [0] a non-finite key element
+  unsigned char* region_a = smem_raw + 16;
+  float* Ks = reinterpret_cast<float*>(region_a);            // key rows, then scratch
+  float* Vt = reinterpret_cast<float*>(region_a + hist_region_a_bytes<NT>());
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int blk = xcd_logical_block(blockIdx.x, nblocks);
+  const int b = blk / n_qblk, qblk = blk - b * n_qblk;
+  const int q0 = (qblk * kHistWaves + wave) * 16;  // first query of this wave (uniform)
+  const int col = lane & 15, grp = lane >> 4;
+  const bool live = q0 + col < N;
+  const int qi = live ? q0 + col : N - 1;
+  const size_t boff = static_cast<size_t>(b) * N * D;
+  const float* Kb = Kx + boff;
+
+  // ---- stage the row's keys and transposed values ------------------------
+  if (threadIdx.x == 0) flags[0] = 0u;
+  stage_rows<float, D, LDK>(Ks, Kb, N, NP);
+  stage_vt<float, D, 16>(Vt, LDV, V + boff, N, NP);
+  F frag;
+  frag.load_q(Q + boff + static_cast<size_t>(qi) * D, grp, scale);  // exact: power-of-two scale
+  bool finite_in = true;  // this lane's query elements
+#pragma unroll
+  for (int e = 0; e < F::E; ++e) finite_in = finite_in && __builtin_isfinite(frag.q[e]);
+  __syncthreads();
+  {
+    bool kfin = true;  // the staged keys, a quarter row per thread and pass
+    for (int v = threadIdx.x; v < N * 4; v += blockDim.x) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(Ks + (v >> 2) * LDK + 4 * (v & 3));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) kfin = kfin && __builtin_isfinite(x[e]);
+    }
+    if (!__all(kfin) && lane == 0) atomicOr(flags, 1u);
+  }
+
+  // ---- canonical scores, masked self / padding ----------------------------
+  float s[NT][4];
+  const int diag = q0 >> 4;  // the tile holding this wave's self pairs
+#pragma unroll
+  for (int t0 = 0; t0 < NT; t0 += BT) {
+    f32x4 acc[1][BT];
+    F fr[1] = {frag};
+    block_scores<F, 1, BT>(fr, Ks, 16 * t0, LDK, lane, acc);
+#pragma unroll
+    for (int t = 0; t < BT; ++t) {
+      const int tt = t0 + t;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[tt][r] = acc[0][t][r];
+      if (tt == diag || 16 * tt + 16 > N) {  // wave-uniform
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = 16 * tt + 4 * grp + r;
+          if (j >= N || j == qi) s[tt][r] = masked_score();
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // one block's key fragments live at a time
+  }
+  __syncthreads();  // every wave is past its scores: region A becomes the waves' scratch
+  if (q0 >= N) return;  // a wave of padding queries (no barrier follows)
+  finite_in = finite_in && flags[0] == 0u;
+
+  unsigned* qscr = reinterpret_cast<unsigned*>(region_a) +
+                   static_cast<size_t>(wave * 16 + col) * kHistQWords;  // this lane's query
+  unsigned* hist = qscr;                   // [kHistBins]
+  unsigned* selw = qscr + kHistBins;       // [kHistSel] selection bitmask
+  {
+    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+    // a query's 144 words: 36 uint4, 9 per lane row
+#pragma unroll
+    for (int i = 0; i < kHistQWords / 16; ++i)
+      reinterpret_cast<uint4*>(qscr)[grp * (kHistQWords / 16) + i] = z;
+  }
+
+  // ---- range and histogram ------------------------------------------------
+  float mx = -INFINITY, mn = INFINITY;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      mx = fmaxf(mx, s[t][r]);  // NaN (masked) operands are ignored
+      mn = fminf(mn, s[t][r]);
+    }
+  mx = rows_max(mx);
+  mn = rows_min(mn);
+  const float range = mx - mn;
+  const bool finite_s = __builtin_isfinite(range);
+  const float inv = (finite_s && range > 0.f) ? (kHistBins * (1.f - 0x1p-20f)) / range : 0.f;
+  const float c0 = -mn * inv;
+  wave_lds_sync();
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) atomicAdd(hist + bin_of(s[t][r], inv, c0), 1u);
+  wave_lds_sync();
+
+  // ---- scan: the bin tb holding the k-th largest -------------------------
+  const unsigned n_masked = static_cast<unsigned>(NP - N + 1);  // padding keys and self, in bin 0
+  const unsigned kq = static_cast<unsigned>(topk);
+  // four-bin group sums of this lane row's 32 bins (32 grp .. 32 grp + 31)
+  unsigned q4[8], tot = 0u;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint4 w = reinterpret_cast<const uint4*>(hist)[grp * 8 + i];
+    q4[i] = w.x + w.y + w.z + w.w - ((grp == 0 && i == 0) ? n_masked : 0u);
+    tot += q4[i];
+  }
+  uint32_t rt[4];
+  gather_rows(tot, rt);
+  unsigned above = 0u;  // valid scores in the rows above this lane's
+#pragma unroll
+  for (int g = 0; g < 4; ++g) above += g > grp ? rt[g] : 0u;
+  // the group of four bins, then the bin (scanning downwards)
+  int qg = -1;
+  unsigned above_g = 0u, run = above;
+#pragma unroll
+  for (int i = 7; i >= 0; --i) {
+    const unsigned nrun = run + q4[i];
+    if (run < kq && nrun >= kq) {
+      qg = i;
+      above_g = run;
+    }
+    run = nrun;
+  }
+  int tb_l = -1;
+  unsigned above_l = 0u;
+  if (qg >= 0) {
+    const uint4 w = reinterpret_cast<const uint4*>(hist)[grp * 8 + qg];
+    const unsigned hq[4] = {w.x - ((grp == 0 && qg == 0) ? n_masked : 0u), w.y, w.z, w.w};
+    unsigned rr = above_g;
+#pragma unroll
+    for (int e = 3; e >= 0; --e) {
+      const unsigned nr = rr + hq[e];
+      if (rr < kq && nr >= kq) {
+        tb_l = 32 * grp + 4 * qg + e;
+        above_l = rr;
+      }
+      rr = nr;
+    }
+  }
+  int tb;
+  unsigned above_tb;
+  {
+    uint32_t tv[4], av[4];
+    gather_rows(static_cast<uint32_t>(tb_l + 1), tv);
+    gather_rows(above_l, av);
+    tb = -1;
+    above_tb = 0u;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      if (tv[g] != 0u) {
+        tb = static_cast<int>(tv[g]) - 1;
+        above_tb = av[g];
+      }
+  }
+  // bins tb - 1 .. tb + 1 bound the list (the margin is under half a bin)
+  auto bin_count = [&](int bin) -> unsigned {
+    if (bin < 0 || bin >= kHistBins) return 0u;
+    const unsigned h = hist[bin];
+    return bin == 0 ? h - n_masked : h;
+  };
+  const unsigned n_valid = static_cast<unsigned>(N - 1);
+  const unsigned cand_bound = inv > 0.f ? bin_count(tb - 1) + bin_count(tb) + bin_count(tb + 1)
+                                        : n_valid;
+
+  // ---- thresholds ---------------------------------------------------------
+  // bin tb spans [lo_edge, hi_edge) up to the rounding of the binning (slack)
+  const float w = inv > 0.f ? 1.f / inv : 0.f;
+  const float lo_edge = inv > 0.f ? fmaf(static_cast<float>(tb), w, mn) : mn;
+  const float hi_edge = inv > 0.f ? fmaf(static_cast<float>(tb + 1), w, mn) : mx;
+  const float slack = 0x1p-18f * (fabsf(mx) + fabsf(mn) + range);
+  const float hiT = hi_edge + slack, loT = lo_edge - slack;
+  const bool fast = finite_in && finite_s && cand_bound <= 4 * kHistLane &&
+                    (inv == 0.f || slack < 0.5f * w);
+
+  if (!__all(fast)) {
+    hist_fallback_wave<NT>(Q + boff, Kb, V + boff, O + boff,
+                           Idx ? Idx + static_cast<size_t>(b) * N * topk : nullptr, N, q0, topk,
+                           scale, lane);
+    return;
+  }
+
+  // ---- kept keys into the product; the band between the edges flagged ------
+  // exponents: one fma while the maximum is small enough for its rounding in
+  // -m log2(e) to be negligible, else subtract first (exact near the maximum)
+  const bool small = __all(fabsf(mx) <= 16.f);
+  const float nm = -mx * kLog2eF;
+  auto expw = [&](float x) {
+    return small ? fast_exp2(fmaf(x, kLog2eF, nm)) : fast_exp2((x - mx) * kLog2eF);
+  };
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  float lsum = 0.f;
+  constexpr int NB32 = (NT * 4 + 31) / 32;
+  uint32_t band[NB32];     // bit (4 t + r) % 32 of word (4 t + r) / 32: in the band
+  uint32_t kept[NB32];     // the same for kept keys (retained indices only)
+#pragma unroll
+  for (int i = 0; i < NB32; ++i) band[i] = kept[i] = 0u;
+  auto pv_pass = [&](auto exp_small) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float x = s[t][r];
+        const bool keep = x > hiT;
+        // the select goes on the exponent (2^-inf = 0): no branch around the exp
+        const float y = exp_small ? fmaf(x, kLog2eF, nm) : (x - mx) * kLog2eF;
+        p[r] = fast_exp2(keep ? y : -INFINITY);
+        lsum += p[r];
+        const int bit = (4 * t + r) & 31, word = (4 * t + r) >> 5;
+        band[word] |= static_cast<uint32_t>(!keep && x >= loT) << bit;
+        if (WITH_IDX) kept[word] |= static_cast<uint32_t>(keep) << bit;
+      }
+      const f32x4 vv = *reinterpret_cast<const f32x4*>(Vt + col * LDV + 16 * t + 4 * grp);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc = mfma_f32_16x16x4(vv[u], p[u], acc);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  if (small) pv_pass(std::true_type{});
+  else pv_pass(std::false_type{});
+#pragma unroll
+  for (int i = 0; i < NB32; ++i) {  // materialised here: the scores die with the pass
+    band[i] = static_cast<uint32_t>(opaque(static_cast<int>(band[i])));
+    kept[i] = static_cast<uint32_t>(opaque(static_cast<int>(kept[i])));
+  }
+
+  // ---- the band onto per-lane lists (its scores recomputed canonically) -----
+  // lane row g of a query lists at words [16 g, 16 g + 16): key, bit 31 set
+  // when its bin lies above tb; its score at [64 + 16 g, ...)
+  unsigned nl = 0u;
+  {
+    float qs[16];
+    ld_f32<16>(qs, Q + boff + static_cast<size_t>(qi) * D);
+#pragma unroll
+    for (int c = 0; c < 16; ++c) qs[c] *= scale;
+#pragma unroll
+    for (int w = 0; w < NB32; ++w) {
+      uint32_t bits = band[w];
+      while (bits) {  // a few keys per lane
+        const int pos = 32 * w + __builtin_ctz(bits);
+        bits &= bits - 1u;
+        const int j = 16 * (pos >> 2) + 4 * grp + (pos & 3);
+        if (nl < kHistLane) {
+          const float c = canon_row16(qs, Kb + static_cast<size_t>(j) * D);  // equals s[t][r]
+          const bool upper = static_cast<int>(bin_of(c, inv, c0)) > tb;
+          qscr[kHistLane * grp + nl] = static_cast<unsigned>(j) | (upper ? kListUpper : 0u);
+          qscr[4 * kHistLane + kHistLane * grp + nl] = __float_as_uint(c);
+        }
+        ++nl;
+      }
+    }
+  }
+  if (!__all(nl <= kHistLane)) {  // a lane's share of the band overflowed: start over exactly
+    hist_fallback_wave<NT>(Q + boff, Kb, V + boff, O + boff,
+                           Idx ? Idx + static_cast<size_t>(b) * N * topk : nullptr, N, q0, topk,
+                           scale, lane);
+    return;
+  }
+  wave_lds_sync();
+
+  // ---- rank the listed keys ------------------------------------------------
+  // Lists are read four entries at a time (one 16-byte LDS read for keys,
+  // one for scores); loop bounds are the wave's maxima, entries past a list's
+  // end are masked.
+  uint32_t nls[4];
+  gather_rows(nl, nls);  // list lengths of the query's four lane rows
+  const unsigned nlq = max(max(nls[0], nls[1]), max(nls[2], nls[3]));
+  const int chunks = static_cast<int>(wave_max_rows(static_cast<float>((nlq + 3u) >> 2)));
+  const uint4* lj4 = reinterpret_cast<const uint4*>(qscr);                   // keys
+  const f32x4* lc4 = reinterpret_cast<const f32x4*>(qscr + 4 * kHistLane);  // scores
+  unsigned upper = 0u;
+  for (int u = 0; u < chunks; ++u) {
+    const uint4 w = lj4[4 * grp + u];
+    const unsigned wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) upper += (4u * u + e < nl) ? (wv[e] >> 31) : 0u;
+  }
+  upper = rows_sum(upper);
+  const unsigned need = kq - (above_tb - upper);  // 1 <= need <= listed
+  uint32_t taken = 0u;  // bit i: own entry i joins
+  for (int u = 0; u < chunks; ++u) {
+    const uint4 ow = lj4[4 * grp + u];
+    const f32x4 oc = lc4[4 * grp + u];
+    const unsigned oj[4] = {ow.x & 0xffffu, ow.y & 0xffffu, ow.z & 0xffffu, ow.w & 0xffffu};
+    unsigned rank[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      for (int v = 0; v < chunks; ++v) {
+        const uint4 w = lj4[4 * g + v];
+        const f32x4 c2 = lc4[4 * g + v];
+        const unsigned j2[4] = {w.x & 0xffffu, w.y & 0xffffu, w.z & 0xffffu, w.w & 0xffffu};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool in = 4u * v + e < nls[g];
+#pragma unroll
+          for (int o = 0; o < 4; ++o)
+            rank[o] += (in && (c2[e] > oc[o] || (c2[e] == oc[o] && j2[e] < oj[o]))) ? 1u : 0u;
+        }
+      }
+#pragma unroll
+    for (int o = 0; o < 4; ++o)
+      taken |= (4u * u + o < nl && rank[o] < need) ? (1u << (4 * u + o)) : 0u;
+  }
+  wave_lds_sync();
+  // joining entries carry their weight in the score slot, the others 0
+  for (int u = 0; u < chunks; ++u) {
+    f32x4 c = lc4[4 * grp + u];
+#pragma unroll
+    for (int o = 0; o < 4; ++o) {
+      const float e = expw(c[o]);
+      c[o] = (taken >> (4 * u + o)) & 1u ? e : 0.f;
+    }
+    reinterpret_cast<f32x4*>(qscr + 4 * kHistLane)[4 * grp + u] = c;
+  }
+  wave_lds_sync();
+
+  // ---- the joining keys' value rows (from the transposed copy in LDS) ------
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+    for (int v = 0; v < chunks; ++v) {
+      const uint4 w = lj4[4 * g + v];
+      const f32x4 pw = lc4[4 * g + v];
+      const unsigned jj[4] = {w.x & 0xffffu, w.y & 0xffffu, w.z & 0xffffu, w.w & 0xffffu};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool in = 4u * v + e < nls[g];
+        const float p = in ? pw[e] : 0.f;
+        const unsigned j = in ? jj[e] : 0u;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = fmaf(p, Vt[(4 * grp + r) * LDV + j], acc[r]);
+        lsum += grp == 0 ? p : 0.f;
+      }
+    }
+  if constexpr (WITH_IDX) {  // the owners mark their joining entries
+    for (int u = 0; u < chunks; ++u) {
+      const uint4 w = lj4[4 * grp + u];
+      const unsigned jj[4] = {w.x & 0xffffu, w.y & 0xffffu, w.z & 0xffffu, w.w & 0xffffu};
+#pragma unroll
+      for (int o = 0; o < 4; ++o)
+        if ((taken >> (4 * u + o)) & 1u) atomicOr(selw + (jj[o] >> 5), 1u << (jj[o] & 31));
+    }
+  }
+
+  // ---- normalise and store ------------------------------------------------
+  const float l = rows_sum(lsum);
+  const float il = 1.f / l;
+  if (live) {
+    f32x4 o;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = acc[r] * il;
+    *reinterpret_cast<f32x4*>(O + boff + static_cast<size_t>(qi) * D + 4 * grp) = o;
+  }
+  if constexpr (!WITH_IDX) return;
+  // ---- retained indices, ascending -----------------------------------------
+  // the kept flags of tiles 2w and 2w + 1 fill word w: lane row g holds bits
+  // 4 g .. 4 g + 3 of each 16-key half
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const uint32_t nib = (kept[(4 * t) >> 5] >> ((4 * t) & 31)) & 0xfu;
+    if (nib) atomicOr(selw + (t >> 1), nib << (16 * (t & 1) + 4 * grp));
+  }
+  wave_lds_sync();
+  if (!live) return;
+  constexpr int NW = NP / 32;
+  uint32_t wv[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) wv[i] = selw[i];
+  unsigned base = 0u;
+  int32_t* dst = Idx + (static_cast<size_t>(b) * N + qi) * topk;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    if ((i & 3) == grp) {
+      uint32_t bits = wv[i];
+      unsigned pos = base;
+      while (bits) {
+        if (pos < static_cast<unsigned>(topk)) dst[pos] = 32 * i + __builtin_ctz(bits);
+        ++pos;
+        bits &= bits - 1u;
+      }
+    }
+    base += __builtin_popcount(wv[i]);
+  }
+}
+
+bool topk_hist_supported(const TopkArgs& a) {
+  return a.dtype == kF32 && a.d == 16 && a.select == kSelTopk && a.topk > kTopkSmallMax &&
+         a.N <= 512 && (__builtin_bit_cast(uint32_t, a.scale) & 0x007fffffu) == 0u;
+}
+
+template <int NT>
+static hipError_t launch_hist(const TopkArgs& a) {
+  const int n_qblk = (a.N + 16 * kHistWaves - 1) / (16 * kHistWaves);
+  const int nblocks = a.B * n_qblk;
+  auto kern = a.idx != nullptr ? topk_hist_kernel<NT, true> : topk_hist_kernel<NT, false>;
+  hipLaunchKernelGGL(kern, dim3(nblocks), dim3(64 * kHistWaves), hist_lds_bytes<NT>(),
+                     static_cast<hipStream_t>(a.stream), static_cast<const float*>(a.q),
+                     static_cast<const float*>(a.k), static_cast<const float*>(a.v),
+                     static_cast<float*>(a.out), a.idx, a.N, n_qblk, a.topk, a.scale, nblocks);
+  return hipGetLastError();
+}
+
+hipError_t run_topk_hist(const TopkArgs& a) {
+  if (a.N <= 128) return launch_hist<8>(a);
+  if (a.N <= 256) return launch_hist<16>(a);
+  if (a.N <= 384) return launch_hist<24>(a);
+  return launch_hist<32>(a);
+}
+
+}  // namespace tarmac

@@ -46,18 +46,6 @@
 
 namespace tarmac {
 
-// bf16 score error bound, relative to |q| |k_j|: bf16 MFMA sums exact
-// products with an accumulation error measured <= 2^-21.9 of the sum of
-// their magnitudes; the canonical fp32 chain adds <= d 2^-24 of it (one
-// rounding per step); sum_c |q_c k_c| <= |q| |k_j|. 2^-18 (d <= 32) and
-// 2^-17 (d = 64) cover both with margin, including the fp32 rounding of the
-// bound itself.
-template <int D>
-constexpr float packed_eps() {
-  return D <= 32 ? 1.0f / 262144.0f : 1.0f / 131072.0f;
-}
-constexpr float kPackedNormLimit = 1.329228e36f;  // 2^120: |q| max|k| at or above fails the proof
-
 // 16-key tiles per scan block: two keep the block's scores and key fragments
 // at 24 VGPRs (four tiles: 48).
 constexpr int kPackedBlockTiles = 2;
