@@ -1,0 +1,124 @@
+"""Full-batch equivalence at the timed configurations, every row checked.
+
+The reference checks its kernels over every timed configuration
+(scripts/verify_all_configurations.py:41-53,117-265); here each shape the
+benchmark times runs at its full batch, with the benchmark's own inputs where
+it draws them, against the C oracle (canonical fp32 scores, float64
+aggregation):
+
+* fp32, B = 1024, d = 16, N in {32, ..., 512}, k in {1, 2, 4};
+  retained indices bit-exact in (score desc, index asc) order, outputs within
+  1e-5 (normwise); dense at N = 256 and 512 within 1e-5 of float64;
+* streaming top-k, B = 256, d = 16, N in {512, 1024}, k in
+  {1, 2, 4}, fp32 (1e-5) and bf16 (indices on the canonical fp32 scores of
+  the bf16 inputs, outputs within 1e-2);
+* Z-order select+attend, B = 1024, N = 512, k = 2, 16 bits:
+  selection bit-exact, outputs within 1e-5 of float64 over that selection;
+* bf16 at B = 4096, one (N, d) per k.
+
+The oracle's top-k lists for k = 4 carry those for k = 1 and 2 as prefixes
+(one order, score desc / index asc), so each shape calls it once.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import tarmac_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-5
+BF16_TOL = 1e-2
+
+
+def _inputs(seed, B, N, d):
+    g = np.random.default_rng(seed)
+    return [g.standard_normal((B, N, d)).astype(np.float32) for _ in range(3)]
+
+
+def _topk(q, k, v, kk, dtype=torch.float32, key_chunk=None):
+    from tarmac.kernels import topk_attention
+    qd, kd, vd = (torch.from_numpy(x).cuda().to(dtype) for x in (q, k, v))
+    out, idx = topk_attention(qd, kd, vd, kk, return_indices=True, key_chunk=key_chunk)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy(), idx.cpu().numpy()
+
+
+def _attend64(q, k, v, idx):
+    """float64 softmax attention of each query over its listed peers."""
+    q64, k64, v64 = (x.astype(np.float64) for x in (q, k, v))
+    rows = np.arange(q.shape[0])[:, None, None]
+    kg, vg = k64[rows, idx], v64[rows, idx]           # [B, N, k, d]
+    s = np.einsum("bnd,bnkd->bnk", q64, kg) / np.sqrt(q.shape[-1])
+    w = np.exp(s - s.max(-1, keepdims=True))
+    w /= w.sum(-1, keepdims=True)
+    return np.einsum("bnk,bnkd->bnd", w, vg)
+
+
+def _check_prefixes(q, k, v, got, tol):
+    """got: {k: (out, idx)}; the oracle run once at the largest k."""
+    kmax = max(got)
+    _, idx_c = O.canon_topk(q, k, v, kmax)
+    for kk, (out, idx) in got.items():
+        want = idx_c[..., :kk]
+        assert np.array_equal(idx, want), f"k={kk}: retained indices differ from the oracle"
+        ref = _attend64(q, k, v, want)
+        err = np.abs(out - ref).max() / np.abs(ref).max()
+        assert err <= tol, f"k={kk}: output error {err:.2e}"
+
+
+@pytest.mark.parametrize("N", [32, 64, 128, 256, 384, 512])
+def test_configs1_full_batch(N):
+    B, d = 1024, 16
+    q, k, v = _inputs(1234 + 7 * N + d, B, N, d)  # the benchmark's inputs
+    got = {kk: _topk(q, k, v, kk) for kk in (1, 2, 4)}
+    _check_prefixes(q, k, v, got, F32_TOL)
+
+
+@pytest.mark.parametrize("N", [256, 512])
+def test_configs1_dense_full_batch(N):
+    from tarmac.kernels import fused_dense_attention
+    B, d = 1024, 16
+    q, k, v = _inputs(1234 + 7 * N + d, B, N, d)
+    out = fused_dense_attention(*(torch.from_numpy(x).cuda() for x in (q, k, v)))
+    ref = O.canon_dense(q, k, v)
+    err = np.abs(out.cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err <= F32_TOL
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("N", [512, 1024])
+def test_configs3_streaming_full_batch(N, dtype):
+    B, d = 256, 16
+    q, k, v = _inputs(4242 if N == 1024 else 4242 + N, B, N, d)  # the benchmark's inputs
+    if dtype == "bf16":
+        q, k, v = (O.bf16_round(x) for x in (q, k, v))
+    tdt = torch.float32 if dtype == "fp32" else torch.bfloat16
+    got = {kk: _topk(q, k, v, kk, tdt, key_chunk=0) for kk in (1, 2, 4)}
+    _check_prefixes(q, k, v, got, F32_TOL if dtype == "fp32" else BF16_TOL)
+
+
+def test_configs4_zorder_full_batch():
+    from tarmac.kernels import zorder_attention
+    B, N, d, kk, bits = 1024, 512, 16, 2, 16
+    g = np.random.default_rng(4242 + N)  # the benchmark's inputs
+    q, k, v = (g.standard_normal((B, N, d)).astype(np.float32) for _ in range(3))
+    pos = g.random((B, N, 2)).astype(np.float32)
+    out, idx = zorder_attention(*(torch.from_numpy(x).cuda() for x in (q, k, v, pos)), kk, bits,
+                                return_indices=True)
+    torch.cuda.synchronize()
+    want = O.canon_morton_window(pos, kk, bits)
+    assert np.array_equal(idx.cpu().numpy(), want)
+    ref = _attend64(q, k, v, want)
+    assert np.abs(out.cpu().numpy() - ref).max() <= F32_TOL * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("N,d,kk", [(64, 16, 1), (256, 16, 2), (64, 64, 4), (64, 32, 2)])
+def test_configs2_bf16_b4096(N, d, kk):
+    B = 4096
+    q, k, v = (O.bf16_round(x) for x in _inputs(77 + N + d, B, N, d))  # the benchmark's inputs
+    out, idx = _topk(q, k, v, kk, torch.bfloat16)
+    _check_prefixes(q, k, v, {kk: (out, idx)}, BF16_TOL)
