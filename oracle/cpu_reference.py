@@ -1,11 +1,11 @@
 """The reference's CPU path, restated in torch (CPU) -- TEST INFRASTRUCTURE ONLY.
 
-Only ``bench.py``'s ``cpu_baseline`` leg imports this module: it times the
-reference's compositions of the attention core on the host's own cores, beside
-the GPU numbers, as the reference's CPU microbenchmark does
-(``scripts/microbenchmark_comm.py:117-125`` ``_time_cpu``, ``:236-264``
-``host_report``; ``scripts/run_microbenchmarks.sh:49-52`` warm-up 10, reps
-30, runs 5). Nothing in the product package imports it.
+``bench.py``'s ``cpu_baseline`` leg times the reference's compositions of
+the attention core with it on the host's own cores, beside the GPU numbers, as
+the reference's CPU microbenchmark does (``scripts/microbenchmark_comm.py:117-125``
+``_time_cpu``, ``:236-264`` ``host_report``; ``scripts/run_microbenchmarks.sh:49-52``
+warm-up 10, reps 30, runs 5); ``tests/test_oracle.py`` checks it against the
+pinned numpy oracle. Nothing in the product package imports it.
 
 Each function computes what the reference's torch composition computes, in
 this module's own code:

@@ -885,3 +885,28 @@ def test_entmax_pin_rejects_planted_mistakes():
 
     for mutant in (wrong_power, few_steps, softmax_instead):
         assert not pin_entmax(mutant), mutant.__name__
+
+
+def test_cpu_baseline_restatement_matches_oracle(golden):
+    """The torch-CPU compositions bench.py times as the CPU baseline compute
+    what the pinned numpy oracle computes (float64 inputs: 1e-12; Morton codes
+    and window peers bit-exact on the golden positions)."""
+    import cpu_reference as C
+    q, k, v = qkv(31, 3, 40, 16, F64)
+    t = [torch.from_numpy(x) for x in (q, k, v)]
+    for kk in (1, 2, 7):
+        got = C.topk_gather(*t, kk).numpy()
+        assert np.abs(got - O.topk_gather(q, k, v, kk)[0]).max() < 1e-12
+    assert np.abs(C.dense_unfused(*t).numpy() - O.dense_unfused(q, k, v)).max() < 1e-12
+    for name in ("m64", "m512", "mgrid"):
+        pos = golden[f"{name}_pos"]
+        for bits in (10, 16):
+            codes = C.morton_codes(torch.from_numpy(pos), bits).numpy()
+            assert np.array_equal(codes, O.morton_code(pos, bits))
+    pos = golden["m64_pos"]
+    B, N = pos.shape[:2]
+    q, k, v = qkv(32, B, N, 16, F64)
+    for kk in (1, 2, 5):
+        got = C.zorder(*(torch.from_numpy(x) for x in (q, k, v, pos)), kk, 16).numpy()
+        want, _ = O.zorder_attention(q, k, v, pos, kk, 16)
+        assert np.abs(got - want).max() < 1e-12
