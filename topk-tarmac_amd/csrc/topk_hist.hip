@@ -17,15 +17,20 @@
 //  2. histogram: kHistBins bins spanning [min, max] of a query's scores,
 //     counted with LDS atomics; a scan from the top finds the bin tb that
 //     holds the k-th largest.
-//  3. select: scores above tb's upper edge (plus the binning's rounding
-//     slack) are kept, scores below its lower edge are dropped; the scores in
-//     between -- bin tb, every tie at the k-th score among them -- go to
-//     per-lane lists and are ranked by (score desc, index asc); the best
-//     k - |kept| join.
+//  3. select, in the pass that aggregates: scores above tb's upper edge (plus
+//     the binning's rounding slack) are kept, scores below its lower edge are
+//     dropped; the scores in between -- bin tb, every tie at the k-th score
+//     among them -- are written to per-lane LDS slots as the pass goes.
 //  4. aggregate: P = 2^((s - max) log2 e) on the kept keys (0 elsewhere) in
-//     the fp32 MFMA P V product of the dense kernel, plus the joining keys'
-//     value rows; out = acc / sum.
-//  fallback: a wave with a query whose band could overflow the lists (ties,
+//     the fp32 MFMA P V product of the dense kernel.
+//  5. rank the band: the wave's band entries form one flat list (query-major),
+//     each as a 64-bit key (ordered score, descending | key index); every lane
+//     ranks one or more entries against its query's entries, and a query's
+//     best k - |kept| join; their value rows are added by the query's lanes.
+//  6. indices (optional): kept and joining keys set bits of a per-query mask;
+//     the wave's 16 rows of ascending indices are staged in LDS and stored as
+//     one contiguous block.
+//  fallback: a wave with a query whose band could overflow the slots (ties,
 //     rows of nearly equal scores) or with non-finite inputs or scores takes
 //     the queries one at a time over the whole wave: the k-th largest 32-bit
 //     ordered key by bisection, ties to the lower index.
@@ -40,12 +45,11 @@ namespace tarmac {
 namespace {
 
 constexpr int kHistBins = 128;   // per query
-constexpr int kHistLane = 16;    // listed keys per lane (fast path); 4 lanes per query
+constexpr int kHistSlots = 16;   // band score slots per lane (fast path: fewer entries)
 constexpr int kHistWaves = 4;    // 16-query waves per workgroup
 constexpr int kHistSel = 16;     // selection bitmask words per query (N <= 512)
 constexpr int kHistQWords = kHistBins + kHistSel;  // scratch words per query
 constexpr unsigned kHistMaskedBits = 0xffffffffu;  // a NaN; its ordered key is INT_MIN
-constexpr unsigned kListUpper = 0x80000000u;       // listed key lies in a bin above tb
 
 __device__ __forceinline__ float masked_score() { return __uint_as_float(kHistMaskedBits); }
 
@@ -67,6 +71,12 @@ __device__ __forceinline__ unsigned cvt_u32(float y) {
 // kHistBins (such rows also fail the fast path's margin test).
 __device__ __forceinline__ unsigned bin_of(float x, float inv, float c0) {
   return min(cvt_u32(fmaf(x, inv, c0)), static_cast<unsigned>(kHistBins - 1));
+}
+
+// x of lane l - N of the same 16-lane row (0 in the row's first N lanes).
+template <int N>
+__device__ __forceinline__ int dpp_shr(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, 0x110 + N, 0xF, 0xF, false);
 }
 
 // x, as a value the compiler cannot relate to other expressions: key
@@ -434,7 +444,7 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   const float hi_edge = inv > 0.f ? fmaf(static_cast<float>(tb + 1), w, mn) : mx;
   const float slack = 0x1p-18f * (fabsf(mx) + fabsf(mn) + range);
   const float hiT = hi_edge + slack, loT = lo_edge - slack;
-  const bool fast = finite_in && finite_s && cand_bound <= 4 * kHistLane &&
+  const bool fast = finite_in && finite_s && cand_bound <= 4 * kHistSlots &&
                     (inv == 0.f || slack < 0.5f * w);
 
   if (!__all(fast)) {
@@ -444,7 +454,7 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
     return;
   }
 
-  // ---- kept keys into the product; the band between the edges flagged ------
+  // ---- kept keys into the product; the band onto per-lane lists -----------
   // exponents: one fma while the maximum is small enough for its rounding in
   // -m log2(e) to be negligible, else subtract first (exact near the maximum)
   const bool small = __all(fabsf(mx) <= 16.f);
@@ -455,13 +465,30 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   float lsum = 0.f;
   constexpr int NB32 = (NT * 4 + 31) / 32;
-  uint32_t band[NB32];     // bit (4 t + r) % 32 of word (4 t + r) / 32: in the band
-  uint32_t kept[NB32];     // the same for kept keys (retained indices only)
+  uint32_t kept[NB32];  // bit (4 t + r) % 32 of word (4 t + r) / 32: kept key
 #pragma unroll
-  for (int i = 0; i < NB32; ++i) band[i] = kept[i] = 0u;
+  for (int i = 0; i < NB32; ++i) kept[i] = 0u;
+  uint32_t band[NB32];  // the same for band keys
+#pragma unroll
+  for (int i = 0; i < NB32; ++i) band[i] = 0u;
+  // Band scores go to this lane's kHistSlots slots, in key order (the keys
+  // come back from the band bits): every score is written to slot nl mod
+  // kHistSlots and only band scores advance nl, so no branch is needed
+  // (slots past nl are stale; a lane holds at most kHistSlots - 1 band
+  // scores on the fast path). The histogram words the slots reuse are no
+  // longer read.
+  float* slots = reinterpret_cast<float*>(qscr) + kHistSlots * grp;
+  unsigned nl = 0u;
+  wave_lds_sync();
   auto pv_pass = [&](auto exp_small) {
+    const float* vrow = Vt + col * LDV + 4 * grp;
+    f32x4 vnext = *reinterpret_cast<const f32x4*>(vrow);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
+      // this tile's value fragment was read a tile ahead: the MFMA below does
+      // not wait on the slot writes
+      const f32x4 vv = vnext;
+      if (t + 1 < NT) vnext = *reinterpret_cast<const f32x4*>(vrow + 16 * (t + 1));
       float p[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -472,10 +499,12 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
         p[r] = fast_exp2(keep ? y : -INFINITY);
         lsum += p[r];
         const int bit = (4 * t + r) & 31, word = (4 * t + r) >> 5;
-        band[word] |= static_cast<uint32_t>(!keep && x >= loT) << bit;
-        if (WITH_IDX) kept[word] |= static_cast<uint32_t>(keep) << bit;
+        const bool inband = !keep && x >= loT;
+        kept[word] |= static_cast<uint32_t>(keep) << bit;
+        band[word] |= static_cast<uint32_t>(inband) << bit;
+        slots[nl & (kHistSlots - 1)] = x;
+        nl += inband ? 1u : 0u;
       }
-      const f32x4 vv = *reinterpret_cast<const f32x4*>(Vt + col * LDV + 16 * t + 4 * grp);
 #pragma unroll
       for (int u = 0; u < 4; ++u) acc = mfma_f32_16x16x4(vv[u], p[u], acc);
       __builtin_amdgcn_sched_barrier(0);
@@ -485,124 +514,125 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   else pv_pass(std::false_type{});
 #pragma unroll
   for (int i = 0; i < NB32; ++i) {  // materialised here: the scores die with the pass
-    band[i] = static_cast<uint32_t>(opaque(static_cast<int>(band[i])));
     kept[i] = static_cast<uint32_t>(opaque(static_cast<int>(kept[i])));
+    band[i] = static_cast<uint32_t>(opaque(static_cast<int>(band[i])));
   }
-
-  // ---- the band onto per-lane lists (its scores recomputed canonically) -----
-  // lane row g of a query lists at words [16 g, 16 g + 16): key, bit 31 set
-  // when its bin lies above tb; its score at [64 + 16 g, ...)
-  unsigned nl = 0u;
-  {
-    float qs[16];
-    ld_f32<16>(qs, Q + boff + static_cast<size_t>(qi) * D);
-#pragma unroll
-    for (int c = 0; c < 16; ++c) qs[c] *= scale;
-#pragma unroll
-    for (int w = 0; w < NB32; ++w) {
-      uint32_t bits = band[w];
-      while (bits) {  // a few keys per lane
-        const int pos = 32 * w + __builtin_ctz(bits);
-        bits &= bits - 1u;
-        const int j = 16 * (pos >> 2) + 4 * grp + (pos & 3);
-        if (nl < kHistLane) {
-          const float c = canon_row16(qs, Kb + static_cast<size_t>(j) * D);  // equals s[t][r]
-          const bool upper = static_cast<int>(bin_of(c, inv, c0)) > tb;
-          qscr[kHistLane * grp + nl] = static_cast<unsigned>(j) | (upper ? kListUpper : 0u);
-          qscr[4 * kHistLane + kHistLane * grp + nl] = __float_as_uint(c);
-        }
-        ++nl;
-      }
-    }
-  }
-  if (!__all(nl <= kHistLane)) {  // a lane's share of the band overflowed: start over exactly
+  if (!__all(nl < static_cast<unsigned>(kHistSlots))) {  // a lane's share overflowed
     hist_fallback_wave<NT>(Q + boff, Kb, V + boff, O + boff,
                            Idx ? Idx + static_cast<size_t>(b) * N * topk : nullptr, N, q0, topk,
                            scale, lane);
     return;
   }
-  wave_lds_sync();
 
-  // ---- rank the listed keys ------------------------------------------------
-  // Lists are read four entries at a time (one 16-byte LDS read for keys,
-  // one for scores); loop bounds are the wave's maxima, entries past a list's
-  // end are masked.
+  // ---- rank the band over the wave's flat list ----------------------------
+  // Entry e of the wave's list (at most 512) sits in the upper half of query
+  // (e / 32)'s words; a query's entries are contiguous (its four lane rows in
+  // order), as (ordered key of the score, descending | key index, query). A
+  // query takes its `need` best band entries: k minus the keys kept by the
+  // pass.
+  unsigned nk = 0u;
+#pragma unroll
+  for (int i = 0; i < NB32; ++i) nk += __builtin_popcount(kept[i]);
+  const unsigned need = kq - rows_sum(nk);
   uint32_t nls[4];
-  gather_rows(nl, nls);  // list lengths of the query's four lane rows
-  const unsigned nlq = max(max(nls[0], nls[1]), max(nls[2], nls[3]));
-  const int chunks = static_cast<int>(wave_max_rows(static_cast<float>((nlq + 3u) >> 2)));
-  const uint4* lj4 = reinterpret_cast<const uint4*>(qscr);                   // keys
-  const f32x4* lc4 = reinterpret_cast<const f32x4*>(qscr + 4 * kHistLane);  // scores
-  unsigned upper = 0u;
-  for (int u = 0; u < chunks; ++u) {
-    const uint4 w = lj4[4 * grp + u];
-    const unsigned wv[4] = {w.x, w.y, w.z, w.w};
+  gather_rows(nl, nls);
+  const unsigned cnt = nls[0] + nls[1] + nls[2] + nls[3];
+  unsigned rowoff = 0u;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) upper += (4u * u + e < nl) ? (wv[e] >> 31) : 0u;
+  for (int g = 0; g < 4; ++g) rowoff += g < grp ? nls[g] : 0u;
+  unsigned incl = cnt;  // prefix over the 16 queries of a row (the four rows agree)
+  incl += static_cast<unsigned>(dpp_shr<1>(static_cast<int>(incl)));
+  incl += static_cast<unsigned>(dpp_shr<2>(static_cast<int>(incl)));
+  incl += static_cast<unsigned>(dpp_shr<4>(static_cast<int>(incl)));
+  incl += static_cast<unsigned>(dpp_shr<8>(static_cast<int>(incl)));
+  const unsigned qoff = incl - cnt;
+  const unsigned total = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(incl), 15));
+  if (total > 512u) {  // beyond the flat list's room (16 x 32 entries)
+    hist_fallback_wave<NT>(Q + boff, Kb, V + boff, O + boff,
+                           Idx ? Idx + static_cast<size_t>(b) * N * topk : nullptr, N, q0, topk,
+                           scale, lane);
+    return;
   }
-  upper = rows_sum(upper);
-  const unsigned need = kq - (above_tb - upper);  // 1 <= need <= listed
-  uint32_t taken = 0u;  // bit i: own entry i joins
-  for (int u = 0; u < chunks; ++u) {
-    const uint4 ow = lj4[4 * grp + u];
-    const f32x4 oc = lc4[4 * grp + u];
-    const unsigned oj[4] = {ow.x & 0xffffu, ow.y & 0xffffu, ow.z & 0xffffu, ow.w & 0xffffu};
-    unsigned rank[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-      for (int v = 0; v < chunks; ++v) {
-        const uint4 w = lj4[4 * g + v];
-        const f32x4 c2 = lc4[4 * g + v];
-        const unsigned j2[4] = {w.x & 0xffffu, w.y & 0xffffu, w.z & 0xffffu, w.w & 0xffffu};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bool in = 4u * v + e < nls[g];
-#pragma unroll
-          for (int o = 0; o < 4; ++o)
-            rank[o] += (in && (c2[e] > oc[o] || (c2[e] == oc[o] && j2[e] < oj[o]))) ? 1u : 0u;
+  unsigned* wscr = reinterpret_cast<unsigned*>(region_a) + kHistWaves * 16 * kHistQWords + wave * 32;
+  unsigned* wreg = reinterpret_cast<unsigned*>(region_a) + static_cast<size_t>(wave) * 16 * kHistQWords;
+  auto flat = [&](unsigned e) -> uint2* {  // e < 512
+    return reinterpret_cast<uint2*>(wreg + (e >> 5) * kHistQWords + 64) + (e & 31u);
+  };
+  if (grp == 0) wscr[col] = qoff | (cnt << 10) | (need << 20);
+  const unsigned mnl = static_cast<unsigned>(wave_max_rows(static_cast<float>(nl)));
+  {
+    // slot i holds the score of the i-th band key in key order
+    uint64_t blo = band[0], bhi = 0u;
+    if constexpr (NB32 > 1) blo |= static_cast<uint64_t>(band[1]) << 32;
+    if constexpr (NB32 > 2) bhi = band[2];
+    if constexpr (NB32 > 3) bhi |= static_cast<uint64_t>(band[3]) << 32;
+    for (unsigned i = 0; i < mnl; ++i) {
+      if (i < nl) {
+        unsigned pos;
+        if (blo != 0u) {
+          pos = static_cast<unsigned>(__builtin_ctzll(blo));
+          blo &= blo - 1u;
+        } else {
+          pos = 64u + static_cast<unsigned>(__builtin_ctzll(bhi));
+          bhi &= bhi - 1u;
         }
+        const unsigned j = 16u * (pos >> 2) + 4u * grp + (pos & 3u);
+        const uint32_t u = __float_as_uint(slots[i] + 0.f);  // -0 -> +0
+        const uint32_t m = static_cast<uint32_t>(static_cast<int>(u) >> 31);
+        *flat(qoff + rowoff + i) = make_uint2((u ^ ~m) & (m | 0x7fffffffu), j | (col << 16));
       }
-#pragma unroll
-    for (int o = 0; o < 4; ++o)
-      taken |= (4u * u + o < nl && rank[o] < need) ? (1u << (4 * u + o)) : 0u;
+    }
+  }
+  const unsigned qcmax = static_cast<unsigned>(wave_max_rows(static_cast<float>(cnt)));
+  wave_lds_sync();
+  const int rounds = static_cast<int>((total + 63u) >> 6);
+  uint32_t tk = 0u;  // bit h: entry lane + 64 h joins
+  for (int h = 0; h < rounds; ++h) {
+    const unsigned e = static_cast<unsigned>(lane + 64 * h);
+    if (e < total) {
+      const uint2 me = *flat(e);
+      const unsigned info = wscr[(me.y >> 16) & 15u];
+      const unsigned qs = info & 1023u, qc = (info >> 10) & 1023u, qn = info >> 20;
+      const uint64_t mk = (static_cast<uint64_t>(me.x) << 32) | me.y;
+      unsigned rank = 0u;
+      for (unsigned i = 0; i < qcmax; ++i) {
+        const uint2 o = *flat(min(qs + i, 511u));
+        const uint64_t ok = (static_cast<uint64_t>(o.x) << 32) | o.y;
+        rank += (i < qc && ok < mk) ? 1u : 0u;
+      }
+      tk |= (rank < qn ? 1u : 0u) << h;
+    }
   }
   wave_lds_sync();
-  // joining entries carry their weight in the score slot, the others 0
-  for (int u = 0; u < chunks; ++u) {
-    f32x4 c = lc4[4 * grp + u];
-#pragma unroll
-    for (int o = 0; o < 4; ++o) {
-      const float e = expw(c[o]);
-      c[o] = (taken >> (4 * u + o)) & 1u ? e : 0.f;
+  // joining entries are flagged (bit 31 of the key word; key indices are
+  // below 2^16) and, with indices, marked in their query's selection bits
+  for (int h = 0; h < rounds; ++h) {
+    const unsigned e = static_cast<unsigned>(lane + 64 * h);
+    if (e < total && ((tk >> h) & 1u)) {
+      uint2* f = flat(e);
+      const unsigned y = f->y;
+      f->y = y | 0x80000000u;
+      if constexpr (WITH_IDX) {
+        const unsigned q = (y >> 16) & 15u, j = y & 0xffffu;
+        atomicOr(wreg + q * kHistQWords + kHistBins + (j >> 5), 1u << (j & 31u));
+      }
     }
-    reinterpret_cast<f32x4*>(qscr + 4 * kHistLane)[4 * grp + u] = c;
   }
   wave_lds_sync();
 
   // ---- the joining keys' value rows (from the transposed copy in LDS) ------
+  // each query's four lanes walk its entries: weights from the query's own
+  // maximum
+  for (unsigned i = 0; i < qcmax; ++i) {
+    if (i < cnt) {
+      const uint2 o = *flat(qoff + i);
+      const uint32_t m = static_cast<uint32_t>(static_cast<int>(o.x) >> 31);
+      const float x = __uint_as_float(m ? o.x : (~o.x & 0x7fffffffu));  // the score back
+      const float pw = (o.y >> 31) ? expw(x) : 0.f;
+      const unsigned j = o.y & 0xffffu;
 #pragma unroll
-  for (int g = 0; g < 4; ++g)
-    for (int v = 0; v < chunks; ++v) {
-      const uint4 w = lj4[4 * g + v];
-      const f32x4 pw = lc4[4 * g + v];
-      const unsigned jj[4] = {w.x & 0xffffu, w.y & 0xffffu, w.z & 0xffffu, w.w & 0xffffu};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bool in = 4u * v + e < nls[g];
-        const float p = in ? pw[e] : 0.f;
-        const unsigned j = in ? jj[e] : 0u;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = fmaf(p, Vt[(4 * grp + r) * LDV + j], acc[r]);
-        lsum += grp == 0 ? p : 0.f;
-      }
-    }
-  if constexpr (WITH_IDX) {  // the owners mark their joining entries
-    for (int u = 0; u < chunks; ++u) {
-      const uint4 w = lj4[4 * grp + u];
-      const unsigned jj[4] = {w.x & 0xffffu, w.y & 0xffffu, w.z & 0xffffu, w.w & 0xffffu};
-#pragma unroll
-      for (int o = 0; o < 4; ++o)
-        if ((taken >> (4 * u + o)) & 1u) atomicOr(selw + (jj[o] >> 5), 1u << (jj[o] & 31));
+      for (int r = 0; r < 4; ++r) acc[r] = fmaf(pw, Vt[(4 * grp + r) * LDV + j], acc[r]);
+      lsum += grp == 0 ? pw : 0.f;
     }
   }
 
@@ -625,20 +655,75 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
     if (nib) atomicOr(selw + (t >> 1), nib << (16 * (t & 1) + 4 * grp));
   }
   wave_lds_sync();
-  if (!live) return;
   constexpr int NW = NP / 32;
   uint32_t wv[NW];
 #pragma unroll
   for (int i = 0; i < NW; ++i) wv[i] = selw[i];
+  const int nq = min(16, N - q0);
+  int32_t* dst = Idx + (static_cast<size_t>(b) * N + q0) * topk;
+  if (topk <= kHistQWords) {
+    // the wave's 16 x topk indices are one contiguous block: staged in the
+    // wave's words (free once the bitmasks are read), then stored with
+    // consecutive lanes on consecutive addresses
+    wave_lds_sync();
+    // lane row g expands words g, g + 4, ... of its query, all lanes at once,
+    // two keys per step
+    unsigned pre[NW];  // selected keys in the words before word i
+    {
+      unsigned run = 0u;
+#pragma unroll
+      for (int i = 0; i < NW; ++i) {
+        pre[i] = run;
+        run += __builtin_popcount(wv[i]);
+      }
+    }
+    unsigned* orow = wreg + col * topk;
+#pragma unroll
+    for (int k = 0; k < (NW + 3) / 4; ++k) {
+      uint32_t bits = 0u;
+      unsigned pos = 0u;
+#pragma unroll
+      for (int i = 4 * k; i < 4 * k + 4 && i < NW; ++i)
+        if ((i & 3) == grp) {
+          bits = wv[i];
+          pos = pre[i];
+        }
+      if (!live) bits = 0u;
+      const unsigned wbase = 32u * static_cast<unsigned>(grp + 4 * k);
+      while (bits) {
+        const unsigned b1 = static_cast<unsigned>(__builtin_ctz(bits));
+        bits &= bits - 1u;
+        orow[pos] = wbase + b1;
+        if (bits) {
+          orow[pos + 1] = wbase + static_cast<unsigned>(__builtin_ctz(bits));
+          bits &= bits - 1u;
+          pos += 2u;
+        } else {
+          pos += 1u;
+        }
+      }
+    }
+    wave_lds_sync();
+    const int count = nq * topk;
+    if ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0u && (count & 3) == 0) {
+      const uint4* src4 = reinterpret_cast<const uint4*>(wreg);
+      uint4* dst4 = reinterpret_cast<uint4*>(dst);
+      for (int e = lane; e < (count >> 2); e += 64) dst4[e] = src4[e];
+    } else {
+      for (int e = lane; e < count; e += 64) dst[e] = static_cast<int32_t>(wreg[e]);
+    }
+    return;
+  }
+  if (!live) return;
   unsigned base = 0u;
-  int32_t* dst = Idx + (static_cast<size_t>(b) * N + qi) * topk;
+  int32_t* qdst = dst + col * topk;
 #pragma unroll
   for (int i = 0; i < NW; ++i) {
     if ((i & 3) == grp) {
       uint32_t bits = wv[i];
       unsigned pos = base;
       while (bits) {
-        if (pos < static_cast<unsigned>(topk)) dst[pos] = 32 * i + __builtin_ctz(bits);
+        if (pos < static_cast<unsigned>(topk)) qdst[pos] = 32 * i + __builtin_ctz(bits);
         ++pos;
         bits &= bits - 1u;
       }
