@@ -547,7 +547,7 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   incl += static_cast<unsigned>(dpp_shr<8>(static_cast<int>(incl)));
   const unsigned qoff = incl - cnt;
   const unsigned total = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(incl), 15));
-  if (total > 512u) {  // beyond the flat list's room (16 x 32 entries)
+  if (total > 512u || !__all(need <= 32u)) {  // beyond the flat list's (16 x 32) or a join list's (32) room
     hist_fallback_wave<NT>(Q + boff, Kb, V + boff, O + boff,
                            Idx ? Idx + static_cast<size_t>(b) * N * topk : nullptr, N, q0, topk,
                            scale, lane);
@@ -584,14 +584,18 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
     }
   }
   const unsigned qcmax = static_cast<unsigned>(wave_max_rows(static_cast<float>(cnt)));
+  const unsigned needmax = static_cast<unsigned>(wave_max_rows(static_cast<float>(need)));
   wave_lds_sync();
   const int rounds = static_cast<int>((total + 63u) >> 6);
-  uint32_t tk = 0u;  // bit h: entry lane + 64 h joins
+  // A joining entry of rank r goes to slot r of its query's join list (the
+  // query's first 64 words, free once the slots are flattened) and, with
+  // indices, sets its bit in the query's selection mask.
   for (int h = 0; h < rounds; ++h) {
     const unsigned e = static_cast<unsigned>(lane + 64 * h);
     if (e < total) {
       const uint2 me = *flat(e);
-      const unsigned info = wscr[(me.y >> 16) & 15u];
+      const unsigned q = (me.y >> 16) & 15u;
+      const unsigned info = wscr[q];
       const unsigned qs = info & 1023u, qc = (info >> 10) & 1023u, qn = info >> 20;
       const uint64_t mk = (static_cast<uint64_t>(me.x) << 32) | me.y;
       unsigned rank = 0u;
@@ -600,38 +604,27 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
         const uint64_t ok = (static_cast<uint64_t>(o.x) << 32) | o.y;
         rank += (i < qc && ok < mk) ? 1u : 0u;
       }
-      tk |= (rank < qn ? 1u : 0u) << h;
-    }
-  }
-  wave_lds_sync();
-  // joining entries are flagged (bit 31 of the key word; key indices are
-  // below 2^16) and, with indices, marked in their query's selection bits
-  for (int h = 0; h < rounds; ++h) {
-    const unsigned e = static_cast<unsigned>(lane + 64 * h);
-    if (e < total && ((tk >> h) & 1u)) {
-      uint2* f = flat(e);
-      const unsigned y = f->y;
-      f->y = y | 0x80000000u;
-      if constexpr (WITH_IDX) {
-        const unsigned q = (y >> 16) & 15u, j = y & 0xffffu;
-        atomicOr(wreg + q * kHistQWords + kHistBins + (j >> 5), 1u << (j & 31u));
+      if (rank < qn) {
+        const unsigned j = me.y & 0xffffu;
+        reinterpret_cast<uint2*>(wreg + q * kHistQWords)[rank] = make_uint2(me.x, j);
+        if constexpr (WITH_IDX)
+          atomicOr(wreg + q * kHistQWords + kHistBins + (j >> 5), 1u << (j & 31u));
       }
     }
   }
   wave_lds_sync();
 
   // ---- the joining keys' value rows (from the transposed copy in LDS) ------
-  // each query's four lanes walk its entries: weights from the query's own
+  // each query's four lanes walk its join list: weights from the query's own
   // maximum
-  for (unsigned i = 0; i < qcmax; ++i) {
-    if (i < cnt) {
-      const uint2 o = *flat(qoff + i);
+  const uint2* jl = reinterpret_cast<const uint2*>(qscr);
+  for (unsigned i = 0; i < needmax; ++i) {
+    if (i < need) {
+      const uint2 o = jl[i];
       const uint32_t m = static_cast<uint32_t>(static_cast<int>(o.x) >> 31);
-      const float x = __uint_as_float(m ? o.x : (~o.x & 0x7fffffffu));  // the score back
-      const float pw = (o.y >> 31) ? expw(x) : 0.f;
-      const unsigned j = o.y & 0xffffu;
+      const float pw = expw(__uint_as_float(m ? o.x : (~o.x & 0x7fffffffu)));  // the score back
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = fmaf(pw, Vt[(4 * grp + r) * LDV + j], acc[r]);
+      for (int r = 0; r < 4; ++r) acc[r] = fmaf(pw, Vt[(4 * grp + r) * LDV + o.y], acc[r]);
       lsum += grp == 0 ? pw : 0.f;
     }
   }
@@ -647,18 +640,17 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   }
   if constexpr (!WITH_IDX) return;
   // ---- retained indices, ascending -----------------------------------------
-  // the kept flags of tiles 2w and 2w + 1 fill word w: lane row g holds bits
-  // 4 g .. 4 g + 3 of each 16-key half
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const uint32_t nib = (kept[(4 * t) >> 5] >> ((4 * t) & 31)) & 0xfu;
-    if (nib) atomicOr(selw + (t >> 1), nib << (16 * (t & 1) + 4 * grp));
-  }
-  wave_lds_sync();
+  // selection word w (keys 32 w .. 32 w + 31) = the kept flags of tiles 2 w
+  // and 2 w + 1 (lane row g holds bits 4 g .. 4 g + 3 of each 16-key half;
+  // the rows' disjoint bits meet in a sum) plus the joining keys' marks
   constexpr int NW = NP / 32;
   uint32_t wv[NW];
 #pragma unroll
-  for (int i = 0; i < NW; ++i) wv[i] = selw[i];
+  for (int w = 0; w < NW; ++w) {
+    const uint32_t n0 = (kept[(8 * w) >> 5] >> ((8 * w) & 31)) & 0xfu;
+    const uint32_t n1 = (kept[(8 * w + 4) >> 5] >> ((8 * w + 4) & 31)) & 0xfu;
+    wv[w] = rows_sum((n0 << (4 * grp)) | (n1 << (16 + 4 * grp))) | selw[w];
+  }
   const int nq = min(16, N - q0);
   int32_t* dst = Idx + (static_cast<size_t>(b) * N + q0) * topk;
   if (topk <= kHistQWords) {
