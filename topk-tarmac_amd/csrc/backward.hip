@@ -23,6 +23,11 @@
 // fp32 atomic adds in no fixed order: per-entry lists in LDS (gather form),
 // accumulators in LDS, or global memory, whichever fits.
 //
+// In the mask kernel each query's pass is a single sweep over its set (dq
+// from the rescaled sums of e_j dw_j k_j and e_j k_j, see
+// fixedset_bwd_row_mask); the per-key pass recomputes each entry from the
+// query's statistics.
+//
 // Dense, self pair excluded: P = softmax(c Q K^T), D_i = dO_i.O_i,
 //   dS = P o (dO V^T - D 1^T),  dQ = c dS K,  dK = c dS^T Q,  dV = P^T dO.
 // Pass 1 (per query, quad of lanes) forms the row statistics, dQ, and stores
@@ -397,6 +402,81 @@ struct MaskSink {
   }
 };
 
+// One query (a quad of lanes) in one pass over its set, for the mask form:
+// with e_j = 2^(s_j - m) under a running maximum m,
+//   dq = sum_j w_j (dw_j - D) k_j = (sum_j e_j dw_j k_j - D sum_j e_j k_j) / l,
+// l = sum_j e_j, D = sum_j e_j dw_j / l, all four sums rescaled as m grows;
+// each valid peer sets its bit in the mask (sink). Returns the statistics the
+// per-key pass recomputes the entries from.
+template <int D, typename I>
+__device__ __forceinline__ RowStats fixedset_bwd_row_mask(const float* __restrict__ qrow,
+                                                      const float* __restrict__ grow,
+                                                      const float* Kb, const float* Vb,
+                                                      const I* __restrict__ ir,
+                                                      float* __restrict__ dqrow, int N, int kk,
+                                                      float scale, int sub, MaskSink sink) {
+  constexpr int E = D / 4;
+  constexpr int U = E <= 4 ? 8 : (E <= 8 ? 4 : 1);
+  const float c2 = scale * kLog2eF;  // scores in the exp2 domain
+  float q[E], g[E];
+  ld_f32<E>(q, qrow + sub * E);
+  ld_f32<E>(g, grow + sub * E);
+  float m = -INFINITY, l = 0.f, a = 0.f, ak[E], bk[E];
+#pragma unroll
+  for (int c = 0; c < E; ++c) ak[c] = bk[c] = 0.f;
+  bool bad = false;
+  for (int j0 = 0; j0 < kk; j0 += U) {
+    int p[U];
+    float kr[U][E], vr[U][E], sc[U], dw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) p[u] = j0 + u < kk ? static_cast<int>(ir[j0 + u]) : 0;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int pc = min(max(p[u], 0), N - 1);
+      ld_f32<E>(kr[u], Kb + static_cast<size_t>(pc) * D + sub * E);
+      ld_f32<E>(vr[u], Vb + static_cast<size_t>(pc) * D + sub * E);
+    }
+    float mb = m;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      sc[u] = j0 + u < kk ? quad_dot<E>(q, kr[u]) * c2 : -INFINITY;
+      dw[u] = quad_dot<E>(g, vr[u]);
+      bad |= j0 + u < kk && ((p[u] < 0) | (p[u] >= N));
+      mb = fmaxf(mb, sc[u]);
+    }
+    const float alpha = m == -INFINITY ? 0.f : fast_exp2(m - mb);
+    l *= alpha;
+    a *= alpha;
+#pragma unroll
+    for (int c = 0; c < E; ++c) {
+      ak[c] *= alpha;
+      bk[c] *= alpha;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float e = fast_exp2(sc[u] - mb);  // 0 for the -inf padding
+      const float ed = e * dw[u];
+      l += e;
+      a += ed;
+#pragma unroll
+      for (int c = 0; c < E; ++c) {
+        ak[c] = fmaf(ed, kr[u][c], ak[c]);
+        bk[c] = fmaf(e, kr[u][c], bk[c]);
+      }
+      if (j0 + u < kk && p[u] >= 0 && p[u] < N) sink(j0 + u, p[u], q, g, 0.f, 0.f);
+    }
+    m = mb;
+  }
+  const float inv_l = 1.f / l;
+  const float Dq = a * inv_l;
+  float dq[E];
+#pragma unroll
+  for (int c = 0; c < E; ++c)
+    dq[c] = bad ? __int_as_float(0x7fc00000) : fmaf(-Dq, bk[c], ak[c]) * inv_l * scale;
+  st_f32<E>(dqrow + sub * E, dq);
+  return RowStats{m, inv_l, Dq};
+}
+
 size_t fixedset_mask_lds_bytes(int N, int D, bool stage) {
   const size_t words = (static_cast<size_t>(N) + 31) / 32;
   return (stage ? 8 * static_cast<size_t>(N) * D : 0) + 16 * static_cast<size_t>(N) +
@@ -439,9 +519,9 @@ fixedset_bwd_mask_kernel(const float* __restrict__ Q, const float* __restrict__ 
     const int i = i0 + (tid >> 2);
     if (i < N) {  // whole quads agree
       const size_t row = static_cast<size_t>(b) * N + i;
-      const RowStats r = fixedset_bwd_row<D, I>(Q + row * D, dO + row * D, Kb, Vb, Idx + row * kk,
-                                                dQ + row * D, N, kk, scale, sub,
-                                                MaskSink{mask, repeated, words, i, sub});
+      const RowStats r = fixedset_bwd_row_mask<D, I>(Q + row * D, dO + row * D, Kb, Vb,
+                                                     Idx + row * kk, dQ + row * D, N, kk, scale,
+                                                     sub, MaskSink{mask, repeated, words, i, sub});
       if (sub == 0) stats[i] = make_float4(r.m, r.inv_l, r.dsum, 0.f);
     }
   }
