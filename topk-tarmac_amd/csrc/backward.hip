@@ -34,6 +34,7 @@
 // (logsumexp_i, D_i); pass 2 (per key) forms dK and dV from them. The other
 // side's rows stream through LDS in chunks.
 #include <algorithm>
+#include <type_traits>
 
 #include "frag.hpp"
 #include "tarmac_internal.hpp"
@@ -49,6 +50,17 @@ __device__ __forceinline__ float quad_dot(const float (&a)[E], const float (&b)[
 #pragma unroll
   for (int c = 0; c < E; ++c) s = fmaf(a[c], b[c], s);
   return quad_sum(s);
+}
+
+// dot over a group of G lanes (2 or 4, aligned): lane (l % G) holds E of the
+// d channels; the sum lands in all G lanes
+template <int G, int E>
+__device__ __forceinline__ float group_dot(const float (&a)[E], const float (&b)[E]) {
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < E; ++c) s = fmaf(a[c], b[c], s);
+  if constexpr (G == 2) return s + dpp_mov<kDppQuadXor1>(s);
+  else return quad_sum(s);
 }
 
 template <int E>
@@ -402,20 +414,20 @@ struct MaskSink {
   }
 };
 
-// One query (a quad of lanes) in one pass over its set, for the mask form:
+// One query (a group of G lanes) in one pass over its set, for the mask form:
 // with e_j = 2^(s_j - m) under a running maximum m,
 //   dq = sum_j w_j (dw_j - D) k_j = (sum_j e_j dw_j k_j - D sum_j e_j k_j) / l,
 // l = sum_j e_j, D = sum_j e_j dw_j / l, all four sums rescaled as m grows;
 // each valid peer sets its bit in the mask (sink). Returns the statistics the
 // per-key pass recomputes the entries from.
-template <int D, typename I>
+template <int D, int G, typename I>
 __device__ __forceinline__ RowStats fixedset_bwd_row_mask(const float* __restrict__ qrow,
                                                       const float* __restrict__ grow,
                                                       const float* Kb, const float* Vb,
                                                       const I* __restrict__ ir,
                                                       float* __restrict__ dqrow, int N, int kk,
                                                       float scale, int sub, MaskSink sink) {
-  constexpr int E = D / 4;
+  constexpr int E = D / G;
   constexpr int U = E <= 4 ? 8 : (E <= 8 ? 4 : 1);
   const float c2 = scale * kLog2eF;  // scores in the exp2 domain
   float q[E], g[E];
@@ -439,8 +451,8 @@ __device__ __forceinline__ RowStats fixedset_bwd_row_mask(const float* __restric
     float mb = m;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      sc[u] = j0 + u < kk ? quad_dot<E>(q, kr[u]) * c2 : -INFINITY;
-      dw[u] = quad_dot<E>(g, vr[u]);
+      sc[u] = j0 + u < kk ? group_dot<G, E>(q, kr[u]) * c2 : -INFINITY;
+      dw[u] = group_dot<G, E>(g, vr[u]);
       bad |= j0 + u < kk && ((p[u] < 0) | (p[u] >= N));
       mb = fmaxf(mb, sc[u]);
     }
@@ -483,14 +495,14 @@ size_t fixedset_mask_lds_bytes(int N, int D, bool stage) {
          4 * static_cast<size_t>(N) * words + 16;
 }
 
-template <int D, typename I, bool STAGE>
+template <int D, int G, typename I, bool STAGE>
 __global__ void __launch_bounds__(1024)
 fixedset_bwd_mask_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
                          const float* __restrict__ V, const float* __restrict__ dO,
                          const I* __restrict__ Idx, float* __restrict__ dQ,
                          float* __restrict__ dK, float* __restrict__ dV, int N, int kk,
                          float scale) {
-  constexpr int E = D / 4;
+  constexpr int E = D / G;  // channels per lane
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int nd = N * D, words = (N + 31) >> 5;
   float* rows = reinterpret_cast<float*>(smem_raw);  // STAGE: K, V, then Q, dO
@@ -499,7 +511,7 @@ fixedset_bwd_mask_kernel(const float* __restrict__ Q, const float* __restrict__ 
   int* repeated = reinterpret_cast<int*>(mask + static_cast<size_t>(N) * words);
   const int b = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
   const size_t boff = static_cast<size_t>(b) * nd;
-  const int sub = tid & 3, quads = nt >> 2;
+  const int sub = tid & (G - 1), groups = nt / G;
 
   for (int t = tid; t < N * words; t += nt) mask[t] = 0u;
   if (tid == 0) *repeated = 0;
@@ -514,12 +526,12 @@ fixedset_bwd_mask_kernel(const float* __restrict__ Q, const float* __restrict__ 
     Vb = rows + nd;
   }
   __syncthreads();
-  // 1. per query
-  for (int i0 = 0; i0 < N; i0 += quads) {
-    const int i = i0 + (tid >> 2);
-    if (i < N) {  // whole quads agree
+  // 1. per query (a group of G lanes)
+  for (int i0 = 0; i0 < N; i0 += groups) {
+    const int i = i0 + tid / G;
+    if (i < N) {  // whole groups agree
       const size_t row = static_cast<size_t>(b) * N + i;
-      const RowStats r = fixedset_bwd_row_mask<D, I>(Q + row * D, dO + row * D, Kb, Vb,
+      const RowStats r = fixedset_bwd_row_mask<D, G, I>(Q + row * D, dO + row * D, Kb, Vb,
                                                      Idx + row * kk, dQ + row * D, N, kk, scale,
                                                      sub, MaskSink{mask, repeated, words, i, sub});
       if (sub == 0) stats[i] = make_float4(r.m, r.inv_l, r.dsum, 0.f);
@@ -533,12 +545,13 @@ fixedset_bwd_mask_kernel(const float* __restrict__ Q, const float* __restrict__ 
       reinterpret_cast<float4*>(dV + boff)[t] = z;
     }
     __syncthreads();
+    const int sub4 = tid & 3, quads = nt >> 2;
     for (int i0 = 0; i0 < N; i0 += quads) {
       const int i = i0 + (tid >> 2);
       if (i < N) {
         const size_t row = static_cast<size_t>(b) * N + i;
         fixedset_bwd_row<D, I>(Q + row * D, dO + row * D, Kb, Vb, Idx + row * kk, dQ + row * D, N,
-                               kk, scale, sub, AtomicSink<D>{dK + boff, dV + boff, sub, scale});
+                               kk, scale, sub4, AtomicSink<D>{dK + boff, dV + boff, sub4, scale});
       }
     }
     return;
@@ -554,11 +567,11 @@ fixedset_bwd_mask_kernel(const float* __restrict__ Q, const float* __restrict__ 
     Gb = rows + nd;
     __syncthreads();
   }
-  // 2. per key
+  // 2. per key (a group of G lanes)
   const float c2 = scale * kLog2eF;
-  for (int p0 = 0; p0 < N; p0 += quads) {
-    const int p = p0 + (tid >> 2);
-    if (p >= N) break;  // whole quads agree; no barrier follows
+  for (int p0 = 0; p0 < N; p0 += groups) {
+    const int p = p0 + tid / G;
+    if (p >= N) break;  // whole groups agree; no barrier follows
     float kr[E], vr[E], dk[E], dv[E];
     ld_f32<E>(kr, Kx + boff + static_cast<size_t>(p) * D + sub * E);
     ld_f32<E>(vr, V + boff + static_cast<size_t>(p) * D + sub * E);
@@ -567,15 +580,15 @@ fixedset_bwd_mask_kernel(const float* __restrict__ Q, const float* __restrict__ 
     const unsigned* mrow = mask + static_cast<size_t>(p) * words;
     for (int w = 0; w < words; ++w) {
       unsigned bits = mrow[w];
-      while (bits) {  // the same bits on the quad's four lanes
+      while (bits) {  // the same bits on the group's lanes
         const int i = (w << 5) + __builtin_ctz(bits);
         bits &= bits - 1u;
         float q[E], g[E];
         ld_f32<E>(q, Qb + static_cast<size_t>(i) * D + sub * E);
         ld_f32<E>(g, Gb + static_cast<size_t>(i) * D + sub * E);
         const float4 st = stats[i];
-        const float sc = quad_dot<E>(q, kr) * c2;
-        const float dw = quad_dot<E>(g, vr);
+        const float sc = group_dot<G, E>(q, kr) * c2;
+        const float dw = group_dot<G, E>(g, vr);
         const float wgt = fast_exp2(sc - st.x) * st.y;
         const float ds = wgt * (dw - st.z);
 #pragma unroll
@@ -922,15 +935,28 @@ static hipError_t launch_fixedset_bwd_t(const FixedsetBwdArgs& a) {
   const size_t row_bytes = static_cast<size_t>(a.N) * D * sizeof(float);
   const size_t mask_stage = fixedset_mask_lds_bytes(a.N, D, true);
   const size_t mask_plain = fixedset_mask_lds_bytes(a.N, D, false);
-  if (mask_stage <= kMaskLdsBudget) {  // statistics, bitmask and the row's K, V fit LDS
-    hipLaunchKernelGGL((fixedset_bwd_mask_kernel<D, I, true>), dim3(a.B), dim3(1024), mask_stage,
-                       st, a.q, a.k, a.v, a.dout, idx, a.dq, a.dk, a.dv, a.N, a.kk, a.scale);
+  // lanes per query / key: pairs where quads would take a second, partly
+  // idle round and 512 pairs cover the row in one (256 < N <= 512), while a
+  // lane's share (D / 2 channels) stays within the register budget
+  // (B=256 N=384 k=95: 97 -> 90 us)
+  auto launch_mask = [&](auto g, auto stage, size_t lds) {
+    hipLaunchKernelGGL((fixedset_bwd_mask_kernel<D, decltype(g)::value, I, decltype(stage)::value>),
+                       dim3(a.B), dim3(1024), lds, st, a.q, a.k, a.v, a.dout, idx, a.dq, a.dk, a.dv,
+                       a.N, a.kk, a.scale);
     return hipGetLastError();
+  };
+  using G2 = std::integral_constant<int, 2>;
+  using G4 = std::integral_constant<int, 4>;
+  const bool pairs = D <= 16 && a.N > 256 && a.N <= 512;
+  if (mask_stage <= kMaskLdsBudget) {  // statistics, bitmask and the row's K, V fit LDS
+    if constexpr (D <= 16)
+      if (pairs) return launch_mask(G2{}, std::true_type{}, mask_stage);
+    return launch_mask(G4{}, std::true_type{}, mask_stage);
   }
   if (mask_plain <= kMaskLdsBudget) {  // statistics and bitmask fit LDS
-    hipLaunchKernelGGL((fixedset_bwd_mask_kernel<D, I, false>), dim3(a.B), dim3(1024), mask_plain,
-                       st, a.q, a.k, a.v, a.dout, idx, a.dq, a.dk, a.dv, a.N, a.kk, a.scale);
-    return hipGetLastError();
+    if constexpr (D <= 16)
+      if (pairs) return launch_mask(G2{}, std::false_type{}, mask_plain);
+    return launch_mask(G4{}, std::false_type{}, mask_plain);
   }
   const size_t gather_lds = fixedset_gather_lds_bytes(a.N, D, a.kk);
   if (gather_lds <= kBwdLdsBudget) {  // rows and per-entry lists fit LDS
