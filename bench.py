@@ -527,19 +527,24 @@ def main() -> int:
     # ---- forward + backward (the reference's module benchmark times both,
     # scripts/microbenchmark_comm.py:401): HIP backward kernels vs torch
     # autograd of the composed reference arm, eager, same weights
-    def fwd_bwd_time(fn, reps):
-        for _ in range(5):
-            fn()
+    def fwd_bwd_times(fns, reps):
+        """Minimum over reps of one forward + backward per arm, the arms
+        interleaved within every repetition (autograd needs its own graph per
+        call, so these run eagerly, with the grad mode on)."""
+        for fn in fns.values():
+            for _ in range(5):
+                fn()
         torch.cuda.synchronize()
-        best = float("inf")
+        best = {nm: float("inf") for nm in fns}
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         for _ in range(reps):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            fn()
-            e1.record()
-            e1.synchronize()
-            best = min(best, e0.elapsed_time(e1) * 1e3)
-        return round(best, 3)
+            for nm, fn in fns.items():
+                e0.record()
+                fn()
+                e1.record()
+                e1.synchronize()
+                best[nm] = min(best[nm], e0.elapsed_time(e1) * 1e3)
+        return {nm: round(t, 3) for nm, t in best.items()}
 
     fb_rows = {}
     for n in (6, 96, 384):
@@ -548,21 +553,20 @@ def main() -> int:
         x = torch.from_numpy(gx.standard_normal((256, n, 64)).astype(np.float32)).to(dev)
         x.requires_grad_(True)
         gout = torch.from_numpy(gx.standard_normal((256, n, 16)).astype(np.float32)).to(dev)
-        row = {}
+        fns = {}
         for mode in ("dense", "topk_gather"):
             cfg = MAPPOConfig(obs_dim=18, n_actions=5, n_agents=n, hidden=64, use_comm=True,
                               msg_dim=16, attn_mode=mode, topk=kk)
             m = AttentionComm(cfg, in_dim=64).to(dev)
             m.collect_info = False
-            row[f"hip_{mode}"] = fwd_bwd_time(lambda m=m: (m(x)[0] * gout).sum().backward(),
-                                              args.reps)
+            fns[f"hip_{mode}"] = lambda m=m: (m(x)[0] * gout).sum().backward()
             if mode == "topk_gather":
                 def torch_fb(m=m, kk=kk):
                     q_, k_, v_ = (t.contiguous() for t in m.qkv(x).chunk(3, dim=-1))
                     out_ = m.proj(F.gelu(reference_topk_attention(q_, k_, v_, kk)))
                     (out_ * gout).sum().backward()
-                row["torch_topk_gather"] = fwd_bwd_time(torch_fb, args.reps)
-        fb_rows[f"N{n}_k{kk}"] = row
+                fns["torch_topk_gather"] = torch_fb
+        fb_rows[f"N{n}_k{kk}"] = fwd_bwd_times(fns, args.reps)
     detail["module_fwd_bwd_B256_in64_msg16_us"] = fb_rows
 
     # ---- core backward kernels at the metric point (B=1024, N=256, d=16) ---
