@@ -159,6 +159,26 @@ def profile_one(args, q, k, v, dev) -> int:
         q7, k7, v7 = (torch.from_numpy(g.standard_normal((256, 384, D)).astype(np.float32)).to(dev)
                       for _ in range(3))
         fn = bound.topk(q7, k7, v7, 95)
+    elif name == "large95":
+        # the module benchmark's large-k core and its training pass, B=256,
+        # N=384, d=16, k=95: dense forward, top-k forward with and without
+        # indices, fixed-set backward on the retained sets, dense backward
+        from tarmac.kernels import dense_attention_backward, fixedset_attention_backward
+        g = np.random.default_rng(1234 + 7 * 384 + D)
+        q7, k7, v7, g7 = (torch.from_numpy(g.standard_normal((256, 384, D)).astype(np.float32))
+                          .to(dev) for _ in range(4))
+        fd = bound.dense(q7, k7, v7)
+        ft = bound.topk(q7, k7, v7, 95)
+        fi = bound.topk(q7, k7, v7, 95, with_idx=True)
+        fi()
+        out_d = fd()
+
+        def fn():
+            fd()
+            ft()
+            fi()
+            fixedset_attention_backward(q7, k7, v7, fi.idx, g7)
+            dense_attention_backward(q7, k7, v7, out_d, g7)
     elif name == "stream2":
         g = np.random.default_rng(4242)
         q4, k4, v4 = (torch.from_numpy(g.standard_normal((256, 1024, D)).astype(np.float32)).to(dev)
@@ -196,8 +216,8 @@ def main() -> int:
     ap.add_argument("--value-only", action="store_true",
                     help="time only the value kernel (for profiler runs)")
     ap.add_argument("--profile-kernel", default=None,
-                    choices=["dense", "dense_bf16", "dense_bf16_d16", "topk1", "topk95", "topk2", "topk4", "fixedset2", "zorder",
-                             "stream2"],
+                    choices=["dense", "dense_bf16", "dense_bf16_d16", "topk1", "topk95", "topk2", "topk4",
+                             "fixedset2", "zorder", "stream2", "large95"],
                     help="run only this kernel (headline shape; zorder/stream at their configs) "
                          "--warmup + --steps times, for profiler counter passes")
     ap.add_argument("--topk-filter", type=int, default=None, choices=[0, 1, 2, 3, 4],
