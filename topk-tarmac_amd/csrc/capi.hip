@@ -35,7 +35,7 @@ int hip_status(hipError_t e, const char* what) {
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 constexpr size_t kLdsBudget = 64 * 1024;
-constexpr size_t kBf16TopkLds = 40 * 1024;
+constexpr size_t kBf16TopkLds = 49 * 1024;
 constexpr int kZorderMaxN = 4096;  // agents per row the Morton selector sorts
 constexpr size_t kZorderLds = 160 * 1024;  // LDS per workgroup on gfx950
 
@@ -83,9 +83,9 @@ int topk_common(const void* q, const void* k, const void* v, void* out, int32_t*
   int kc;
   if (key_chunk <= 0) {
     kc = n64 < kmax ? n64 : kmax;
-    // bf16: keep the key copy within 40 KiB so four workgroups share a CU (a
-    // whole 512-key row at d = 64 would allow two, and measured 1.4x slower
-    // than 256-key chunks in the register-list kernel)
+    // bf16: keep the key copy within 49 KiB so three workgroups share a CU
+    // (a whole 512-key row at d = 64 would allow two; a whole 1024-key row
+    // at d = 16, 48 KiB of rows, runs 1.2x faster than 832-key chunks)
     if (dtype == tarmac::kBf16)
       while (kc > 64 && tarmac::topk_lds_bytes(dtype, d, kc) > kBf16TopkLds) kc -= 64;
   } else {
@@ -96,6 +96,9 @@ int topk_common(const void* q, const void* k, const void* v, void* out, int32_t*
                   fn, key_chunk, kmax, d);
     kc = key_chunk;
   }
+  // a chunk beyond the row is the resident row: LDS is sized for the row, not
+  // the chunk (a larger allocation only costs workgroups per CU)
+  if (kc > n64) kc = n64;
   tarmac::TopkArgs a{q, k, v, out, idx_out, B, N, d, topk, dtype, kc, inv_sqrt(d), stream};
   return hip_status(tarmac::run_topk(a), fn);
 }
