@@ -179,6 +179,19 @@ def profile_one(args, q, k, v, dev) -> int:
             fi()
             fixedset_attention_backward(q7, k7, v7, fi.idx, g7)
             dense_attention_backward(q7, k7, v7, out_d, g7)
+    elif name == "dense_small":
+        # the memory-bound end of the configs[1] sweep: fp32 dense at B=1024,
+        # d=16, N=32 and N=64 (one call of each per step)
+        fns = []
+        for n in (32, 64):
+            g = np.random.default_rng(1234 + 7 * n + D)
+            qs, ks, vs = (torch.from_numpy(g.standard_normal((1024, n, D)).astype(np.float32))
+                          .to(dev) for _ in range(3))
+            fns.append(bound.dense(qs, ks, vs))
+
+        def fn():
+            for f in fns:
+                f()
     elif name == "stream2":
         g = np.random.default_rng(4242)
         q4, k4, v4 = (torch.from_numpy(g.standard_normal((256, 1024, D)).astype(np.float32)).to(dev)
@@ -217,7 +230,7 @@ def main() -> int:
                     help="time only the value kernel (for profiler runs)")
     ap.add_argument("--profile-kernel", default=None,
                     choices=["dense", "dense_bf16", "dense_bf16_d16", "topk1", "topk95", "topk2", "topk4",
-                             "fixedset2", "zorder", "stream2", "large95"],
+                             "fixedset2", "zorder", "stream2", "large95", "dense_small"],
                     help="run only this kernel (headline shape; zorder/stream at their configs) "
                          "--warmup + --steps times, for profiler counter passes")
     ap.add_argument("--topk-filter", type=int, default=None, choices=[0, 1, 2, 3, 4],
