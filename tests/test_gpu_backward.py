@@ -63,7 +63,8 @@ def _dev(*xs):
 
 @pytest.mark.parametrize("N,d,kk", [(6, 16, 2), (24, 8, 5), (100, 16, 3), (256, 16, 2),
                                     (256, 32, 4), (300, 64, 12), (512, 16, 8), (96, 16, 23),
-                                    (384, 16, 95), (384, 32, 95), (1000, 16, 40), (1500, 8, 3)])
+                                    (384, 16, 95), (384, 32, 95), (300, 8, 30), (1000, 16, 40),
+                                    (1500, 8, 3)])
 def test_topk_backward(N, d, kk):
     from tarmac.kernels import fixedset_attention_backward, topk_attention
     B = 3
@@ -76,11 +77,14 @@ def test_topk_backward(N, d, kk):
     _close(got, _ref_set(q, k, v, idx.cpu().numpy(), g))
 
 
+@pytest.mark.parametrize("N,d,kk", [(40, 16, 6), (300, 16, 30), (300, 8, 7)])
 @pytest.mark.parametrize("idx_dtype", [torch.int32, torch.int64])
-def test_fixedset_backward_any_sets(idx_dtype):
-    """Arbitrary peer sets, repeated peers and the self pair included."""
+def test_fixedset_backward_any_sets(idx_dtype, N, d, kk):
+    """Arbitrary peer sets, repeated peers and the self pair included (rows
+    of 300 take lane pairs per query in the per-query pass, the repeated-peer
+    path quads)."""
     from tarmac.kernels import fixedset_attention_backward
-    B, N, d, kk = 2, 40, 16, 6
+    B = 2
     q, k, v = qkv(9, B, N, d)
     g = np.random.default_rng(2).standard_normal(q.shape).astype(np.float32)
     idx = np.random.default_rng(3).integers(0, N, size=(B, N, kk))
