@@ -14,7 +14,10 @@ aggregation):
   the bf16 inputs, outputs within 1e-2);
 * Z-order select+attend, B = 1024, N = 512, k = 2, 16 bits:
   selection bit-exact, outputs within 1e-5 of float64 over that selection;
-* bf16 at B = 4096, one (N, d) per k.
+* configs[2]: bf16 at B = 4096, one (N, d) per k;
+* the reference's masked (34 halvings) and sort rules at the shapes bench
+  times them (B = 1024, N = 256 and B = 256, N = 384, d = 16): sort indices
+  bit-exact, both outputs within 1e-5 of float64 over the oracle's sets.
 
 The oracle's top-k lists for k = 4 carry those for k = 1 and 2 as prefixes
 (one order, score desc / index asc), so each shape calls it once.
@@ -122,3 +125,30 @@ def test_configs2_bf16_b4096(N, d, kk):
     q, k, v = (O.bf16_round(x) for x in _inputs(77 + N + d, B, N, d))  # the benchmark's inputs
     out, idx = _topk(q, k, v, kk, torch.bfloat16)
     _check_prefixes(q, k, v, {kk: (out, idx)}, BF16_TOL)
+
+
+@pytest.mark.parametrize("B,N,kk", [(1024, 256, 1), (1024, 256, 2), (1024, 256, 4), (256, 384, 2)])
+def test_rule_variants_full_batch(B, N, kk):
+    """fused_topk_attention_masked / _sort over every row: random rows hold a
+    few exact ties at the k-th score, which the two rules resolve their own
+    ways (all tied peers / the higher indices)."""
+    from tarmac import _lib
+    from tarmac.kernels import fused_topk_attention_masked, topk_variant_attention
+    d = 16
+    q, k, v = _inputs(1234 + 7 * N + d, B, N, d)
+    qd, kd, vd = (torch.from_numpy(x).cuda() for x in (q, k, v))
+    masked = fused_topk_attention_masked(qd, kd, vd, kk).cpu().numpy()
+    srt, sidx = topk_variant_attention(qd, kd, vd, kk, _lib.VARIANT_SORT, return_indices=True)
+    srt, sidx = srt.cpu().numpy(), sidx.cpu().numpy()
+    for b0 in range(0, B, 128):  # oracle in slices of batch rows (memory)
+        sl = slice(b0, b0 + 128)
+        s = O.canon_scores(q[sl], k[sl])
+        keep = O.masked_threshold_keep(s, kk, 34)
+        ref = O.weights_attention(s, keep, v[sl])
+        assert np.abs(masked[sl] - ref).max() <= F32_TOL * np.abs(ref).max()
+        want = O.sort_select(s, kk)
+        assert np.array_equal(sidx[sl], np.sort(want, -1))
+        keep = np.zeros_like(s, dtype=bool)
+        np.put_along_axis(keep, want, True, -1)
+        ref = O.weights_attention(s, keep, v[sl])
+        assert np.abs(srt[sl] - ref).max() <= F32_TOL * np.abs(ref).max()

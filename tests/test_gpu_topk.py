@@ -346,7 +346,8 @@ def _variant_inputs(seed, B, N, d, ties):
 
 
 @pytest.mark.parametrize("N,d,kk,ties", [(6, 16, 2, False), (24, 16, 3, True), (100, 32, 4, False),
-                                         (256, 16, 2, True), (256, 64, 8, False), (513, 16, 5, True)])
+                                         (256, 16, 2, True), (256, 64, 8, False), (513, 16, 5, True),
+                                         (1024, 16, 1, True), (1024, 64, 7, True)])
 @pytest.mark.parametrize("bisect", [34, 32, 20, 5, 0])
 def test_masked_variant_matches_bisection_oracle(N, d, kk, ties, bisect):
     """fused_topk_attention_masked: the kept set is the reference's bisection
@@ -365,7 +366,8 @@ def test_masked_variant_matches_bisection_oracle(N, d, kk, ties, bisect):
 
 
 @pytest.mark.parametrize("N,d,kk,ties", [(6, 16, 2, True), (24, 8, 5, True), (100, 32, 4, False),
-                                         (256, 16, 2, True), (256, 64, 8, True), (300, 16, 12, True)])
+                                         (256, 16, 2, True), (256, 64, 8, True), (300, 16, 12, True),
+                                         (1024, 16, 3, True), (1024, 32, 8, True)])
 def test_sort_variant_keeps_higher_index_on_ties(N, d, kk, ties):
     from tarmac.kernels import fused_topk_attention_sort, topk_variant_attention
     from tarmac import _lib
@@ -385,6 +387,39 @@ def test_sort_variant_keeps_higher_index_on_ties(N, d, kk, ties):
     assert np.abs(out.cpu().numpy() - ref).max() <= F32_TOL * np.abs(ref).max()
     if ties:  # the tie rule is visible: rows of +0 scores keep the top indices
         assert np.all(idx.cpu().numpy()[:, 0] == np.arange(N - kk, N))
+
+
+@pytest.mark.parametrize("variant", ["masked", "sort"])
+def test_variants_nonfinite_inputs(variant):
+    """An infinite key element (batch row 0) and an infinite query element
+    (batch row 1): scores of +-inf, no NaN (each infinite element is the first
+    of its fmaf chain). The rules rank them by integer key like any score;
+    kept sets bit-exact (sort indices), NaN rows where an infinite score is
+    kept (inf - inf in the softmax), the other rows within 1e-5."""
+    from tarmac.kernels import topk_variant_attention
+    from tarmac import _lib
+    B, N, d, kk = 2, 256, 16, 3
+    q, k, v = qkv(91, B, N, d)
+    k[0, 37, 0] = np.inf
+    q[1, 9, 0] = -np.inf
+    qd, kd, vd = dev(q, k, v)
+    s = O.canon_scores(q, k)
+    assert not np.isnan(s).any()
+    if variant == "sort":
+        out, idx = topk_variant_attention(qd, kd, vd, kk, _lib.VARIANT_SORT, return_indices=True)
+        want = O.sort_select(s, kk)
+        assert np.array_equal(idx.cpu().numpy(), np.sort(want, -1))
+        keep = np.zeros_like(s, dtype=bool)
+        np.put_along_axis(keep, want, True, -1)
+    else:
+        out = topk_variant_attention(qd, kd, vd, kk, _lib.VARIANT_MASKED)
+        keep = O.masked_threshold_keep(s, kk, 34)
+    with np.errstate(invalid="ignore"):
+        ref = O.weights_attention(s, keep, v)
+    got = out.cpu().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(ref)) and np.isnan(ref).any()
+    fin = ~np.isnan(ref)
+    assert np.abs(got[fin] - ref[fin]).max() <= F32_TOL * np.abs(ref[fin]).max()
 
 
 def test_variants_equal_topk_without_ties():

@@ -176,7 +176,11 @@ int tarmac_topk_variant_fwd(const void* q, const void* k, const void* v, void* o
     return fail(TARMAC_ERR_INVALID, "%s: the masked variant keeps a variable number of peers; "
                 "idx_out must be NULL", fn);
   if (idx_out && !aligned(idx_out, 4)) return fail(TARMAC_ERR_INVALID, "%s: idx_out misaligned", fn);
-  tarmac::TopkArgs a{q, k, v, out, idx_out, B, N, d, topk, dtype, 0, inv_sqrt(d), stream};
+  // key chunk of the register-list kernel, which serves fp32 k <= 8 (the
+  // wide kernels ignore it): the whole row when it fits
+  const int n64 = (N + 63) / 64 * 64, kmax = max_topk_chunk(dtype, d);
+  tarmac::TopkArgs a{q, k, v, out, idx_out, B, N, d, topk, dtype, n64 < kmax ? n64 : kmax,
+                     inv_sqrt(d), stream};
   a.select = variant == TARMAC_VARIANT_MASKED ? tarmac::kSelMasked : tarmac::kSelSort;
   a.bisect = bisect;
   if (static_cast<size_t>(N + tarmac::wide_cap(a)) * 4 > kLdsBudget)

@@ -21,9 +21,13 @@
 //     the 4 lanes of a query each compute d/4 output channels from the k
 //     gathered V rows.
 //
-// Large k (> 8): one wave per query, the score row in LDS, an exact threshold
-// found by bisection on the order-preserving integer key, ties at the
-// threshold resolved to the lowest indices.
+// The same kernel with RULE serves the reference's masked (>= 32 halvings)
+// and sort selection rules at k <= 8 (src/kernels/fused_topk_attention.py:
+// 127-208, 405-504); queries the lists cannot settle go to rule_query_exact.
+//
+// Large k (> 8), and the rules elsewhere: sixteen lanes or one wave per query,
+// an exact threshold found by bisection on the order-preserving integer key,
+// ties at the threshold resolved by index.
 #include <atomic>
 
 #include "frag.hpp"
@@ -32,11 +36,166 @@
 
 namespace tarmac {
 
-template <typename T, int D, int K, int QT>
+__device__ __forceinline__ int ordered_key(float x) {
+  // Monotone fp32 -> int32 (src/kernels/fused_topk_attention.py:113-124).
+  const int i = __float_as_int(x);
+  return i ^ ((i >> 31) & 0x7fffffff);
+}
+
+__device__ __forceinline__ int wave_sum(int x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+__device__ __forceinline__ float wave_sumf(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+// One query of the masked rule (bisect >= 32) or the sort rule, by the whole
+// wavefront, on the integer keys of its canonical scores: the row's keys
+// (j = lane + 64 m) from K in global memory in the MFMA chain's fmaf order,
+// kept in the wave's LDS row `skey`; the k-th key by bisection; then every
+// key above it and, of the keys equal to it, all (masked) or the
+// highest-index ones (sort). The same function as topk_wide_kernel, for the
+// rows the register lists cannot settle: a tie across the k-th / (k+1)-th
+// score, or non-finite inputs. Runtime loops keep its registers below the
+// list pass's. `idx_row` (sort only, may be null) receives the set in
+// ascending index order.
+template <int D, bool POW2>
+__device__ __forceinline__ void rule_query_exact(const float* __restrict__ Qb,
+                                                 const float* __restrict__ Kb,
+                                                 const float* __restrict__ Vb, float* __restrict__ Ob,
+                                                 int32_t* __restrict__ idx_row, int* skey, int qi,
+                                                 int N, int topk, float scale, int mode) {
+  const int lane = threadIdx.x & 63;
+  const unsigned long long below = (1ull << lane) - 1ull;
+  const int nm = (N + 63) / 64;  // keys per lane (uniform)
+  {
+    float q[D];
+    ld_f32<D>(q, Qb + static_cast<size_t>(qi) * D);
+    if constexpr (POW2) {
+#pragma unroll
+      for (int c = 0; c < D; ++c) q[c] *= scale;
+    }
+#pragma unroll 1
+    for (int m = 0; m < nm; ++m) {
+      const int j = lane + 64 * m;
+      const float* krow = Kb + static_cast<size_t>(min(j, N - 1)) * D;
+      float acc = 0.f;
+#pragma unroll
+      for (int t = 0; t < D / 4; ++t)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) acc = fmaf(q[kk * (D / 4) + t], krow[kk * (D / 4) + t], acc);
+      if constexpr (!POW2) acc *= scale;
+      if (j < N) skey[j] = ordered_key(j == qi ? -INFINITY : acc);
+    }
+  }
+  auto key_at = [&](int m) { return skey[lane + 64 * m]; };  // m < nm, lane + 64 m < N
+  auto count_ge = [&](long t) {
+    int c = 0;
+#pragma unroll 1
+    for (int m = 0; m < nm; ++m) c += (lane + 64 * m < N && key_at(m) >= t) ? 1 : 0;
+    return wave_sum(c);
+  };
+  // largest t with count(key >= t) >= topk, or a t with exactly topk keys at
+  // or above it: both keep {key >= t_k} for the masked rule
+  long lo = -2147483648L, hi = 2147483647L;
+  while (lo < hi) {
+    const long mid = lo + (hi - lo + 1) / 2;
+    const int c = count_ge(mid);
+    if (c >= topk) lo = mid; else hi = mid - 1;
+    if (c == topk) break;
+  }
+  const int thr = static_cast<int>(lo);
+  int gt = 0, eq = 0;
+#pragma unroll 1
+  for (int m = 0; m < nm; ++m) {
+    if (lane + 64 * m >= N) continue;
+    const int key = key_at(m);
+    gt += key > thr ? 1 : 0;
+    eq += key == thr ? 1 : 0;
+  }
+  gt = wave_sum(gt);
+  eq = wave_sum(eq);
+  const int need_ties = mode == kSelMasked ? eq : topk - gt;
+  const int skip_ties = mode == kSelSort ? eq - need_ties : 0;
+  unsigned picks = 0u;  // bit m: key lane + 64 m is kept
+  int taken = 0, ties = 0;
+  float mx = -INFINITY;
+#pragma unroll 1
+  for (int m = 0; m < nm; ++m) {
+    const int j = lane + 64 * m;
+    const int key = j < N ? key_at(m) : 0;
+    const bool is_tie = j < N && key == thr;
+    const unsigned long long tmask = __ballot(is_tie);
+    const int tie_rank = ties + __popcll(tmask & below);
+    const bool pick = j < N && (key > thr || (is_tie && tie_rank >= skip_ties &&
+                                              tie_rank < skip_ties + need_ties));
+    const unsigned long long pmask = __ballot(pick);
+    if (pick) {
+      picks |= 1u << m;
+      mx = fmaxf(mx, __int_as_float(key ^ ((key >> 31) & 0x7fffffff)));
+      if (idx_row != nullptr) idx_row[taken + __popcll(pmask & below)] = j;
+    }
+    taken += __popcll(pmask);
+    ties += __popcll(tmask);
+  }
+  mx = wave_max(mx);
+  auto weight = [&](int m) {
+    const int key = key_at(m);
+    return fast_exp2((__int_as_float(key ^ ((key >> 31) & 0x7fffffff)) - mx) * kLog2eF);
+  };
+  float den = 0.f;
+#pragma unroll 1
+  for (int m = 0; m < nm; ++m)
+    if ((picks >> m) & 1u) den += weight(m);
+  den = wave_sumf(den);
+  constexpr int CH = D < 16 ? D : 16;  // output channels per pass
+#pragma unroll 1
+  for (int c0 = 0; c0 < D; c0 += CH) {
+    float a[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) a[c] = 0.f;
+#pragma unroll 1
+    for (int m = 0; m < nm; ++m) {
+      if ((picks >> m) & 1u) {
+        const float w = weight(m);
+        float vr[CH];
+        ld_f32<CH>(vr, Vb + static_cast<size_t>(lane + 64 * m) * D + c0);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) a[c] = fmaf(w, vr[c], a[c]);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c) a[c] = wave_sumf(a[c]);
+    if (lane == 0) {
+      const float inv = 1.f / den;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) a[c] *= inv;
+      st_f32<CH>(Ob + static_cast<size_t>(qi) * D + c0, a);
+    }
+  }
+}
+
+// RULE: the reference's masked (bisect >= 32) and sort rules, fp32. Both keep
+// exactly the top k when the k-th and (k+1)-th scores differ, so the lists
+// also carry the (k+1)-th value (val[K]); a query whose k-th and (k+1)-th
+// values are equal, or whose inputs are not all finite (a NaN score is absent
+// from a list but ranks in the integer key order), goes to rule_query_exact.
+template <typename T, int D, int K, int QT, bool RULE = false>
 __global__ void __launch_bounds__(256)
 topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
                   T* __restrict__ O, int32_t* __restrict__ Idx, int N, int n_qblk, int kc,
-                  float scale, int nblocks) {
+                  float scale, int nblocks, int mode) {
   using F = Frag<T, D>;
   constexpr int LDK = F::LDK;
   constexpr int EO = D / 4;  // output channels per lane
@@ -61,12 +220,31 @@ topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __
   }
 
   static_assert(sizeof(T) == 4, "the register-list pass selects on exact fp32 scores");
-  float val[QT][K];
+  constexpr int KV = RULE ? K + 1 : K;  // RULE: val[K] is the (K+1)-th best value
+  float val[QT][KV];
   int ix[QT][K];
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt)
+  for (int qt = 0; qt < QT; ++qt) {
 #pragma unroll
-    for (int m = 0; m < K; ++m) { val[qt][m] = -INFINITY; ix[qt][m] = kIdxSentinel; }
+    for (int m = 0; m < KV; ++m) val[qt][m] = -INFINITY;
+#pragma unroll
+    for (int m = 0; m < K; ++m) ix[qt][m] = kIdxSentinel;
+  }
+  // RULE: a non-finite element among the staged keys (one flag word past the
+  // key rows) or in this lane's part of a query row
+  unsigned* kflag = reinterpret_cast<unsigned*>(
+      smem_raw + static_cast<size_t>((kc + kBlockKeys - 1) / kBlockKeys * kBlockKeys) * LDK * sizeof(T));
+  int* skey = reinterpret_cast<int*>(kflag + 4) + static_cast<size_t>(wave) * ((N + 63) & ~63);
+  bool qbad[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    qbad[qt] = false;
+    if constexpr (RULE) {
+#pragma unroll
+      for (int e = 0; e < F::E; ++e) qbad[qt] = qbad[qt] || !__builtin_isfinite(frag[qt].q[e]);
+    }
+  }
+  if (RULE && threadIdx.x == 0) *kflag = 0u;
 
   bool self_r[4];  // element r of a diagonal tile is this lane's self pair
 #pragma unroll
@@ -82,6 +260,15 @@ topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __
     __syncthreads();
     stage_rows<T, D, LDK>(Ks, Kx + boff + static_cast<size_t>(c0) * D, cn, cnb);
     __syncthreads();
+    if constexpr (RULE) {
+      bool kfin = true;  // a quarter row per thread and pass
+      for (int u = threadIdx.x; u < cn * (D / 4); u += blockDim.x) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(Ks + (u / (D / 4)) * LDK + 4 * (u % (D / 4)));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kfin = kfin && __builtin_isfinite(x[e]);
+      }
+      if (!__all(kfin) && lane == 0) atomicOr(kflag, 1u);
+    }
     if (q0 >= N) continue;
     const int kend = c0 + cn;  // rows past the chunk end are zero padding
     for (int kb0 = 0; kb0 < cnb; kb0 += kBlockKeys) {
@@ -96,10 +283,14 @@ topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __
 #pragma unroll
         for (int t = 0; t < BT; ++t)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) topk_insert<K>(val[qt], ix[qt], s[qt][t][r], 16 * t + r);
+          for (int r = 0; r < 4; ++r) {
+            if constexpr (RULE) topk_insert_x<K>(val[qt], ix[qt], s[qt][t][r], 16 * t + r);
+            else topk_insert<K>(val[qt], ix[qt], s[qt][t][r], 16 * t + r);
+          }
     }
   }
   rebase_list<QT, K>(ix, -base);  // back to absolute key indices
+  if constexpr (RULE) __syncthreads();  // every wave's key check is in
   if (q0 >= N) return;
 
 #pragma unroll
@@ -108,22 +299,37 @@ topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __
     for (int m = 0; m < K; ++m) ix[qt][m] += 4 * grp;
 #pragma unroll
     for (int step = 16; step <= 32; step <<= 1) {
-      float pv[K];
+      float pv[KV];
       int pi[K];
 #pragma unroll
-      for (int m = 0; m < K; ++m) {
-        pv[m] = __shfl_xor(val[qt][m], step);
-        pi[m] = __shfl_xor(ix[qt][m], step);
-      }
+      for (int m = 0; m < KV; ++m) pv[m] = __shfl_xor(val[qt][m], step);
 #pragma unroll
-      for (int m = 0; m < K; ++m) topk_insert_lex<K>(val[qt], ix[qt], pv[m], pi[m]);
+      for (int m = 0; m < K; ++m) pi[m] = __shfl_xor(ix[qt][m], step);
+      if constexpr (RULE) {
+#pragma unroll
+        for (int m = 0; m < K; ++m) topk_insert_lex_x<K>(val[qt], ix[qt], pv[m], pi[m]);
+        val[qt][K] = vmax(val[qt][K], pv[K]);  // the partner's (K+1)-th
+      } else {
+#pragma unroll
+        for (int m = 0; m < K; ++m) topk_insert_lex<K>(val[qt], ix[qt], pv[m], pi[m]);
+      }
+    }
+  }
+  bool slow[QT];  // RULE: this lane's query goes to rule_query_exact
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    slow[qt] = false;
+    if constexpr (RULE) {
+      const unsigned long long bad = __ballot(qbad[qt]);
+      slow[qt] = *kflag != 0u || ((bad >> col) & 0x0001000100010001ull) != 0ull ||
+                 val[qt][K - 1] == val[qt][K];
     }
   }
 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int qi = q0 + 16 * qt + col;
-    if (qi >= N) continue;
+    if (qi >= N || slow[qt]) continue;
     const float mx = val[qt][0];
     float acc[EO];
 #pragma unroll
@@ -146,7 +352,30 @@ topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __
     if (Idx != nullptr && grp == 0) {
       int32_t* dst = Idx + (static_cast<size_t>(b) * N + qi) * K;
 #pragma unroll
-      for (int m = 0; m < K; ++m) dst[m] = ix[qt][m];
+      for (int m = 0; m < K; ++m) {
+        if constexpr (RULE) {  // the rules' sets in ascending index order
+          int rank = 0;
+#pragma unroll
+          for (int u = 0; u < K; ++u) rank += ix[qt][u] < ix[qt][m] ? 1 : 0;
+          dst[rank] = ix[qt][m];
+        } else {
+          dst[m] = ix[qt][m];
+        }
+      }
+    }
+  }
+  if constexpr (RULE) {
+    // the unsettled queries, one at a time across the whole wave
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      unsigned long long todo = __ballot(grp == 0 && slow[qt] && q0 + 16 * qt + col < N);
+      while (todo != 0ull) {
+        const int qj = q0 + 16 * qt + __builtin_ctzll(todo);
+        todo &= todo - 1ull;
+        rule_query_exact<D, POW2>(Q + boff, Kx + boff, V + boff, O + boff,
+                                  Idx != nullptr ? Idx + (static_cast<size_t>(b) * N + qj) * K : nullptr,
+                                  skey, qj, N, K, scale, mode);
+      }
     }
   }
 }
@@ -154,24 +383,6 @@ topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __
 // ---------------------------------------------------------------------------
 // large k: one wave per query row
 // ---------------------------------------------------------------------------
-
-__device__ __forceinline__ int ordered_key(float x) {
-  // Monotone fp32 -> int32 (src/kernels/fused_topk_attention.py:113-124).
-  const int i = __float_as_int(x);
-  return i ^ ((i >> 31) & 0x7fffffff);
-}
-
-__device__ __forceinline__ int wave_sum(int x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  return x;
-}
-
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
-}
 
 template <typename T, int D>
 __device__ __forceinline__ float canon_score(const float (&q)[D], const T* krow) {
@@ -538,7 +749,7 @@ topk_wide16_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
 // launchers
 // ---------------------------------------------------------------------------
 
-template <typename T, int D>
+template <typename T, int D, bool RULE = false>
 static hipError_t launch_small(const TopkArgs& a, int kc) {
   constexpr int QT = kTopkQueryTiles;
   const int per_wave = 16 * QT;
@@ -549,7 +760,9 @@ static hipError_t launch_small(const TopkArgs& a, int kc) {
   const int nblocks = a.B * n_qblk;
   // this kernel's own key copy (topk_lds_bytes also covers the filter
   // kernel's larger split rows; allocating that would cost occupancy)
-  const size_t lds = plain_lds_bytes(a.dtype, a.d, kc);
+  // RULE: + the key flag and one key row per wave for rule_query_exact
+  const size_t lds = plain_lds_bytes(a.dtype, a.d, kc) +
+                     (RULE ? 16 + static_cast<size_t>(nw) * ((a.N + 63) & ~63) * 4 : 0);
   const T* q = static_cast<const T*>(a.q);
   const T* k = static_cast<const T*>(a.k);
   const T* v = static_cast<const T*>(a.v);
@@ -557,8 +770,8 @@ static hipError_t launch_small(const TopkArgs& a, int kc) {
   hipStream_t st = static_cast<hipStream_t>(a.stream);
 #define TARMAC_TOPK_CASE(KK)                                                                   \
   case KK:                                                                                     \
-    hipLaunchKernelGGL((topk_small_kernel<T, D, KK, QT>), dim3(nblocks), dim3(64 * nw), lds, st, \
-                       q, k, v, o, a.idx, a.N, n_qblk, kc, a.scale, nblocks);                 \
+    hipLaunchKernelGGL((topk_small_kernel<T, D, KK, QT, RULE>), dim3(nblocks), dim3(64 * nw), lds, \
+                       st, q, k, v, o, a.idx, a.N, n_qblk, kc, a.scale, nblocks, a.select);  \
     break;
   switch (a.topk) {
     TARMAC_TOPK_CASE(1)
@@ -629,8 +842,20 @@ static hipError_t launch_wide(const TopkArgs& a) {
   return hipGetLastError();
 }
 
+// The masked rule after >= 32 halvings and the sort rule, fp32, k <= 8,
+// N <= 1024 (the reference's own limit): the register lists with the
+// (k+1)-th value, per-query fallback to the exact wave path. 32 halvings close
+// any interval of 2^32 integer keys, so the masked threshold is then the k-th
+// key itself; fewer halvings (a superset) and bf16 run the wide kernels.
+bool topk_rule_lists(const TopkArgs& a) {
+  return a.select != kSelTopk && a.dtype == kF32 && a.topk <= kTopkSmallMax && a.N <= 1024 &&
+         (a.select == kSelSort || a.bisect >= 32) && a.key_chunk > 0;
+}
+
 template <typename T, int D>
 static hipError_t dispatch_topk(const TopkArgs& a) {
+  if constexpr (sizeof(T) == 4)
+    if (topk_rule_lists(a)) return launch_small<T, D, true>(a, a.key_chunk);
   if (a.topk > kTopkSmallMax || a.select != kSelTopk) return launch_wide<T, D>(a);
   if constexpr (sizeof(T) == 4) return launch_small<T, D>(a, a.key_chunk);
   return hipErrorInvalidValue;  // bf16 k <= 8 runs the packed or filter kernels
