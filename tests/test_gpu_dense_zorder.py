@@ -40,7 +40,7 @@ def normwise(got, ref):
 
 @pytest.mark.parametrize("N,d", [(2, 16), (6, 16), (6, 8), (17, 16), (64, 32), (100, 16),
                                  (128, 64), (256, 16), (384, 16), (512, 32), (1024, 16),
-                                 (1024, 64)])
+                                 (1024, 64), (32, 64), (40, 8), (33, 32), (64, 16), (48, 64)])
 def test_dense_f32(N, d):
     from tarmac.kernels import fused_dense_attention
     B = max(2, min(16, 4096 // N))
@@ -50,7 +50,7 @@ def test_dense_f32(N, d):
     assert normwise(out, ref) <= F32_TOL
 
 
-@pytest.mark.parametrize("N,d,chunk", [(256, 16, 64), (1000, 16, 128), (512, 64, 64)])
+@pytest.mark.parametrize("N,d,chunk", [(256, 16, 64), (1000, 16, 128), (512, 64, 64), (64, 16, 32)])
 def test_dense_streamed_chunks(N, d, chunk):
     from tarmac.kernels import fused_dense_attention
     q, k, v = qkv(N + chunk, 3, N, d)

@@ -234,8 +234,153 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
   }
 }
 
+// fp32, N <= 64: no LDS, no barrier. Every MFMA operand of a wave (its query
+// fragments, the 16-key K fragments, the V^T fragments of the P.V product) is
+// loaded from global memory at the start, so the row's q, k and v arrive in
+// one memory round trip (the LDS kernel stages K, then V, then waits at a
+// barrier). A K fragment is 16 rows x 64 B (coalesced); a V^T fragment element
+// is read per lane, 16 consecutive channels per row. One softmax over the
+// whole row; for N <= 64 this is the LDS kernel's arithmetic, operation for
+// operation (one 64-key block), so the two give identical results.
+template <int D, int QT, int NT>
+__global__ void __launch_bounds__(64)
+dense_reg_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
+                 const float* __restrict__ V, float* __restrict__ O, float* __restrict__ lse, int N,
+                 int n_qblk, float scale, int nblocks) {
+  using F = Frag<float, D>;
+  constexpr int NH = PvOperand<float, D>::NH;
+  const int lane = threadIdx.x;
+  const int blk = xcd_logical_block(blockIdx.x, nblocks);
+  const int b = blk / n_qblk, qb = blk - b * n_qblk;
+  const int q0 = qb * 16 * QT;
+  const int col = lane & 15, grp = lane >> 4;
+  const size_t boff = static_cast<size_t>(b) * N * D;
+
+  F frag[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+    frag[qt].load_q(Q + boff + static_cast<size_t>(min(q0 + 16 * qt + col, N - 1)) * D, grp,
+                    scale * kLog2e);
+  typename F::KF kf[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+    kf[t] = F::load_k(Kx + boff + static_cast<size_t>(min(16 * t + col, N - 1)) * D, grp);
+  f32x4 vv[NT][NH];  // V^T fragment: element u = V[16t + 4 grp + u][16h + col]
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int row = 16 * t + 4 * grp + u, c = 16 * h + col;
+        vv[t][h][u] = (row < N && c < D) ? V[boff + static_cast<size_t>(row) * D + c] : 0.f;
+      }
+
+  f32x4 s[QT][NT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < F::NI; ++i) acc = frag[qt].step(kf[t], i, acc);
+      if (16 * t + 16 > N || 16 * t == q0 + 16 * qt) {  // wave-uniform: the tail or the diagonal tile
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = 16 * t + 4 * grp + r;
+          if (key >= N || key == q0 + 16 * qt + col) acc[r] = -INFINITY;
+        }
+      }
+      s[qt][t] = acc;
+    }
+  f32x4 acc[QT][NH];
+  float m_row[QT], l[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) m = fmaxf(m, s[qt][t][r]);
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    m_row[qt] = m;
+    const float neg = -(m == -INFINITY ? 0.f : m);
+    l[qt] = 0.f;
+#pragma unroll
+    for (int h = 0; h < NH; ++h) acc[qt][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        s[qt][t][r] = fast_exp2(fmaf(s[qt][t][r], 1.f, neg));
+        l[qt] += s[qt][t][r];
+      }
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+          acc[qt][h] = mfma_f32_16x16x4(vv[t][h][u], s[qt][t][u], acc[qt][h]);
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    float l_tot = l[qt] + __shfl_xor(l[qt], 16);
+    l_tot += __shfl_xor(l_tot, 32);
+    const int qi = q0 + 16 * qt + col;
+    if (qi >= N) continue;
+    if (lse != nullptr && grp == 0)
+      lse[static_cast<size_t>(b) * 2 * N + qi] = m_row[qt] + log2f(l_tot);
+    const float inv = 1.f / l_tot;
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      const int cbase = 16 * h + 4 * grp;
+      if (cbase < D) {
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = acc[qt][h][r] * inv;
+        st_row<float, 4>(O + boff + static_cast<size_t>(qi) * D + cbase, o);
+      }
+    }
+  }
+}
+
+template <int D, int NT>
+static hipError_t launch_dense_reg(const DenseArgs& a) {
+  constexpr int QT = 2;
+  const int n_qblk = (a.N + 16 * QT - 1) / (16 * QT);
+  const int nblocks = a.B * n_qblk;
+  hipLaunchKernelGGL((dense_reg_kernel<D, QT, NT>), dim3(nblocks), dim3(64), 0,
+                     static_cast<hipStream_t>(a.stream), static_cast<const float*>(a.q),
+                     static_cast<const float*>(a.k), static_cast<const float*>(a.v),
+                     static_cast<float*>(a.out), a.stats, a.N, n_qblk, a.scale, nblocks);
+  return hipGetLastError();
+}
+
+// Register kernel for fp32 rows of up to 64 keys (32 at d = 64, where 64
+// keys of K and V fragments would not leave registers for two query tiles).
+// B=1024 d=16, rocprof average: N = 32 5.7 -> 3.5 us, N = 64 7.1 -> 6.5 us.
+template <int D>
+static bool dense_reg(const DenseArgs& a, hipError_t* e) {
+  if (a.N > (D <= 32 ? 64 : 32) || a.key_chunk < a.N) return false;  // an explicit smaller chunk keeps LDS
+  switch ((a.N + 15) / 16) {
+    case 1: *e = launch_dense_reg<D, 1>(a); return true;
+    case 2: *e = launch_dense_reg<D, 2>(a); return true;
+    case 3: *e = launch_dense_reg<D, 3>(a); return true;
+    case 4: if constexpr (D <= 32) { *e = launch_dense_reg<D, 4>(a); return true; }
+  }
+  return false;
+}
+
 template <typename T, int D>
 static hipError_t launch_dense(const DenseArgs& a) {
+  if constexpr (sizeof(T) == 4) {
+    hipError_t e;
+    if (dense_reg<D>(a, &e)) return e;
+  }
   constexpr int QT = kDenseQueryTiles;
   const int per_wave = 16 * QT;
   const int waves = (a.N + per_wave - 1) / per_wave;
