@@ -380,6 +380,131 @@ topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __
   }
 }
 
+// fp32 rows of up to 64 keys (N * d <= 2048), k <= 8: the register-list
+// selection of topk_small_kernel with every operand fetched in one memory
+// round trip. The wave loads its query fragments and the 16-key K fragments
+// straight from global memory (16 rows x 64 B per fragment, coalesced) and,
+// in the same burst, the batch row's V into LDS; selection then runs while the
+// LDS writes land, and the k value rows are gathered from LDS instead of a
+// second trip to memory. Selection and arithmetic are those of
+// topk_small_kernel, so the results are identical.
+template <int D, int K, int NT>
+__global__ void __launch_bounds__(64)
+topk_reg_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
+                const float* __restrict__ V, float* __restrict__ O, int32_t* __restrict__ Idx,
+                int N, int n_qblk, float scale, int nblocks) {
+  using F = Frag<float, D>;
+  constexpr int QT = 2;
+  constexpr int EO = D / 4;
+  constexpr int LDV = D + 4;                 // padded LDS value row
+  constexpr int NV = (NT * 16 * D / 4 + 63) / 64;  // float4 of V per lane
+  constexpr bool POW2 = pow2_scale<D>();
+  __shared__ __align__(16) float Vs[NT * 16 * LDV];
+  const int lane = threadIdx.x;
+  const int blk = xcd_logical_block(blockIdx.x, nblocks);
+  const int b = blk / n_qblk, qb = blk - b * n_qblk;
+  const int q0 = qb * 16 * QT;
+  const int col = lane & 15, grp = lane >> 4;
+  const size_t boff = static_cast<size_t>(b) * N * D;
+
+  F frag[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+    frag[qt].load_q(Q + boff + static_cast<size_t>(min(q0 + 16 * qt + col, N - 1)) * D, grp,
+                    POW2 ? scale : 1.f);
+  typename F::KF kf[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+    kf[t] = F::load_k(Kx + boff + static_cast<size_t>(min(16 * t + col, N - 1)) * D, grp);
+  f32x4 vr[NV];
+  const f32x4* vsrc = reinterpret_cast<const f32x4*>(V + boff);
+  const int nv4 = N * D / 4;
+#pragma unroll
+  for (int u = 0; u < NV; ++u) {
+    const int e = lane + 64 * u;
+    vr[u] = e < nv4 ? vsrc[e] : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int u = 0; u < NV; ++u) {
+    const int e = lane + 64 * u;
+    if (e < nv4) {
+      const int row = e / (D / 4), c4 = e - row * (D / 4);
+      *reinterpret_cast<f32x4*>(Vs + row * LDV + 4 * c4) = vr[u];
+    }
+  }
+
+  float val[QT][K];
+  int ix[QT][K];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int m = 0; m < K; ++m) { val[qt][m] = -INFINITY; ix[qt][m] = kIdxSentinel; }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < F::NI; ++i) sc = frag[qt].step(kf[t], i, sc);
+      if constexpr (!POW2) sc *= scale;
+      if (16 * t + 16 > N || 16 * t == q0 + 16 * qt) {  // wave-uniform: the tail or the diagonal tile
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = 16 * t + 4 * grp + r;
+          if (key >= N || key == q0 + 16 * qt + col) sc[r] = -INFINITY;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) topk_insert<K>(val[qt], ix[qt], sc[r], 16 * t + 4 * grp + r);
+    }
+  }
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+    for (int step = 16; step <= 32; step <<= 1) {
+      float pv[K];
+      int pi[K];
+#pragma unroll
+      for (int m = 0; m < K; ++m) {
+        pv[m] = __shfl_xor(val[qt][m], step);
+        pi[m] = __shfl_xor(ix[qt][m], step);
+      }
+#pragma unroll
+      for (int m = 0; m < K; ++m) topk_insert_lex<K>(val[qt], ix[qt], pv[m], pi[m]);
+    }
+  }
+  __syncthreads();  // the value rows are in LDS
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qi = q0 + 16 * qt + col;
+    if (qi >= N) continue;
+    const float mx = val[qt][0];
+    float acc[EO];
+#pragma unroll
+    for (int c = 0; c < EO; ++c) acc[c] = 0.f;
+    float den = 0.f;
+#pragma unroll
+    for (int m = 0; m < K; ++m) {
+      const float w = fast_exp2((val[qt][m] - mx) * kLog2eF);
+      den += w;
+      const int row = min(max(ix[qt][m], 0), N - 1);
+      float vrow[EO];
+      ld_f32<EO>(vrow, Vs + row * LDV + grp * EO);
+#pragma unroll
+      for (int c = 0; c < EO; ++c) acc[c] = fmaf(w, vrow[c], acc[c]);
+    }
+    const float inv = 1.f / den;
+#pragma unroll
+    for (int c = 0; c < EO; ++c) acc[c] *= inv;
+    st_row<float, EO>(O + boff + static_cast<size_t>(qi) * D + grp * EO, acc);
+    if (Idx != nullptr && grp == 0) {
+      int32_t* dst = Idx + (static_cast<size_t>(b) * N + qi) * K;
+#pragma unroll
+      for (int m = 0; m < K; ++m) dst[m] = ix[qt][m];
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // large k: one wave per query row
 // ---------------------------------------------------------------------------
@@ -789,6 +914,51 @@ static hipError_t launch_small(const TopkArgs& a, int kc) {
   return hipGetLastError();
 }
 
+template <int D, int NT>
+static hipError_t launch_reg(const TopkArgs& a) {
+  const int n_qblk = (a.N + 31) / 32;
+  const int nblocks = a.B * n_qblk;
+  const float* q = static_cast<const float*>(a.q);
+  const float* k = static_cast<const float*>(a.k);
+  const float* v = static_cast<const float*>(a.v);
+  float* o = static_cast<float*>(a.out);
+  hipStream_t st = static_cast<hipStream_t>(a.stream);
+#define TARMAC_TOPK_REG_CASE(KK)                                                                  \
+  case KK:                                                                                        \
+    hipLaunchKernelGGL((topk_reg_kernel<D, KK, NT>), dim3(nblocks), dim3(64), 0, st, q, k, v, o,   \
+                       a.idx, a.N, n_qblk, a.scale, nblocks);                                     \
+    break;
+  switch (a.topk) {
+    TARMAC_TOPK_REG_CASE(1)
+    TARMAC_TOPK_REG_CASE(2)
+    TARMAC_TOPK_REG_CASE(3)
+    TARMAC_TOPK_REG_CASE(4)
+    TARMAC_TOPK_REG_CASE(5)
+    TARMAC_TOPK_REG_CASE(6)
+    TARMAC_TOPK_REG_CASE(7)
+    TARMAC_TOPK_REG_CASE(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef TARMAC_TOPK_REG_CASE
+  return hipGetLastError();
+}
+
+// topk_reg_kernel's domain: fp32 rows of up to 64 keys with N * d <= 2048
+// (the V row block fits a lane's share of registers on its way to LDS), the
+// whole row resident (no explicit smaller key chunk).
+template <int D>
+static bool topk_reg(const TopkArgs& a, hipError_t* e) {
+  if (a.N > 64 || a.N * D > 2048 || a.key_chunk < a.N) return false;
+  switch ((a.N + 15) / 16) {
+    case 1: *e = launch_reg<D, 1>(a); return true;
+    case 2: *e = launch_reg<D, 2>(a); return true;
+    case 3: if constexpr (D <= 32) { *e = launch_reg<D, 3>(a); return true; } break;
+    case 4: if constexpr (D <= 32) { *e = launch_reg<D, 4>(a); return true; } break;
+  }
+  return false;
+}
+
 int wide_cap(const TopkArgs& a) { return a.select == kSelMasked ? a.N : a.topk; }
 
 template <typename T, int D, int NS>
@@ -857,7 +1027,11 @@ static hipError_t dispatch_topk(const TopkArgs& a) {
   if constexpr (sizeof(T) == 4)
     if (topk_rule_lists(a)) return launch_small<T, D, true>(a, a.key_chunk);
   if (a.topk > kTopkSmallMax || a.select != kSelTopk) return launch_wide<T, D>(a);
-  if constexpr (sizeof(T) == 4) return launch_small<T, D>(a, a.key_chunk);
+  if constexpr (sizeof(T) == 4) {
+    hipError_t e;
+    if (topk_reg<D>(a, &e)) return e;
+    return launch_small<T, D>(a, a.key_chunk);
+  }
   return hipErrorInvalidValue;  // bf16 k <= 8 runs the packed or filter kernels
 }
 
