@@ -146,13 +146,11 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
     const int cn = min(kc, N - c0);
     const int cnp = (cn + BK - 1) / BK * BK;
     __syncthreads();
-    stage_rows<T, D, LDK>(Ks, Kx + boff + static_cast<size_t>(c0) * D, cn, cnp);
-    // bf16 rows transpose four at a time (8-byte stores instead of 2-byte
-    // ones); fp32 keeps one store per element, measured no slower
-    if constexpr (sizeof(T) == 4)
-      stage_vt<T, D, PV::CP>(Vt, ldv, V + boff + static_cast<size_t>(c0) * D, cn, cnp);
-    else
-      stage_vt_quads<T, D, PV::CP>(Vt, ldv, V + boff + static_cast<size_t>(c0) * D, cn, cnp);
+    // K and V^T in one pass of loads; bf16 rows transpose four at a time
+    // (8-byte stores instead of 2-byte ones), fp32 keeps one store per
+    // element, measured no slower
+    stage_kv<T, D, LDK, PV::CP>(Ks, Vt, ldv, Kx + boff + static_cast<size_t>(c0) * D,
+                                V + boff + static_cast<size_t>(c0) * D, cn, cnp);
     __syncthreads();
     if (q0 >= N) continue;
     const int kend = c0 + cn;  // rows past the chunk end are zero padding

@@ -294,6 +294,91 @@ __device__ __forceinline__ void stage_rows(T* lds, const T* src, int rows, int r
   }
 }
 
+// stage_rows of K and the transposed V of the same rows together: every pass
+// issues its K and V loads before any LDS write, so a chunk costs one memory
+// round trip per pass rather than one for K and then one for V. fp32 V is
+// written one element per store (stage_vt); bf16 V four rows per thread
+// (stage_vt_quads), whose quad loop has the same trip count as the K loop
+// with kStageBatch = 4 vectors per thread. rows_pad is a multiple of 4.
+template <typename T, int D, int LDK, int CP>
+__device__ __forceinline__ void stage_kv(T* Ks, T* Vt, int ldv, const T* ksrc, const T* vsrc,
+                                         int rows, int rows_pad) {
+  constexpr int VE = 16 / sizeof(T);
+  constexpr int VPR = D / VE;
+  constexpr int U = kStageBatch;
+  constexpr bool QUADS = sizeof(T) == 2;
+  static_assert(D % VE == 0 && (LDK * sizeof(T)) % 16 == 0 && U == 4, "16-byte staging");
+  const char* kbase = reinterpret_cast<const char*>(ksrc);
+  const char* vbase = reinterpret_cast<const char*>(vsrc);
+  const int total = rows_pad * VPR;
+  const int avail = rows * VPR;
+  const int bd = blockDim.x;
+  for (int it = 0; it * U * bd < total; ++it) {
+    const int v0 = threadIdx.x + it * U * bd;
+    uint4 xk[U], xv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int v = v0 + u * bd;
+      xk[u] = make_uint4(0u, 0u, 0u, 0u);
+      if (v < avail) xk[u] = *reinterpret_cast<const uint4*>(kbase + static_cast<uint32_t>(v) * 16u);
+    }
+    // V: QUADS, quad t = threadIdx.x + it * bd covers rows 4 (t / VPR) .. +3 at
+    // vector column t % VPR; otherwise the same vectors as K
+    const int t = threadIdx.x + it * bd;
+    const int quad = t / VPR, cq = t - quad * VPR, row0 = 4 * quad;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      xv[u] = make_uint4(0u, 0u, 0u, 0u);
+      if constexpr (QUADS) {
+        if (t < total / 4 && row0 + u < rows)
+          xv[u] = *reinterpret_cast<const uint4*>(
+              vbase + static_cast<uint32_t>((row0 + u) * VPR + cq) * 16u);
+      } else {
+        const int v = v0 + u * bd;
+        if (v < avail) xv[u] = *reinterpret_cast<const uint4*>(vbase + static_cast<uint32_t>(v) * 16u);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int v = v0 + u * bd, row = v / VPR, cv = v - row * VPR;
+      if (v < total) *reinterpret_cast<uint4*>(Ks + row * LDK + cv * VE) = xk[u];
+    }
+    if constexpr (QUADS) {
+      if (t < total / 4) {
+        const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&xv[0]);
+        const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&xv[1]);
+        const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&xv[2]);
+        const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&xv[3]);
+#pragma unroll
+        for (int e = 0; e < VE; ++e) {
+          // element e is the low (e even) or high (e odd) half of word e / 2
+          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+          *reinterpret_cast<uint2*>(Vt + (cq * VE + e) * ldv + row0) =
+              make_uint2(__builtin_amdgcn_perm(w1[e / 2], w0[e / 2], sel),
+                         __builtin_amdgcn_perm(w3[e / 2], w2[e / 2], sel));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int v = v0 + u * bd, row = v / VPR, cv = v - row * VPR;
+        if (v >= total) break;
+        T x[VE];
+        __builtin_memcpy(x, &xv[u], 16);
+#pragma unroll
+        for (int e = 0; e < VE; ++e) Vt[(cv * VE + e) * ldv + row] = x[e];
+      }
+    }
+  }
+  if constexpr (CP > D) {
+    const int pad = (CP - D) * rows_pad;
+    for (int v = threadIdx.x; v < pad; v += bd) {
+      const int c = D + v / rows_pad, row = v % rows_pad;
+      Vt[c * ldv + row] = T(0);
+    }
+  }
+}
+
 // Stage V[rows, D] transposed into Vt[c][key] (row stride ldv), zero-filling
 // keys [rows, rows_pad) and channels [D, CP).
 template <typename T, int D, int CP>

@@ -1052,8 +1052,9 @@ enum TopkPath { kPathPacked, kPathPackedSplit, kPathFilter, kPathLists };
 //     38.1 vs 44.1 filter, 56.5 lists; N=512 k=2: 83.5 vs 96.2 filter, 117.4
 //     lists); below N = 256 the register lists for k <= 2 (N=64 k=1: 5.9 vs
 //     6.7 packed, 9.2 split) and the fp32-MFMA packed pass above (N=128 k=4:
-//     17.9 vs 19.9 lists).
-//   fp32, d = 8, 32, 64: register lists for k <= 2, packed above.
+//     17.9 vs 19.9 lists), except at N <= 32, where the one-round-trip list
+//     kernel wins at every k (rocprof, B=1024 N=32 k=4: 7.4 vs 7.8 packed).
+//   fp32, d = 8, 32, 64: register lists for k <= 2 (every k at N <= 32), packed above.
 //   bf16: packed, or the bf16 filter at d = 16 with k >= 4 and N >= 256
 //     (B=1024 N=256 k=4: 35.1 vs 40.4); the register lists do not serve bf16
 //     (their selection would run on the approximate bf16 scores).
@@ -1069,7 +1070,7 @@ static TopkPath choose_path(const TopkArgs& a, int mode) {
   }
   if (a.dtype == kBf16) return (filt && a.topk >= 4 && a.N >= 256) ? kPathFilter : kPathPacked;
   if (split && a.N >= 256) return kPathPackedSplit;
-  return a.topk <= 2 ? kPathLists : kPathPacked;
+  return (a.topk <= 2 || a.N <= 32) ? kPathLists : kPathPacked;
 }
 
 hipError_t run_topk(const TopkArgs& a) {
