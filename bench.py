@@ -181,13 +181,17 @@ def profile_one(args, q, k, v, dev) -> int:
             dense_attention_backward(q7, k7, v7, out_d, g7)
     elif name == "dense_small":
         # the memory-bound end of the configs[1] sweep: fp32 dense at B=1024,
-        # d=16, N=32 and N=64 (one call of each per step)
+        # d=16, N=32 and N=64 (one call of each per step), each beside the
+        # elementwise floor of the same bytes (torch.addcmul: reads q, k, v,
+        # writes one [B, N, d] tensor)
         fns = []
         for n in (32, 64):
             g = np.random.default_rng(1234 + 7 * n + D)
             qs, ks, vs = (torch.from_numpy(g.standard_normal((1024, n, D)).astype(np.float32))
                           .to(dev) for _ in range(3))
             fns.append(bound.dense(qs, ks, vs))
+            fl = torch.empty_like(qs)
+            fns.append(lambda qs=qs, ks=ks, vs=vs, fl=fl: torch.addcmul(qs, ks, vs, out=fl))
 
         def fn():
             for f in fns:
