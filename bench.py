@@ -410,7 +410,6 @@ def main() -> int:
     del fi, q7, k7, v7
 
     # ---- streaming top-k, B=256, N in {512, 1024}, fp32 and bf16
-    from tarmac.kernels import streaming_topk_attention
     b4 = 256
     for n4 in (512, 1024):
         g4 = np.random.default_rng(4242 if n4 == 1024 else 4242 + n4)
@@ -418,14 +417,16 @@ def main() -> int:
                  for _ in range(3)]
         for dt in (torch.float32, torch.bfloat16):
             q4, k4, v4 = (t.to(dt) for t in base4)
-            f4 = {"dense": lambda: fused_dense_attention(q4, k4, v4)}
+            # pre-bound C calls (tarmac_dense_fwd, tarmac_topk_stream_fwd: what
+            # fused_dense_attention / streaming_topk_attention call), so the
+            # event pair brackets the launch and not the Python wrapper
+            f4 = {"dense": bound.dense(q4, k4, v4)}
             for kk in KS:
-                # the API default key chunk (the largest that fits LDS), and
+                # the API default key chunk (0: the largest that fits LDS), and
                 # (fp32) the reference's 256-key tile
-                f4[f"stream_k{kk}"] = (lambda kk=kk: streaming_topk_attention(q4, k4, v4, kk))
+                f4[f"stream_k{kk}"] = bound.topk(q4, k4, v4, kk, key_chunk=0)
                 if dt == torch.float32:
-                    f4[f"stream_k{kk}_chunk256"] = (
-                        lambda kk=kk: streaming_topk_attention(q4, k4, v4, kk, block_n=256))
+                    f4[f"stream_k{kk}_chunk256"] = bound.topk(q4, k4, v4, kk, key_chunk=256)
             # each call is one launch: eager event timing is the device time of
             # that launch; graph replay (kept for reference) adds a fixed cost
             s4 = {n: harness.stats(s) for n, s in
