@@ -209,8 +209,11 @@ int tarmac_dense_bwd_noalloc(const float* q, const float* k, const float* v, con
                              int d, void* stream);
 
 /*
- * Which of three equally exact implementations serves topk <= 8 (the result
- * is identical whichever runs; only the time differs):
+ * Which of three equally exact implementations serves topk <= 8 (the retained
+ * set is identical whichever runs, and for fp32 the outputs too, bit for bit;
+ * for bf16 the outputs agree to bf16 rounding: the packed pass computes the
+ * softmax of a proven set on its truncated scores, within the proof's bound,
+ * the other paths on the canonical scores; only the time differs):
  *   packed   -- scores with the key's position in their low mantissa bits,
  *               lists of k+2 values kept with max / med3, a proof that the
  *               truncation (fp32) or the bf16 score error bound (bf16) cannot

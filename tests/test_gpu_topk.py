@@ -165,7 +165,8 @@ def test_headline_shape_properties():
 
 
 @pytest.mark.parametrize("N,d,kk", [(64, 16, 1), (256, 16, 2), (256, 32, 4), (512, 64, 2),
-                                    (100, 16, 3), (1024, 16, 1), (256, 64, 12)])
+                                    (100, 16, 3), (1024, 16, 1), (256, 64, 12), (6, 16, 2),
+                                    (32, 16, 5), (17, 16, 8), (48, 16, 2)])
 def test_topk_bf16(N, d, kk):
     from tarmac.kernels import topk_attention
     B = 8
@@ -202,7 +203,7 @@ def check_bf16_exact(q, k, v, kk, out, idx):
     assert np.abs(out - out_c).max() <= BF16_TOL * max(np.abs(out_c).max(), 1e-30)
 
 
-@pytest.mark.parametrize("N,d", [(64, 16), (256, 32), (300, 64)])
+@pytest.mark.parametrize("N,d", [(64, 16), (256, 32), (300, 64), (32, 16), (24, 16)])
 def test_topk_bf16_exact_with_ties(N, d):
     """bf16 with exact ties (duplicated keys, zero and repeated queries): the
     retained set and its order are the canonical oracle's, ties to the lower
@@ -234,7 +235,9 @@ def test_topk_bf16_configs2_exact(N, d, kk):
 
 
 @pytest.mark.parametrize("N,d,kk,chunk", [(256, 16, 1, 64), (256, 16, 2, 16), (512, 32, 2, 128),
-                                          (1024, 64, 2, 256), (700, 16, 3, 128), (1500, 16, 4, 256)])
+                                          (1024, 64, 2, 256), (700, 16, 3, 128), (1500, 16, 4, 256),
+                                          (64, 16, 2, 16), (32, 16, 4, 16), (64, 32, 2, 32),
+                                          (40, 64, 3, 16)])
 def test_streaming_topk_bf16_matches_fused_bitwise(N, d, kk, chunk):
     """bf16: the streamed kernel (key chunks) returns exactly the resident
     kernel's indices and outputs, on every bf16 selection path."""

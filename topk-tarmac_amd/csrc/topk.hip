@@ -380,24 +380,27 @@ topk_small_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __
   }
 }
 
-// fp32 rows of up to 64 keys (N * d <= 2048), k <= 8: the register-list
+// Rows of up to 64 keys (N * d <= 2048), k <= 8: the register-list
 // selection of topk_small_kernel with every operand fetched in one memory
-// round trip. The wave loads its query fragments and the 16-key K fragments
+// round trip. bf16 inputs are converted to fp32 on load, so the fp32 MFMA
+// chain gives their canonical fp32 scores and the lists select on those
+// exactly (the rule of every bf16 top-k path), with no rescoring. The wave loads its query fragments and the 16-key K fragments
 // straight from global memory (16 rows x 64 B per fragment, coalesced) and,
 // in the same burst, the batch row's V into LDS; selection then runs while the
 // LDS writes land, and the k value rows are gathered from LDS instead of a
 // second trip to memory. Selection and arithmetic are those of
 // topk_small_kernel, so the results are identical.
-template <int D, int K, int NT>
+template <typename T, int D, int K, int NT>
 __global__ void __launch_bounds__(64)
-topk_reg_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
-                const float* __restrict__ V, float* __restrict__ O, int32_t* __restrict__ Idx,
-                int N, int n_qblk, float scale, int nblocks) {
+topk_reg_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
+                T* __restrict__ O, int32_t* __restrict__ Idx, int N, int n_qblk, float scale,
+                int nblocks) {
   using F = Frag<float, D>;
   constexpr int QT = 2;
   constexpr int EO = D / 4;
-  constexpr int LDV = D + 4;                 // padded LDS value row
-  constexpr int NV = (NT * 16 * D / 4 + 63) / 64;  // float4 of V per lane
+  constexpr int LDV = D + 4;                 // padded LDS value row (fp32)
+  constexpr int VE = 16 / static_cast<int>(sizeof(T));  // elements per 16-byte vector
+  constexpr int NV = (NT * 16 * D / VE + 63) / 64;  // 16-byte vectors of V per lane
   constexpr bool POW2 = pow2_scale<D>();
   __shared__ __align__(16) float Vs[NT * 16 * LDV];
   const int lane = threadIdx.x;
@@ -407,29 +410,38 @@ topk_reg_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   const int col = lane & 15, grp = lane >> 4;
   const size_t boff = static_cast<size_t>(b) * N * D;
 
+  // query and key fragments as fp32 (bf16 widened exactly): lane group g
+  // holds elements g*D/4 .. g*D/4 + D/4 - 1 of its row, the MFMA chain's order
   F frag[QT];
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt)
-    frag[qt].load_q(Q + boff + static_cast<size_t>(min(q0 + 16 * qt + col, N - 1)) * D, grp,
-                    POW2 ? scale : 1.f);
+  for (int qt = 0; qt < QT; ++qt) {
+    ld_row<T, F::E>(frag[qt].q,
+                    Q + boff + static_cast<size_t>(min(q0 + 16 * qt + col, N - 1)) * D + grp * F::E);
+    if constexpr (POW2) {
+#pragma unroll
+      for (int e = 0; e < F::E; ++e) frag[qt].q[e] *= scale;
+    }
+  }
   typename F::KF kf[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
-    kf[t] = F::load_k(Kx + boff + static_cast<size_t>(min(16 * t + col, N - 1)) * D, grp);
-  f32x4 vr[NV];
-  const f32x4* vsrc = reinterpret_cast<const f32x4*>(V + boff);
-  const int nv4 = N * D / 4;
+    ld_row<T, F::E>(kf[t].v, Kx + boff + static_cast<size_t>(min(16 * t + col, N - 1)) * D + grp * F::E);
+  uint4 vr[NV];
+  const uint4* vsrc = reinterpret_cast<const uint4*>(V + boff);
+  const int nvv = N * D / VE;
 #pragma unroll
   for (int u = 0; u < NV; ++u) {
     const int e = lane + 64 * u;
-    vr[u] = e < nv4 ? vsrc[e] : f32x4{0.f, 0.f, 0.f, 0.f};
+    vr[u] = e < nvv ? vsrc[e] : make_uint4(0u, 0u, 0u, 0u);
   }
 #pragma unroll
   for (int u = 0; u < NV; ++u) {
     const int e = lane + 64 * u;
-    if (e < nv4) {
-      const int row = e / (D / 4), c4 = e - row * (D / 4);
-      *reinterpret_cast<f32x4*>(Vs + row * LDV + 4 * c4) = vr[u];
+    if (e < nvv) {
+      const int row = e / (D / VE), cv = e - row * (D / VE);
+      float x[VE];
+      ld_row<T, VE>(x, reinterpret_cast<const T*>(&vr[u]));
+      st_f32<VE>(Vs + row * LDV + VE * cv, x);
     }
   }
 
@@ -496,7 +508,7 @@ topk_reg_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
     const float inv = 1.f / den;
 #pragma unroll
     for (int c = 0; c < EO; ++c) acc[c] *= inv;
-    st_row<float, EO>(O + boff + static_cast<size_t>(qi) * D + grp * EO, acc);
+    st_row<T, EO>(O + boff + static_cast<size_t>(qi) * D + grp * EO, acc);
     if (Idx != nullptr && grp == 0) {
       int32_t* dst = Idx + (static_cast<size_t>(b) * N + qi) * K;
 #pragma unroll
@@ -914,18 +926,18 @@ static hipError_t launch_small(const TopkArgs& a, int kc) {
   return hipGetLastError();
 }
 
-template <int D, int NT>
+template <typename T, int D, int NT>
 static hipError_t launch_reg(const TopkArgs& a) {
   const int n_qblk = (a.N + 31) / 32;
   const int nblocks = a.B * n_qblk;
-  const float* q = static_cast<const float*>(a.q);
-  const float* k = static_cast<const float*>(a.k);
-  const float* v = static_cast<const float*>(a.v);
-  float* o = static_cast<float*>(a.out);
+  const T* q = static_cast<const T*>(a.q);
+  const T* k = static_cast<const T*>(a.k);
+  const T* v = static_cast<const T*>(a.v);
+  T* o = static_cast<T*>(a.out);
   hipStream_t st = static_cast<hipStream_t>(a.stream);
 #define TARMAC_TOPK_REG_CASE(KK)                                                                  \
   case KK:                                                                                        \
-    hipLaunchKernelGGL((topk_reg_kernel<D, KK, NT>), dim3(nblocks), dim3(64), 0, st, q, k, v, o,   \
+    hipLaunchKernelGGL((topk_reg_kernel<T, D, KK, NT>), dim3(nblocks), dim3(64), 0, st, q, k, v, o, \
                        a.idx, a.N, n_qblk, a.scale, nblocks);                                     \
     break;
   switch (a.topk) {
@@ -944,17 +956,25 @@ static hipError_t launch_reg(const TopkArgs& a) {
   return hipGetLastError();
 }
 
-// topk_reg_kernel's domain: fp32 rows of up to 64 keys with N * d <= 2048
-// (the V row block fits a lane's share of registers on its way to LDS), the
-// whole row resident (no explicit smaller key chunk).
-template <int D>
+// topk_reg_kernel's domain: rows of up to 64 keys with N * d <= 2048 (the V
+// row block fits a lane's share of registers on its way to LDS). fp32 honours
+// an explicit smaller key chunk (the LDS kernels give identical results);
+// bf16 ignores it, so a streamed bf16 call returns the resident call's
+// outputs bit for bit (the packed pass's softmax runs on its proof-bounded
+// scores, this kernel's on the canonical ones).
+static bool topk_reg_supported(const TopkArgs& a) {
+  return a.N <= 64 && a.N * a.d <= 2048 && (a.dtype == kBf16 || a.key_chunk >= a.N) &&
+         a.topk <= kTopkSmallMax && a.select == kSelTopk;
+}
+
+template <typename T, int D>
 static bool topk_reg(const TopkArgs& a, hipError_t* e) {
-  if (a.N > 64 || a.N * D > 2048 || a.key_chunk < a.N) return false;
+  if (!topk_reg_supported(a)) return false;
   switch ((a.N + 15) / 16) {
-    case 1: *e = launch_reg<D, 1>(a); return true;
-    case 2: *e = launch_reg<D, 2>(a); return true;
-    case 3: if constexpr (D <= 32) { *e = launch_reg<D, 3>(a); return true; } break;
-    case 4: if constexpr (D <= 32) { *e = launch_reg<D, 4>(a); return true; } break;
+    case 1: *e = launch_reg<T, D, 1>(a); return true;
+    case 2: *e = launch_reg<T, D, 2>(a); return true;
+    case 3: if constexpr (D <= 32) { *e = launch_reg<T, D, 3>(a); return true; } break;
+    case 4: if constexpr (D <= 32) { *e = launch_reg<T, D, 4>(a); return true; } break;
   }
   return false;
 }
@@ -1027,11 +1047,9 @@ static hipError_t dispatch_topk(const TopkArgs& a) {
   if constexpr (sizeof(T) == 4)
     if (topk_rule_lists(a)) return launch_small<T, D, true>(a, a.key_chunk);
   if (a.topk > kTopkSmallMax || a.select != kSelTopk) return launch_wide<T, D>(a);
-  if constexpr (sizeof(T) == 4) {
-    hipError_t e;
-    if (topk_reg<D>(a, &e)) return e;
-    return launch_small<T, D>(a, a.key_chunk);
-  }
+  hipError_t e;
+  if (topk_reg<T, D>(a, &e)) return e;
+  if constexpr (sizeof(T) == 4) return launch_small<T, D>(a, a.key_chunk);
   return hipErrorInvalidValue;  // bf16 k <= 8 runs the packed or filter kernels
 }
 
@@ -1056,8 +1074,10 @@ enum TopkPath { kPathPacked, kPathPackedSplit, kPathFilter, kPathLists };
 //     kernel wins at every k (rocprof, B=1024 N=32 k=4: 7.4 vs 7.8 packed).
 //   fp32, d = 8, 32, 64: register lists for k <= 2 (every k at N <= 32), packed above.
 //   bf16: packed, or the bf16 filter at d = 16 with k >= 4 and N >= 256
-//     (B=1024 N=256 k=4: 35.1 vs 40.4); the register lists do not serve bf16
-//     (their selection would run on the approximate bf16 scores).
+//     (B=1024 N=256 k=4: 35.1 vs 40.4); at d = 16, rows of up to 64 keys
+//     with k <= 2 and rows of up to 32 keys take the one-round-trip register
+//     lists, which widen bf16 to fp32 and select on the canonical scores
+//     directly.
 static TopkPath choose_path(const TopkArgs& a, int mode) {
   const bool filt = topk_filter_supported(a.dtype, a.d, a.topk);
   const bool split = packed_split_supported(a.dtype, a.d);
@@ -1068,7 +1088,14 @@ static TopkPath choose_path(const TopkArgs& a, int mode) {
     case kFilterPackedSplit: return split ? kPathPackedSplit : kPathPacked;
     default: break;
   }
-  if (a.dtype == kBf16) return (filt && a.topk >= 4 && a.N >= 256) ? kPathFilter : kPathPacked;
+  if (a.dtype == kBf16) {
+    // the one-round-trip lists (exact fp32 chain on the widened inputs) at
+    // d = 16 where they win: k <= 2, or every k at N <= 32 (B=4096 N=64 k=1:
+    // 11.5 vs 12.5 packed; N=32 k=1/4: 5.5/10.5 vs 8.0/12.2; at d = 32 the
+    // fp32 chain's 8 steps per tile lose: N=64 k=1 21.9 vs 16.6)
+    if (topk_reg_supported(a) && a.d == 16 && (a.topk <= 2 || a.N <= 32)) return kPathLists;
+    return (filt && a.topk >= 4 && a.N >= 256) ? kPathFilter : kPathPacked;
+  }
   if (split && a.N >= 256) return kPathPackedSplit;
   return (a.topk <= 2 || a.N <= 32) ? kPathLists : kPathPacked;
 }
