@@ -239,52 +239,59 @@ __device__ __forceinline__ float bf16_frag_norm2(const Frag<bf16, D>& f) {
   return n2 + __shfl_xor(n2, 32);
 }
 
-// The exact top-k lists of one 16-query tile (merged over the four lanes of
-// each query), in the canonical fp32 order: fp32 MFMA on the inputs converted
-// to fp32, per-score insertion with ties to the lower index. Keys come from
-// the LDS copy when it holds every key as plain rows of stride LDK (from_lds,
-// wave-uniform), otherwise from global memory.
-template <typename T, int D, int K, int LDK>
-__device__ __forceinline__ void exact_tile_plain(const T* __restrict__ Qb, const T* __restrict__ Kb,
-                                                 const T* Ks, bool from_lds, int N, int qbase,
+// The exact top K of one query's canonical fp32 scores (score desc, index
+// asc), by the whole wavefront. The MFMA runs with its operands' roles
+// swapped: the query fills every row of the A operand and 16 keys the
+// columns of B, so lane (col, g) receives the score of key kb + col (in all
+// four of its elements); the products and their order are those of the
+// canonical chain, so the scores are bit-identical. Lane row g keeps the
+// keys of every fourth tile (t % 4 == g), each lane in ascending key order,
+// and the lists merge in six xor steps, after which every lane holds the
+// result. Key fragments come from global memory (bf16 widened), TB tiles per
+// burst (16 VGPRs of fragments, at most four tiles). The fallback for a query whose packed or
+// filtered selection could not be proven: the other queries of its tile keep
+// their proven sets, and the row costs N / (16 TB) memory round trips instead
+// of one per 16-key tile.
+template <typename T, int D, int K>
+__device__ __forceinline__ void exact_query_topk(const T* __restrict__ Qb,
+                                                 const T* __restrict__ Kb, int N, int qi,
                                                  float scale, int lane, float (&val)[K],
                                                  int (&ix)[K]) {
   using F = Frag<float, D>;
   constexpr bool POW2 = pow2_scale<D>();
   constexpr int E = F::E;
+  constexpr int TB = E >= 16 ? 1 : (E >= 8 ? 2 : 4);  // 16-key tiles per burst (<= 16 VGPRs)
   const int col = lane & 15, grp = lane >> 4;
-  const int self = qbase + col;
-  F frag;
-  ld_row<T, E>(frag.q, Qb + static_cast<size_t>(min(self, N - 1)) * D + grp * E);
+  float qa[E];  // the query's elements g*E .. g*E+E-1, the same in every lane row
+  ld_row<T, E>(qa, Qb + static_cast<size_t>(qi) * D + grp * E);
   if constexpr (POW2) {
 #pragma unroll
-    for (int t = 0; t < E; ++t) frag.q[t] *= scale;
+    for (int i = 0; i < E; ++i) qa[i] *= scale;
   }
 #pragma unroll
   for (int m = 0; m < K; ++m) { val[m] = -INFINITY; ix[m] = kIdxSentinel; }
-  // rolled: this pass is rare, and its registers add to the caller's peak
+  const int nt = (N + 15) / 16;
 #pragma unroll 1
-  for (int kb = 0; kb < N; kb += 16) {
-    typename F::KF kf;
-    if (from_lds) {
-      // rows [N, 64 * ceil(N / 64)) of the copy are staged zero rows
-      ld_row<T, E>(kf.v, Ks + (kb + col) * LDK + grp * E);
-    } else {
-      ld_row<T, E>(kf.v, Kb + static_cast<size_t>(min(kb + col, N - 1)) * D + grp * E);
-    }
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  for (int t0 = 0; t0 < nt; t0 += TB) {
+    float kb[TB][E];
 #pragma unroll
-    for (int i = 0; i < F::NI; ++i) s = frag.step(kf, i, s);
+    for (int u = 0; u < TB; ++u)
+      ld_row<T, E>(kb[u], Kb + static_cast<size_t>(min(16 * (t0 + u) + col, N - 1)) * D + grp * E);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int key = kb + 4 * grp + r;
-      float v = POW2 ? s[r] : s[r] * scale;
-      if (key >= N || key == self) v = -INFINITY;
-      topk_insert<K>(val, ix, v, key);
+    for (int u = 0; u < TB; ++u) {
+      const int t = t0 + u;
+      if (t >= nt) break;  // uniform
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < E; ++i) acc = mfma_f32_16x16x4(qa[i], kb[u][i], acc);
+      const int j = 16 * t + col;
+      float v = POW2 ? acc[0] : acc[0] * scale;
+      if (j >= N || j == qi || (t & 3) != grp) v = -INFINITY;
+      topk_insert<K>(val, ix, v, j);
     }
   }
 #pragma unroll
-  for (int step = 16; step <= 32; step <<= 1) {
+  for (int step = 1; step < 64; step <<= 1) {
     float pv[K];
     int pi[K];
 #pragma unroll

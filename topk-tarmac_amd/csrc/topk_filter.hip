@@ -28,10 +28,10 @@
 //     k, so the result IS the exact top k. Rescoring one spare candidate
 //     settles near-ties between the k-th and (k+1)-th scores (duplicated keys
 //     included) without the fallback.
-//  3. fallback: a 16-query tile with any unproven query recomputes exactly
-//     (fp32 MFMA over all keys, read from the LDS copy when that holds them
-//     all exactly), so the result never depends on the filter -- only the
-//     time does.
+//  3. fallback: an unproven query is recomputed exactly by the whole wave
+//     (exact_query_topk: its row's canonical scores, per-lane lists, a
+//     six-step merge), so the result never depends on the filter -- only
+//     the time does.
 //
 // Reference behaviour: src/kernels/fused_topk_attention.py:211-333 and
 // src/kernels/streaming_topk_attention.py:66-258 (including the retained
@@ -119,65 +119,6 @@ struct FilterIn<bf16, D> {
 };
 
 // ---------------------------------------------------------------------------
-// exact fp32 pass for one query tile (fallback)
-// ---------------------------------------------------------------------------
-
-// The tile's exact top-k lists (merged over the four lanes of each query), in
-// the canonical fp32 order (fp32 MFMA on the inputs converted to fp32).
-// from_lds (wave-uniform): key rows are rebuilt from the rows resident in LDS
-// (all N keys, each rebuilt exactly); otherwise they come from global memory.
-template <typename T, int D, int K>
-__device__ __forceinline__ void exact_tile(const T* __restrict__ Qb, const T* __restrict__ Kb,
-                                           const bf16* Ks, bool from_lds, int N, int qbase,
-                                           float scale, int lane, float (&val)[K], int (&ix)[K]) {
-  using F = Frag<float, D>;
-  constexpr bool POW2 = pow2_scale<D>();
-  constexpr int E = F::E;
-  constexpr int LDK = FilterIn<T, D>::LDK;
-  const int col = lane & 15, grp = lane >> 4;
-  const int self = qbase + col;
-  F frag;
-  ld_row<T, E>(frag.q, Qb + static_cast<size_t>(min(self, N - 1)) * D + grp * E);
-  if constexpr (POW2) {
-#pragma unroll
-    for (int t = 0; t < E; ++t) frag.q[t] *= scale;
-  }
-#pragma unroll
-  for (int m = 0; m < K; ++m) { val[m] = -INFINITY; ix[m] = kIdxSentinel; }
-  for (int kb = 0; kb < N; kb += 16) {
-    typename F::KF kf;
-    if (from_lds) {
-      // rows [N, 16 * ceil(N / 16)) are staged zero rows
-      FilterIn<T, D>::template row_f32<E>(kf.v, Ks + (kb + col) * LDK, grp * E);
-    } else {
-      ld_row<T, E>(kf.v, Kb + static_cast<size_t>(min(kb + col, N - 1)) * D + grp * E);
-    }
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < F::NI; ++i) s = frag.step(kf, i, s);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int key = kb + 4 * grp + r;
-      float v = POW2 ? s[r] : s[r] * scale;
-      if (key >= N || key == self) v = -INFINITY;
-      topk_insert<K>(val, ix, v, key);
-    }
-  }
-#pragma unroll
-  for (int step = 16; step <= 32; step <<= 1) {
-    float pv[K];
-    int pi[K];
-#pragma unroll
-    for (int m = 0; m < K; ++m) {
-      pv[m] = __shfl_xor(val[m], step);
-      pi[m] = __shfl_xor(ix[m], step);
-    }
-#pragma unroll
-    for (int m = 0; m < K; ++m) topk_insert_lex<K>(val, ix, pv[m], pi[m]);
-  }
-}
-
-// ---------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------
 
@@ -248,7 +189,6 @@ topk_filter_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
   extern __shared__ __align__(16) unsigned char smem_raw[];
   bf16* Ks = reinterpret_cast<bf16*>(smem_raw + 16);
   unsigned* kmax_slot = reinterpret_cast<unsigned*>(smem_raw);      // max |k|^2 of the chunk
-  unsigned* inexact_slot = kmax_slot + 1;  // some staged element is not rebuilt exactly
 
   const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -289,21 +229,14 @@ topk_filter_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
     const int cn = min(kc, N - c0);
     const int cnb = (cn + kBlockKeys - 1) / kBlockKeys * kBlockKeys;
     __syncthreads();
-    if (threadIdx.x == 0) {
-      *kmax_slot = 0u;
-      *inexact_slot = 0u;
-    }
-    bool exact = true;
+    if (threadIdx.x == 0) *kmax_slot = 0u;
+    bool exact = true;  // (whether the LDS rows rebuild the inputs exactly: not needed here)
     const float mine = FI::stage(Ks, Kb + static_cast<size_t>(c0) * D, cn, cnb, exact);
     // one LDS atomic per wave (a per-lane atomic compiles to a 64-step
     // readlane loop); non-negative floats order like their bits
     const float wmax = wave_max_rows(mine);
-    const bool wexact = __all(exact);
     __syncthreads();
-    if (lane == 0) {
-      atomicMax(kmax_slot, __float_as_uint(wmax));
-      if (!wexact) atomicOr(inexact_slot, 1u);
-    }
+    if (lane == 0) atomicMax(kmax_slot, __float_as_uint(wmax));
     if (q0 < N) {
       const int kend = c0 + cn;
       for (int kb0 = 0; kb0 < cnb; kb0 += 16 * BT) {
@@ -344,7 +277,6 @@ topk_filter_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
   }
   if (q0 >= N) return;
   // the exact fallback may rebuild keys from LDS: one chunk holds them all
-  const bool lds_exact = ONESEG && *inexact_slot == 0u;
 
   // ---- merge the four lane lists of each query ---------------------------
   // cand: the k+1 candidates (identical on the four lanes of a query;
@@ -436,10 +368,22 @@ topk_filter_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
     ok[qt] = self[qt] >= N || (nprod < kNormLimit && bound < val[qt][K - 1]);
   }
 
+  // unproven queries: recomputed exactly one at a time across the whole wave
+  // (the tile's proven queries keep their sets)
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    if (!__all(ok[qt]))
-      exact_tile<T, D, K>(Qb, Kb, Ks, lds_exact, N, q0 + 16 * qt, scale, lane, val[qt], ix[qt]);
+    unsigned long long todo = __ballot(grp == 0 && !ok[qt]);
+    while (todo != 0ull) {
+      const int c = __builtin_ctzll(todo);
+      todo &= todo - 1ull;
+      float ev[K];
+      int ei[K];
+      exact_query_topk<T, D, K>(Qb, Kb, N, q0 + 16 * qt + c, scale, lane, ev, ei);
+      if (col == c) {
+#pragma unroll
+        for (int m = 0; m < K; ++m) { val[qt][m] = ev[m]; ix[qt][m] = ei[m]; }
+      }
+    }
   }
 
   // ---- k-softmax and gathered aggregation --------------------------------

@@ -34,9 +34,10 @@
 //  4. rescore: the K winners are rescored in the canonical fp32 order (their
 //     softmax weights are then bit-for-bit those of the oracle's scores) and
 //     sorted by (score desc, index asc).
-//  5. fallback: a 16-query tile with an unproven query recomputes exactly
-//     (fp32 MFMA over every key, per-score insertion) -- the result never
-//     depends on the packing, only the time does.
+//  5. fallback: an unproven query is recomputed exactly by the whole wave
+//     (exact_query_topk: its row's canonical scores, per-lane lists, a
+//     six-step merge) -- the result never depends on the packing, only the
+//     time does.
 //  6. k-softmax and the gathered aggregation over the K value rows.
 #include "exact.hpp"
 #include "frag.hpp"
@@ -295,7 +296,7 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
     }
   }
   if (q0 >= N) return;
-  // the fallback may read keys from LDS: one chunk holds them all
+  // rescoring may read keys from LDS: one chunk holds them all
   const bool lds_all = kc >= N;
 
   // ---- merge the four lane lists of each query ---------------------------
@@ -455,21 +456,30 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
     }
   }
   // ---- k-softmax and gathered aggregation --------------------------------
-  // Proven tiles finish first; unproven tiles are recomputed exactly at the
-  // very end, where little else is live, so the rare exact pass does not raise
-  // the kernel's register count (and cost waves per SIMD).
+  // Proven tiles finish first; a tile's unproven queries are recomputed
+  // exactly at the very end, one at a time across the whole wave, where
+  // little else is live, so the rare exact pass does not raise the kernel's
+  // register count (and cost waves per SIMD).
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt)
     if (__all(ok[qt])) finish_tile<T, D, K>(V, O, Idx, b, N, q0 + 16 * qt + col, grp, val[qt], ix[qt]);
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     if (!__all(ok[qt])) {
-      float ev[K];
-      int ei[K];
-      // split rows in LDS do not serve the exact pass: it reads global rows then
-      exact_tile_plain<T, D, K, LDK>(Qb, Kb, reinterpret_cast<const T*>(Ks), lds_all && !SPLIT, N,
-                                     q0 + 16 * qt, scale, lane, ev, ei);
-      finish_tile<T, D, K>(V, O, Idx, b, N, q0 + 16 * qt + col, grp, ev, ei);
+      // one bit per unproven query (its lane in row 0 stands for it)
+      unsigned long long todo = __ballot(grp == 0 && !ok[qt]);
+      while (todo != 0ull) {
+        const int c = __builtin_ctzll(todo);
+        todo &= todo - 1ull;
+        float ev[K];
+        int ei[K];
+        exact_query_topk<T, D, K>(Qb, Kb, N, q0 + 16 * qt + c, scale, lane, ev, ei);
+        if (col == c) {
+#pragma unroll
+          for (int m = 0; m < K; ++m) { val[qt][m] = ev[m]; ix[qt][m] = ei[m]; }
+        }
+      }
+      finish_tile<T, D, K>(V, O, Idx, b, N, q0 + 16 * qt + col, grp, val[qt], ix[qt]);
     }
   }
 }
