@@ -410,6 +410,7 @@ def main() -> int:
     del fi, q7, k7, v7
 
     # ---- streaming top-k, B=256, N in {512, 1024}, fp32 and bf16
+    from tarmac.kernels import streaming_topk_attention
     b4 = 256
     for n4 in (512, 1024):
         g4 = np.random.default_rng(4242 if n4 == 1024 else 4242 + n4)
@@ -438,10 +439,18 @@ def main() -> int:
                 {f"ratio_k{kk}": round(s4[f"stream_k{kk}"]["min_us"] / s4["dense"]["min_us"], 4)
                  for kk in KS})
             if dt == torch.float32 and n4 == 1024:
+                # graphs capture the Python entry points, which launch on the
+                # current (capturing) stream; a pre-bound call keeps the stream
+                # it was bound to and would fall outside the capture
+                fw = {"dense": lambda: fused_dense_attention(q4, k4, v4)}
+                for kk in KS:
+                    fw[f"stream_k{kk}"] = (lambda kk=kk: streaming_topk_attention(q4, k4, v4, kk))
+                    fw[f"stream_k{kk}_chunk256"] = (
+                        lambda kk=kk: streaming_topk_attention(q4, k4, v4, kk, block_n=256))
                 s4g = {n: harness.stats(s) for n, s in
-                       harness.time_interleaved(harness.as_graphs(f4), args.reps, 5, 2).items()}
+                       harness.time_interleaved(harness.as_graphs(fw), args.reps, 5, 2).items()}
                 detail[key]["graph_us"] = {n: round(s["min_us"], 3) for n, s in s4g.items()}
-                detail[key]["graph_nodes_per_call"] = harness.graph_node_counts(f4["stream_k2"])
+                detail[key]["graph_nodes_per_call"] = harness.graph_node_counts(fw["stream_k2"])
             del q4, k4, v4, f4
         del base4
 
