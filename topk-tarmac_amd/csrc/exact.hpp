@@ -247,15 +247,17 @@ __device__ __forceinline__ float bf16_frag_norm2(const Frag<bf16, D>& f) {
 // canonical chain, so the scores are bit-identical. Lane row g keeps the
 // keys of every fourth tile (t % 4 == g), each lane in ascending key order,
 // and the lists merge in six xor steps, after which every lane holds the
-// result. Key fragments come from global memory (bf16 widened), TB tiles per
-// burst (16 VGPRs of fragments, at most four tiles). The fallback for a query whose packed or
+// result. Key fragments come TB tiles per burst (16 VGPRs of fragments, at
+// most four tiles) from global memory or, where the kernel holds the whole
+// row as plain rows, from LDS (bf16 widened). The fallback for a query whose packed or
 // filtered selection could not be proven: the other queries of its tile keep
 // their proven sets, and the row costs N / (16 TB) memory round trips instead
 // of one per 16-key tile.
-template <typename T, int D, int K>
-__device__ __forceinline__ void exact_query_topk(const T* __restrict__ Qb,
-                                                 const T* __restrict__ Kb, int N, int qi,
-                                                 float scale, int lane, float (&val)[K],
+// load_k(dst, row, g): elements g*E .. g*E+E-1 of key row `row` as fp32 (a
+// global row, or a plain row of the LDS copy).
+template <typename T, int D, int K, typename LoadK>
+__device__ __forceinline__ void exact_query_topk(const T* __restrict__ Qb, LoadK load_k, int N,
+                                                 int qi, float scale, int lane, float (&val)[K],
                                                  int (&ix)[K]) {
   using F = Frag<float, D>;
   constexpr bool POW2 = pow2_scale<D>();
@@ -276,7 +278,7 @@ __device__ __forceinline__ void exact_query_topk(const T* __restrict__ Qb,
     float kb[TB][E];
 #pragma unroll
     for (int u = 0; u < TB; ++u)
-      ld_row<T, E>(kb[u], Kb + static_cast<size_t>(min(16 * (t0 + u) + col, N - 1)) * D + grp * E);
+      load_k(kb[u], min(16 * (t0 + u) + col, N - 1), grp);
 #pragma unroll
     for (int u = 0; u < TB; ++u) {
       const int t = t0 + u;
@@ -302,6 +304,18 @@ __device__ __forceinline__ void exact_query_topk(const T* __restrict__ Qb,
 #pragma unroll
     for (int m = 0; m < K; ++m) topk_insert_lex<K>(val, ix, pv[m], pi[m]);
   }
+}
+
+// exact_query_topk with the keys read from global memory.
+template <typename T, int D, int K>
+__device__ __forceinline__ void exact_query_topk_global(const T* __restrict__ Qb,
+                                                        const T* __restrict__ Kb, int N, int qi,
+                                                        float scale, int lane, float (&val)[K],
+                                                        int (&ix)[K]) {
+  constexpr int E = D / 4;
+  exact_query_topk<T, D, K>(
+      Qb, [&](float (&dst)[E], int row, int g) { ld_row<T, E>(dst, Kb + static_cast<size_t>(row) * D + g * E); },
+      N, qi, scale, lane, val, ix);
 }
 
 }  // namespace tarmac

@@ -378,7 +378,7 @@ topk_filter_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
       todo &= todo - 1ull;
       float ev[K];
       int ei[K];
-      exact_query_topk<T, D, K>(Qb, Kb, N, q0 + 16 * qt + c, scale, lane, ev, ei);
+      exact_query_topk_global<T, D, K>(Qb, Kb, N, q0 + 16 * qt + c, scale, lane, ev, ei);
       if (col == c) {
 #pragma unroll
         for (int m = 0; m < K; ++m) { val[qt][m] = ev[m]; ix[qt][m] = ei[m]; }

@@ -473,7 +473,15 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
         todo &= todo - 1ull;
         float ev[K];
         int ei[K];
-        exact_query_topk<T, D, K>(Qb, Kb, N, q0 + 16 * qt + c, scale, lane, ev, ei);
+        // plain rows of the whole row in LDS serve it there (split rows do not)
+        const bool from_lds = lds_all && !SPLIT;  // uniform
+        exact_query_topk<T, D, K>(
+            Qb,
+            [&](float (&dst)[D / 4], int row, int g) {
+              if (from_lds) ld_row<T, D / 4>(dst, reinterpret_cast<const T*>(Ks) + row * LDK + g * (D / 4));
+              else ld_row<T, D / 4>(dst, Kb + static_cast<size_t>(row) * D + g * (D / 4));
+            },
+            N, q0 + 16 * qt + c, scale, lane, ev, ei);
         if (col == c) {
 #pragma unroll
           for (int m = 0; m < K; ++m) { val[qt][m] = ev[m]; ix[qt][m] = ei[m]; }
