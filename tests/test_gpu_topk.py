@@ -137,6 +137,22 @@ def test_exact_ties_keep_lower_index():
         assert idx[:, 0].tolist() == [list(range(1, kk + 1))] * B
 
 
+@pytest.mark.parametrize("N,d", [(256, 32), (300, 64), (200, 8)])
+def test_exact_ties_fp32_wide_heads(N, d):
+    """fp32 at d = 8, 32, 64 (the packed pass on fp32 MFMA scores for k >= 3):
+    duplicated keys and zero queries leave the packed proof unsettled, and
+    the per-query exact pass (key rows from the LDS copy) must return the
+    canonical sets, ties to the lower index."""
+    B = 3
+    q, k, v = qkv(31 + N + d, B, N, d)
+    k[:, 1::2] = k[:, 0::2]
+    q[:, :6] = 0.0
+    for kk in (3, 4, 8):
+        out, idx = run_topk(q, k, v, kk)
+        check_f32(q, k, v, kk, out, idx)
+        assert idx[:, 0].tolist() == [list(range(1, kk + 1))] * B
+
+
 def test_topk_clamp_and_default_tiling():
     from tarmac.kernels import (fused_topk_attention, fused_topk_attention_tiled,
                                 streaming_topk_attention)
