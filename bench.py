@@ -671,7 +671,13 @@ def main() -> int:
     line["detail"] = detail
     line["device_probes"] = harness.device_probes(dev)
     line["device"] = torch.cuda.get_device_name(dev)
-    line["host"] = {"cpu": platform.processor() or platform.machine(),
+    cpu = platform.processor() or platform.machine()
+    try:  # the model name, not the architecture
+        with open("/proc/cpuinfo") as f:
+            cpu = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), cpu)
+    except OSError:
+        pass
+    line["host"] = {"cpu": cpu, "arch": platform.machine(),
                     "affinity_cores": len(os.sched_getaffinity(0))}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
