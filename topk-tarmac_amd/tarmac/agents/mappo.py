@@ -268,7 +268,10 @@ class AttentionComm(nn.Module):
         B, N, _ = x.shape
         mode = self.cfg.attn_mode
         qkv = self.qkv(x)
-        q, k, v = (t.contiguous() for t in qkv.chunk(3, dim=-1))
+        # one copy into a [3, B, N, m] buffer: q, k and v are then contiguous
+        # views (three .contiguous() chunks would be three launches)
+        m = qkv.shape[-1] // 3
+        q, k, v = qkv.view(B, N, 3, m).permute(2, 0, 1, 3).contiguous().unbind(0)
 
         if mode == "entmax":
             msg, info = self._entmax(q, k, v, N)
