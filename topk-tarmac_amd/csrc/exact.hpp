@@ -273,6 +273,26 @@ __device__ __forceinline__ void exact_query_topk(const T* __restrict__ Qb, LoadK
 #pragma unroll
   for (int m = 0; m < K; ++m) { val[m] = -INFINITY; ix[m] = kIdxSentinel; }
   const int nt = (N + 15) / 16;
+  if constexpr (TB == 1) {
+    // one-tile bursts (D = 64): the next tile's fragment is in flight during
+    // this tile's MFMAs (a second buffer here does not raise the kernel's
+    // VGPR count, as it would for the multi-tile bursts of D <= 32)
+    float kb[E], kn[E];
+    load_k(kb, min(col, N - 1), grp);
+#pragma unroll 1
+    for (int t = 0; t < nt; ++t) {
+      load_k(kn, min(16 * (t + 1) + col, N - 1), grp);  // clamped: always a valid row
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < E; ++i) acc = mfma_f32_16x16x4(qa[i], kb[i], acc);
+      const int j = 16 * t + col;
+      float v = POW2 ? acc[0] : acc[0] * scale;
+      if (j >= N || j == qi || (t & 3) != grp) v = -INFINITY;
+      topk_insert<K>(val, ix, v, j);
+#pragma unroll
+      for (int i = 0; i < E; ++i) kb[i] = kn[i];
+    }
+  } else {
 #pragma unroll 1
   for (int t0 = 0; t0 < nt; t0 += TB) {
     float kb[TB][E];
@@ -291,6 +311,7 @@ __device__ __forceinline__ void exact_query_topk(const T* __restrict__ Qb, LoadK
       if (j >= N || j == qi || (t & 3) != grp) v = -INFINITY;
       topk_insert<K>(val, ix, v, j);
     }
+  }
   }
 #pragma unroll
   for (int step = 1; step < 64; step <<= 1) {
