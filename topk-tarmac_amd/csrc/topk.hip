@@ -1073,8 +1073,8 @@ enum TopkPath { kPathPacked, kPathPackedSplit, kPathFilter, kPathLists };
 //     17.9 vs 19.9 lists), except at N <= 32, where the one-round-trip list
 //     kernel wins at every k (rocprof, B=1024 N=32 k=4: 7.4 vs 7.8 packed).
 //   fp32, d = 8, 32, 64: register lists for k <= 2 (every k at N <= 32), packed above.
-//   bf16: packed, or the bf16 filter at d = 16 with k >= 4 and N >= 256
-//     (B=1024 N=256 k=4: 35.1 vs 40.4); at d = 16, rows of up to 64 keys
+//   bf16: packed, or the bf16 filter at d = 16 with N >= 256 and k >= 4
+//     (B=1024 N=256 k=4: 35.1 vs 40.4) or k = 2, 3 with B <= 1024; at d = 16, rows of up to 64 keys
 //     with k <= 2 and rows of up to 32 keys take the one-round-trip register
 //     lists, which widen bf16 to fp32 and select on the canonical scores
 //     directly.
@@ -1094,7 +1094,13 @@ static TopkPath choose_path(const TopkArgs& a, int mode) {
     // 11.5 vs 12.5 packed; N=32 k=1/4: 5.5/10.5 vs 8.0/12.2; at d = 32 the
     // fp32 chain's 8 steps per tile lose: N=64 k=1 21.9 vs 16.6)
     if (topk_reg_supported(a) && a.d == 16 && (a.topk <= 2 || a.N <= 32)) return kPathLists;
-    return (filt && a.topk >= 4 && a.N >= 256) ? kPathFilter : kPathPacked;
+    // k = 2, 3 up to B = 1024: the filter's proof leaves fewer queries to the
+    // per-query exact pass, whose tail sets the time of a launch this small
+    // (B=32 N=512 k=2/3: 9.4/10.3 vs 15.7/18.5 packed; B=32 N=1024 k=3: 15.2
+    // vs 30.9; B=256 N=256 k=2/3: 9.3/10.4 vs 11.0/12.9); at B = 4096 the
+    // packed scan's lower cost per score wins (N=512 k=2: 234.9 vs 242.5)
+    if (filt && a.N >= 256 && (a.topk >= 4 || (a.topk >= 2 && a.B <= 1024))) return kPathFilter;
+    return kPathPacked;
   }
   if (split && a.N >= 256) return kPathPackedSplit;
   return (a.topk <= 2 || a.N <= 32) ? kPathLists : kPathPacked;
