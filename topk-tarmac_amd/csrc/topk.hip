@@ -1065,10 +1065,11 @@ enum TopkPath { kPathPacked, kPathPackedSplit, kPathFilter, kPathLists };
 // The implementation for k <= 8 (all return identical results). Automatic
 // choice from interleaved timings on MI355X (B = 1024 for fp32 d = 16, the
 // configs[1] sweep; the configs[2] bf16 grid), us:
-//   fp32, d = 16: the packed pass on split-bf16 scores from N = 256 (N=256
+//   fp32, d = 16: the packed pass on split-bf16 scores from N = 160, and
+//     at N = 128 for k >= 3 with B >= 1024 (see choose_path) (N=256
 //     k=1: 28.4 vs lists 30.4; k=2: 31.1 vs 37.1 lists, 34.5 filter; k=4:
 //     38.1 vs 44.1 filter, 56.5 lists; N=512 k=2: 83.5 vs 96.2 filter, 117.4
-//     lists); below N = 256 the register lists for k <= 2 (N=64 k=1: 5.9 vs
+//     lists); below that the register lists for k <= 2 (N=64 k=1: 5.9 vs
 //     6.7 packed, 9.2 split) and the fp32-MFMA packed pass above (N=128 k=4:
 //     17.9 vs 19.9 lists), except at N <= 32, where the one-round-trip list
 //     kernel wins at every k (rocprof, B=1024 N=32 k=4: 7.4 vs 7.8 packed).
@@ -1102,7 +1103,11 @@ static TopkPath choose_path(const TopkArgs& a, int mode) {
     if (filt && a.N >= 256 && (a.topk >= 4 || (a.topk >= 2 && a.B <= 1024))) return kPathFilter;
     return kPathPacked;
   }
-  if (split && a.N >= 256) return kPathPackedSplit;
+  // split-bf16 scores from N = 160 at any k (B=1024 N=192 k=2/4: 26.0/32.3
+  // vs 28.0 lists / 36.3 packed; B=4096 N=192 k=4: 111.2 vs 126.9), and at
+  // N = 128 for k >= 3 once B >= 1024 (B=4096 N=128 k=3/4: 45.3/52.1 vs
+  // 47.0/53.6 packed; k = 2 stays on the lists there, 39.4 vs 40.4)
+  if (split && (a.N >= 160 || (a.N >= 128 && a.B >= 1024 && a.topk >= 3))) return kPathPackedSplit;
   return (a.topk <= 2 || a.N <= 32) ? kPathLists : kPathPacked;
 }
 
