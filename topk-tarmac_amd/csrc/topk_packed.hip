@@ -516,9 +516,8 @@ static void launch_packed_k(const TopkArgs& a, int kc, int nblocks, int n_qblk, 
                      a.scale, nblocks);
 }
 
-template <typename T, int D, int K, bool SPLIT>
-static hipError_t launch_packed_shape(const TopkArgs& a) {
-  constexpr int QT = kTopkQueryTiles;
+template <typename T, int D, int K, int QT, bool SPLIT>
+static hipError_t launch_packed_shape_q(const TopkArgs& a) {
   constexpr int NS = kPackedSubLists;
   const int per_wave = 16 * QT;
   const int waves = (a.N + per_wave - 1) / per_wave;
@@ -543,6 +542,10 @@ static hipError_t launch_packed_shape(const TopkArgs& a) {
       return hipGetLastError();
     }
   }
+  if constexpr (QT == 1) {  // chosen for rows of up to 1024 keys only
+    launch_packed_k<T, D, K, QT, NS, 10, true, SPLIT>(a, kc, nblocks, n_qblk, nw, lds);
+    return hipGetLastError();
+  } else {
   // a row of up to 1024 keys is one segment of 10-bit fields whether it is
   // resident or streamed in chunks (the fields hold absolute keys): the
   // lists stay packed across chunks, with no per-chunk flush to (score, key)
@@ -553,6 +556,20 @@ static hipError_t launch_packed_shape(const TopkArgs& a) {
   else
     launch_packed_k<T, D, K, QT, NS, 10, false, SPLIT>(a, kc, nblocks, n_qblk, nw, lds);
   return hipGetLastError();
+  }
+}
+
+// Two query tiles per wave halve the per-query staging and merge overhead,
+// but a batch too small to give every SIMD a wave that way (B * N / 32 below
+// 4 * kCUs) leaves SIMDs idle: one tile per wave then doubles the waves
+// (k <= 4, which keeps the build's kernel count down).
+template <typename T, int D, int K, bool SPLIT>
+static hipError_t launch_packed_shape(const TopkArgs& a) {
+  if constexpr (K <= 4) {
+    const long waves2 = static_cast<long>(a.B) * ((a.N + 31) / 32);
+    if (a.N <= 1024 && waves2 < 4L * kCUs) return launch_packed_shape_q<T, D, K, 1, SPLIT>(a);
+  }
+  return launch_packed_shape_q<T, D, K, kTopkQueryTiles, SPLIT>(a);
 }
 
 template <typename T, int D, bool SPLIT>
