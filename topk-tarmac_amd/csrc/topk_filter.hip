@@ -424,9 +424,8 @@ size_t topk_filter_lds_bytes(int dtype, int d, int kc) {
   return 16 + static_cast<size_t>(kcb) * row * sizeof(bf16);
 }
 
-template <typename T, int D>
-static hipError_t launch_filter(const TopkArgs& a, int kc) {
-  constexpr int QT = kTopkQueryTiles;
+template <typename T, int D, int QT>
+static hipError_t launch_filter_q(const TopkArgs& a, int kc) {
   const int per_wave = 16 * QT;
   const int waves = (a.N + per_wave - 1) / per_wave;
   // up to N = 256 the 28 KiB key copy is small: four-wave groups keep five
@@ -470,6 +469,17 @@ static hipError_t launch_filter(const TopkArgs& a, int kc) {
   }
 #undef TARMAC_FILTER_CASE
   return hipGetLastError();
+}
+
+// bf16 batches too small to give every SIMD a wave at two query tiles per
+// wave (B * N / 32 below 4 * kCUs) take one tile per wave: twice the waves.
+template <typename T, int D>
+static hipError_t launch_filter(const TopkArgs& a, int kc) {
+  if constexpr (sizeof(T) == 2) {
+    const long waves2 = static_cast<long>(a.B) * ((a.N + 31) / 32);
+    if (waves2 < 4L * kCUs) return launch_filter_q<T, D, 1>(a, kc);
+  }
+  return launch_filter_q<T, D, kTopkQueryTiles>(a, kc);
 }
 
 // fp32: d = 16, 32, 64. bf16: d = 16 only, where one bf16 product per score
