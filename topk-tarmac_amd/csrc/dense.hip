@@ -373,13 +373,8 @@ static bool dense_reg(const DenseArgs& a, hipError_t* e) {
   return false;
 }
 
-template <typename T, int D>
-static hipError_t launch_dense(const DenseArgs& a) {
-  if constexpr (sizeof(T) == 4) {
-    hipError_t e;
-    if (dense_reg<D>(a, &e)) return e;
-  }
-  constexpr int QT = kDenseQueryTiles;
+template <typename T, int D, int QT>
+static hipError_t launch_dense_q(const DenseArgs& a) {
   const int per_wave = 16 * QT;
   const int waves = (a.N + per_wave - 1) / per_wave;
   const int nw = waves >= 4 ? 4 : waves;
@@ -392,6 +387,19 @@ static hipError_t launch_dense(const DenseArgs& a) {
                      static_cast<const T*>(a.k), static_cast<const T*>(a.v), static_cast<T*>(a.out),
                      a.stats, a.N, n_qblk, a.key_chunk, a.scale, nblocks);
   return hipGetLastError();
+}
+
+// A batch too small to give every SIMD a wave at two query tiles per wave
+// (B * N / 32 below 4 * kCUs) takes one tile per wave: twice the waves.
+template <typename T, int D>
+static hipError_t launch_dense(const DenseArgs& a) {
+  if constexpr (sizeof(T) == 4) {
+    hipError_t e;
+    if (dense_reg<D>(a, &e)) return e;
+  }
+  const long waves2 = static_cast<long>(a.B) * ((a.N + 31) / 32);
+  if (waves2 < 4L * kCUs) return launch_dense_q<T, D, 1>(a);
+  return launch_dense_q<T, D, kDenseQueryTiles>(a);
 }
 
 size_t dense_lds_bytes(int dtype, int d, int kc) {
