@@ -7,7 +7,11 @@ B=1024 episodes, N=256 agents, d=16, fp32, Q/K/V ~ N(0, 1) drawn on the CPU
 from seed 1234 + 7N + d (scripts/bench_attention_core.py:341) and copied to
 HBM before timing. A "step" is one call of the fused score-then-select top-k
 core at k=2 over the whole batch (scores, selection, k-softmax, gathered
-aggregation). ``value`` is its device time per call in microseconds.
+aggregation). ``value`` is its device time per call in microseconds: after a
+time-based pre-warm (the clock ramp), the K calls run as one replay of a
+graph that holds them back to back, under one event pair on the launch
+stream. Beside it: the same K calls launched eagerly, and the configs[1]
+call with its int32 retained indices [B, N, k] written too.
 
 Alongside, with the reference's protocol (interleaved event timing and graph
 replay, minimum over samples): the dense core, top-k at k=1/2/4, the fixed-set
@@ -220,13 +224,73 @@ def profile_one(args, q, k, v, dev) -> int:
     return 0
 
 
+def _prewarm(fn, ms: float) -> dict:
+    """Call ``fn`` for at least ``ms`` milliseconds of wall time (untimed),
+    synchronising every 64 calls so the device is kept busy without an
+    unbounded queue. Returns the time spent and the calls made."""
+    import torch
+    t0 = time.perf_counter()
+    calls = 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(64):
+            fn()
+        calls += 64
+        torch.cuda.synchronize()
+    return {"ms": (time.perf_counter() - t0) * 1e3, "calls": calls}
+
+
+def _graph_of_calls(make_bound, calls: int):
+    """A graph holding ``calls`` launches of one pre-bound call. The call is
+    bound inside the capture, so it launches on the capturing stream."""
+    import torch
+    with torch.no_grad():
+        g = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            fn = make_bound()
+            for _ in range(calls):
+                fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def _replay_us(graph, calls: int) -> float:
+    """Device time per call of one replay of a graph of ``calls`` launches."""
+    import torch
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(st)
+    graph.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / calls
+
+
+def _eager_us(fn, calls: int) -> float:
+    """Device time per call of ``calls`` eager launches under one event pair
+    on the stream ``fn`` is bound to (host launch gaps included)."""
+    import torch
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(st)
+    for _ in range(calls):
+        fn()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / calls
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     # the device needs some tens of milliseconds of sustained load to reach its
-    # working clock (a cold start reads ~20% slow): 3000 untimed calls (~0.1 s)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=3000)
+    # working clock (a cold start reads ~20% slow): an untimed, time-based
+    # pre-warm runs before the timed region whatever --warmup is
+    ap.add_argument("--prewarm-ms", type=float, default=300.0)
     ap.add_argument("--reps", type=int, default=40, help="interleaved repetitions per run")
     ap.add_argument("--runs", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -269,27 +333,45 @@ def main() -> int:
         return profile_one(args, q, k, v, dev)
 
     # ---- timed region: K steps of the value kernel -----------------------
+    # The device reaches its working clock only after some tens of
+    # milliseconds of sustained load, so a time-based pre-warm of
+    # --prewarm-ms runs first whatever --warmup is (a short driver run would
+    # otherwise time a cold clock). The K calls are captured once into one
+    # graph (capture is not timed) and replayed once between the events on
+    # the launch stream: the replay holds the K launches back to back with no
+    # host launch gaps, so the average is the device time per call.
+    prewarm = _prewarm(bound.topk(q, k, v, VALUE_K), args.prewarm_ms)
     step = bound.topk(q, k, v, VALUE_K)
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    # one event pair on the launch stream brackets the K launches: the
-    # average is device time per call, launch gaps included
+    graph = _graph_of_calls(lambda: bound.topk(q, k, v, VALUE_K), args.steps)
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _prewarm(step, 50.0)  # the clock stays up across the capture
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0.record(st)
-    for _ in range(args.steps):
-        step()
+    graph.replay()
     e1.record(st)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     kernel_ms = e0.elapsed_time(e1) / args.steps
     ms_per_step = (t1 - t0) * 1e3 / args.steps
+    del graph
+
+    # the same K calls launched eagerly one by one (host launch gaps
+    # included), and the configs[1] call as BASELINE.json writes it: output
+    # plus the retained indices [B, N, k] int32 (4 B N k more bytes)
+    eager_us = _eager_us(step, args.steps)
+    step_idx = bound.topk(q, k, v, VALUE_K, with_idx=True)
+    gi = _graph_of_calls(lambda: bound.topk(q, k, v, VALUE_K, with_idx=True), args.steps)
+    _prewarm(step_idx, 50.0)
+    idx_us = _replay_us(gi, args.steps)
+    del gi
 
     flops_v = harness.analytic_flops("topk", B, N, D, VALUE_K)
     bytes_v = harness.analytic_bytes("topk", B, N, D, VALUE_K)
+    bytes_i = harness.analytic_bytes("topk", B, N, D, VALUE_K, with_idx=True)
     achieved = flops_v / (kernel_ms * 1e-3)
     line = {
         "metric": _metric(),
@@ -306,8 +388,15 @@ def main() -> int:
         "data": "synthetic: Q,K,V ~ N(0,1) fp32 from a seeded CPU generator, resident in HBM",
         "config": {"workload": "TarMAC attention core, fused score-then-select top-k (configs[1])",
                    "B": B, "N": N, "d": D, "k": VALUE_K, "parallelism": "none (1 GPU)"},
+        "timing": {"method": f"one replay of a graph of the {args.steps} calls, one event pair "
+                             "on the launch stream",
+                   "prewarm_ms": round(prewarm["ms"], 1), "prewarm_calls": prewarm["calls"],
+                   "eager_back_to_back_us": round(eager_us, 3)},
         "roofline": {
-            "bound": "mfma", "achieved": round(achieved / 1e12, 3),
+            # counters (SQ_INSTS_VALU, SQ_VALU_MFMA_BUSY_CYCLES) place the
+            # kernel on fp32 VALU + MFMA issue, whose peak is the fp32 figure
+            # below (VALU fp32 FMA and fp32 MFMA share the 157.3 TFLOP/s rate)
+            "bound": "valu", "achieved": round(achieved / 1e12, 3),
             "peak": harness.PEAK_FP32_FLOPS / 1e12, "unit": "TFLOP/s",
             "frac": round(achieved / harness.PEAK_FP32_FLOPS, 4),
             "traffic": _traffic_from_profiles("topk_fused_k2_B1024_N256_d16"),
@@ -315,6 +404,12 @@ def main() -> int:
             "algorithmic_flops_per_launch": flops_v,
             "algorithmic_bytes_per_launch": bytes_v,
             "hbm_frac": round(bytes_v / (kernel_ms * 1e-3) / harness.PEAK_HBM_BYTES_PER_S, 4),
+        },
+        "with_indices": {
+            "us": round(idx_us, 3),
+            "algorithmic_bytes_per_launch": bytes_i,
+            "frac": round(flops_v / (idx_us * 1e-6) / harness.PEAK_FP32_FLOPS, 4),
+            "hbm_frac": round(bytes_i / (idx_us * 1e-6) / harness.PEAK_HBM_BYTES_PER_S, 4),
         },
     }
     if args.copy_probe:

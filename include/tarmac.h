@@ -6,7 +6,9 @@
  * (a hipStream_t; NULL is the null stream). Nothing is allocated, nothing is
  * synchronised: the kernels are enqueued on `stream` and the call returns.
  * Return value: TARMAC_OK, or an error code whose message is available from
- * tarmac_last_error() on the calling thread. Calls are reentrant.
+ * tarmac_last_error() on the calling thread. Calls are reentrant, with one
+ * exception: tarmac_dense_bwd_noalloc shares one library-held array per GPU,
+ * so its calls that overlap on one GPU race (see its declaration).
  *
  * Scores are q.k / sqrt(d) with the self pair (i == i) excluded, as in every
  * path of the reference. Retained sets are the topk largest scores, ties to
@@ -209,26 +211,38 @@ int tarmac_dense_bwd_noalloc(const float* q, const float* k, const float* v, con
                              int d, void* stream);
 
 /*
- * Which of three equally exact implementations serves topk <= 8 (the retained
+ * Which of four equally exact implementations serves topk <= 8 (the retained
  * set is identical whichever runs, and for fp32 the outputs too, bit for bit;
- * for bf16 the outputs agree to bf16 rounding: the packed pass computes the
- * softmax of a proven set on its truncated scores, within the proof's bound,
- * the other paths on the canonical scores; only the time differs):
- *   packed   -- scores with the key's position in their low mantissa bits,
- *               lists of k+2 values kept with max / med3, a proof that the
- *               truncation (fp32) or the bf16 score error bound (bf16) cannot
- *               change the top k, exact canonical rescoring where it is needed,
- *               and an exact recomputation of any 16-query tile left unproven;
- *   filter   -- all pairs scored on split-bf16 MFMA (fp32 inputs) or bf16
- *               MFMA (bf16, d = 16), k+1 candidates rescored in the canonical
- *               fp32 order and proven against the bf16 error bound;
- *   lists    -- fp32 MFMA scores and per-score (score, index) register lists.
+ * for bf16 the outputs agree to bf16 rounding: the packed pass may compute
+ * the softmax of a proven set on its truncated scores, within the proof's
+ * bound, the other paths on the canonical scores; only the time differs):
+ *   packed       -- scores with the key's position in their low mantissa
+ *                   bits, lists of k+2 values kept with max / med3, a proof
+ *                   that the truncation (fp32) or the bf16 score error bound
+ *                   (bf16) cannot change the top k, and exact canonical
+ *                   rescoring of the k+1 candidates where it is needed;
+ *   packed split -- the packed pass on split-bf16 scores (fp32 inputs,
+ *                   d = 16: x = hi + mid + lo, six bf16 products per score),
+ *                   proven against the split error bound;
+ *   filter       -- all pairs scored on split-bf16 MFMA (fp32 inputs) or
+ *                   bf16 MFMA (bf16, d = 16), k+1 candidates rescored in the
+ *                   canonical fp32 order and proven against the bf16 bound;
+ *   lists        -- fp32 MFMA scores and per-score (score, index) register
+ *                   lists (fp32 inputs; bf16 widened to fp32 at d = 16).
+ * In the packed and filter paths a query whose proof fails (near-ties) is
+ * recomputed by one wavefront from its canonical scores (per-lane lists
+ * merged across the wave); the other queries of its tile keep their proven
+ * sets. The lists path selects on canonical scores and needs no proof.
+ * bf16 exactness rests on a stated bound for the bf16 MFMA accumulation
+ * error (2^-21.9 of the sum of product magnitudes, measured on gfx950, with
+ * eps = 2^-18 at d <= 32 and 2^-17 at d = 64 as the proof's margin).
  * mode: 0 = packed always, 1 = automatic (default; the fastest measured on
  * MI355X for the shape), 2 = filter where supported (fp32 d = 16, 32, 64;
- * bf16 d = 16), 3 = lists for fp32 (bf16 runs packed). bf16 retained sets are
- * always the exact top k of the canonical fp32 scores of the inputs converted
- * to fp32. Process-wide (an atomic setting: concurrent calls stay safe and
- * get identical results). Returns the previous mode, or -1 (and sets the last
+ * bf16 d = 16), 3 = lists for fp32 (bf16 runs packed), 4 = packed split where
+ * supported (fp32 d = 16; packed elsewhere). bf16 retained sets are always
+ * the exact top k of the canonical fp32 scores of the inputs converted to
+ * fp32. Process-wide (an atomic setting: concurrent calls stay safe and get
+ * identical results). Returns the previous mode, or -1 (and sets the last
  * error) for an invalid mode. No counterpart in the reference (its kernels
  * have one path).
  */
@@ -236,7 +250,23 @@ int tarmac_dense_bwd_noalloc(const float* q, const float* k, const float* v, con
 #define TARMAC_FILTER_AUTO 1
 #define TARMAC_FILTER_ALWAYS 2
 #define TARMAC_FILTER_LISTS 3
+#define TARMAC_FILTER_PACKED_SPLIT 4
 int tarmac_set_topk_filter(int mode);
+
+/*
+ * 16-query tiles per wavefront in the dense kernel, the packed top-k pass
+ * (topk <= 4, N <= 1024) and the bf16 filter kernel: 0 = automatic (default:
+ * two, or one when B * ceil(N / 32) < 1024, which would leave SIMDs idle),
+ * 1 = one tile per wave, 2 = two tiles per wave. Results are identical either
+ * way, bit for bit; only the time differs (it lets a small test batch run the
+ * instantiation a large batch uses). Process-wide, atomic. Returns the
+ * previous mode, or -1 (and sets the last error) for an invalid mode. No
+ * counterpart in the reference.
+ */
+#define TARMAC_TILES_AUTO 0
+#define TARMAC_TILES_ONE 1
+#define TARMAC_TILES_TWO 2
+int tarmac_set_query_tiles(int mode);
 
 /* Writes 1.0f to *out: the launch-floor probe of scripts/launch_overhead.py:28-30. */
 int tarmac_noop(float* out, void* stream);

@@ -139,6 +139,23 @@ def test_filter_mode_switch():
         lib.tarmac_set_topk_filter(prev)
 
 
+def test_query_tiles_switch():
+    """tarmac_set_query_tiles: modes 0 to 2 return the previous mode; anything
+    else is refused with -1 and a message, leaving the mode unchanged."""
+    from tarmac import _lib
+    lib = _lib.LIB
+    prev = lib.tarmac_set_query_tiles(0)
+    try:
+        assert lib.tarmac_set_query_tiles(1) == 0
+        assert lib.tarmac_set_query_tiles(2) == 1
+        assert lib.tarmac_set_query_tiles(3) == -1
+        assert "mode must be 0 to 2" in _lib.last_error()
+        assert lib.tarmac_set_query_tiles(-1) == -1
+        assert lib.tarmac_set_query_tiles(0) == 2
+    finally:
+        lib.tarmac_set_query_tiles(prev)
+
+
 def test_grid_knn_shape_matches_the_reference_formula():
     """tarmac_grid_knn_shape (host only) against the oracle's restatement of
     grid_knn_shape (pinned to the reference's values) over a wide range."""

@@ -14,7 +14,12 @@ aggregation):
   the bf16 inputs, outputs within 1e-2);
 * Z-order select+attend, B = 1024, N = 512, k = 2, 16 bits:
   selection bit-exact, outputs within 1e-5 of float64 over that selection;
-* configs[2]: bf16 at B = 4096, one (N, d) per k;
+* bf16 at B = 256 for N in {256, 512}, d in {32, 64} (every
+  row; these batches launch two query tiles per wave, as every bench cell
+  with B >= 256 does, including the chunked d = 64, N = 512 row), at
+  B = 4096 one (N, d) per k on every row, and at B = 4096, N = 512 for
+  d in {16, 32, 64} on a sample of 192 rows;
+* configs[0]: the MPE n6 shape, B = 256, N = 6, d = 16, k = 2, every row;
 * the reference's masked (34 halvings) and sort rules at the shapes bench
   times them (B = 1024, N = 256 and B = 256, N = 384, d = 16): sort indices
   bit-exact, both outputs within 1e-5 of float64 over the oracle's sets.
@@ -125,6 +130,38 @@ def test_configs2_bf16_b4096(N, d, kk):
     q, k, v = (O.bf16_round(x) for x in _inputs(77 + N + d, B, N, d))  # the benchmark's inputs
     out, idx = _topk(q, k, v, kk, torch.bfloat16)
     _check_prefixes(q, k, v, {kk: (out, idx)}, BF16_TOL)
+
+
+@pytest.mark.parametrize("N,d", [(256, 32), (256, 64), (512, 32), (512, 64)])
+def test_configs2_bf16_b256(N, d):
+    """B = 256 with the benchmark's inputs: every row, k = 1, 2, 4."""
+    B = 256
+    q, k, v = (O.bf16_round(x) for x in _inputs(77 + N + d, B, N, d))
+    got = {kk: _topk(q, k, v, kk, torch.bfloat16) for kk in (1, 2, 4)}
+    _check_prefixes(q, k, v, got, BF16_TOL)
+
+
+@pytest.mark.parametrize("d", [16, 32, 64])
+def test_configs2_bf16_b4096_n512_sampled(d):
+    """B = 4096, N = 512 (the largest bf16 cells; d = 64 streams its keys in
+    chunks): the full batch runs, 192 sampled rows meet the oracle."""
+    B, N = 4096, 512
+    q, k, v = (O.bf16_round(x) for x in _inputs(77 + N + d, B, N, d))
+    got = {kk: _topk(q, k, v, kk, torch.bfloat16) for kk in (1, 2, 4)}
+    for out, _ in got.values():
+        assert np.isfinite(out).all()
+    rows = np.sort(np.random.default_rng(d).choice(B, 192, replace=False))
+    _check_prefixes(q[rows], k[rows], v[rows],
+                    {kk: (o[rows], i[rows]) for kk, (o, i) in got.items()}, BF16_TOL)
+
+
+def test_configs0_full_batch():
+    """configs[0], the MPE n6 shape: B = 256, N = 6, d = 16, fp32, k = 2 (and
+    1, 4), every row, with the benchmark's inputs."""
+    B, N, d = 256, 6, 16
+    q, k, v = _inputs(1234 + 7 * N + d, B, N, d)
+    got = {kk: _topk(q, k, v, kk) for kk in (1, 2, 4)}
+    _check_prefixes(q, k, v, got, F32_TOL)
 
 
 @pytest.mark.parametrize("B,N,kk", [(1024, 256, 1), (1024, 256, 2), (1024, 256, 4), (256, 384, 2)])

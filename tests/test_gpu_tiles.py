@@ -1,0 +1,149 @@
+"""Both launch shapes of the kernels that take one or two 16-query tiles per
+wave, at test-sized batches.
+
+The dense kernel, the packed top-k pass (k <= 4, N <= 1024) and the bf16
+filter kernel launch two query tiles per wave when the batch fills the chip
+and one tile per wave below that (B * ceil(N / 32) < 1024). Small test
+batches therefore reach only the one-tile instantiations by default;
+``tarmac_set_query_tiles`` forces either shape, so every instantiation the
+benchmark times at large batches (B >= 256) meets the oracle here:
+
+* dense, fp32 d = 8, 16, 32, 64 and bf16 d = 16, 32, 64: within 1e-5 / 1e-2
+  (normwise) of float64 over the canonical inputs;
+* top-k, bf16 over every (N, d, k) cell of configs[2] and fp32 at d = 8, 16,
+  32, 64 (including exact ties that send queries to the per-query exact
+  pass): retained indices bit-exact against the canonical C oracle, in order;
+* and both shapes return the same bits (outputs and indices).
+"""
+
+from __future__ import annotations
+
+import contextlib
+
+import numpy as np
+import pytest
+import torch
+
+import tarmac_oracle as O
+from conftest import qkv
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-5
+BF16_TOL = 1e-2
+ONE, TWO = 1, 2
+
+
+@contextlib.contextmanager
+def tiles(mode: int):
+    from tarmac import _lib
+    prev = _lib.LIB.tarmac_set_query_tiles(mode)
+    assert prev >= 0
+    try:
+        yield
+    finally:
+        _lib.LIB.tarmac_set_query_tiles(prev)
+
+
+def dev(*xs, dtype=torch.float32):
+    return [torch.from_numpy(np.ascontiguousarray(x)).to("cuda").to(dtype) for x in xs]
+
+
+def normwise(got, ref):
+    return np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)
+
+
+def dense_both(q, k, v, dtype):
+    from tarmac.kernels import fused_dense_attention
+    qd, kd, vd = dev(q, k, v, dtype=dtype)
+    res = {}
+    for mode in (ONE, TWO):
+        with tiles(mode):
+            res[mode] = fused_dense_attention(qd, kd, vd).float().cpu().numpy()
+    return res
+
+
+def topk_both(q, k, v, kk, dtype):
+    from tarmac.kernels import topk_attention
+    qd, kd, vd = dev(q, k, v, dtype=dtype)
+    res = {}
+    for mode in (ONE, TWO):
+        with tiles(mode):
+            out, idx = topk_attention(qd, kd, vd, kk, return_indices=True)
+            res[mode] = (out.float().cpu().numpy(), idx.cpu().numpy())
+    return res
+
+
+@pytest.mark.parametrize("N,d", [(100, 8), (256, 8), (100, 16), (300, 16), (512, 16), (128, 32),
+                                 (384, 32), (256, 64), (512, 64)])
+def test_dense_f32_both_shapes(N, d):
+    q, k, v = qkv(N * 7 + d, 3, N, d)
+    got = dense_both(q, k, v, torch.float32)
+    ref = O.canon_dense(q, k, v)
+    for mode, out in got.items():
+        assert normwise(out, ref) <= F32_TOL, f"tiles={mode}"
+    assert np.array_equal(got[ONE], got[TWO])
+
+
+@pytest.mark.parametrize("N,d", [(64, 16), (256, 16), (512, 16), (64, 32), (256, 32), (512, 32),
+                                 (64, 64), (256, 64), (512, 64), (100, 16)])
+def test_dense_bf16_both_shapes(N, d):
+    q, k, v = (O.bf16_round(x) for x in qkv(77 + N + d, 4, N, d))
+    got = dense_both(q, k, v, torch.bfloat16)
+    ref = O.canon_dense(q, k, v)
+    for mode, out in got.items():
+        assert normwise(out, ref) <= BF16_TOL, f"tiles={mode}"
+    assert np.array_equal(got[ONE], got[TWO])
+
+
+def _check_exact(q, k, v, kk, got, tol):
+    out_c, idx_c = O.canon_topk(q, k, v, kk)
+    for mode, (out, idx) in got.items():
+        assert np.array_equal(idx, idx_c), f"tiles={mode}: retained indices differ from the oracle"
+        assert normwise(out, out_c) <= tol, f"tiles={mode}"
+    assert np.array_equal(got[ONE][1], got[TWO][1])
+    assert np.array_equal(got[ONE][0], got[TWO][0])
+
+
+CONFIGS2 = [(N, d, kk) for N in (64, 256, 512) for d in (16, 32, 64) for kk in (1, 2, 4)]
+
+
+@pytest.mark.parametrize("N,d,kk", CONFIGS2)
+def test_topk_bf16_configs2_both_shapes(N, d, kk):
+    """Every (N, d, k) cell of the bf16 grid under both launch shapes."""
+    q, k, v = (O.bf16_round(x) for x in qkv(77 + N + d, 6, N, d))
+    _check_exact(q, k, v, kk, topk_both(q, k, v, kk, torch.bfloat16), BF16_TOL)
+
+
+@pytest.mark.parametrize("N,d", [(256, 16), (512, 32), (300, 64)])
+def test_topk_bf16_ties_both_shapes(N, d):
+    """Duplicated keys, zero and repeated queries: the per-query exact pass
+    under both launch shapes, ties to the lower index."""
+    q, k, v = (O.bf16_round(x) for x in qkv(600 + N + d, 3, N, d))
+    k[:, 1::2] = k[:, 0::2]
+    q[:, :5] = 0.0
+    q[:, 5:10] = q[:, 5:6]
+    for kk in (1, 2, 3, 4):
+        got = topk_both(q, k, v, kk, torch.bfloat16)
+        _check_exact(q, k, v, kk, got, BF16_TOL)
+        assert got[TWO][1][:, 0].tolist() == [list(range(1, kk + 1))] * 3
+
+
+@pytest.mark.parametrize("N,d", [(256, 8), (200, 16), (512, 16), (256, 32), (300, 64), (1024, 16)])
+@pytest.mark.parametrize("kk", [1, 2, 3, 4])
+def test_topk_f32_both_shapes(N, d, kk):
+    q, k, v = qkv(N * 3 + d + kk, 3, N, d)
+    _check_exact(q, k, v, kk, topk_both(q, k, v, kk, torch.float32), F32_TOL)
+
+
+@pytest.mark.parametrize("N,d", [(256, 32), (300, 64), (200, 8), (256, 16)])
+def test_topk_f32_ties_both_shapes(N, d):
+    """fp32 at k = 3, 4 with duplicated keys and zero queries: the packed
+    proof fails and the per-query exact pass decides, under both shapes."""
+    q, k, v = qkv(31 + N + d, 3, N, d)
+    k[:, 1::2] = k[:, 0::2]
+    q[:, :6] = 0.0
+    for kk in (3, 4):
+        got = topk_both(q, k, v, kk, torch.float32)
+        _check_exact(q, k, v, kk, got, F32_TOL)
+        assert got[TWO][1][:, 0].tolist() == [list(range(1, kk + 1))] * 3

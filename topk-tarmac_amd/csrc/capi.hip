@@ -365,6 +365,14 @@ int tarmac_set_topk_filter(int mode) {
   return tarmac::set_topk_filter_mode(mode);
 }
 
+int tarmac_set_query_tiles(int mode) {
+  if (mode < tarmac::kTilesAuto || mode > tarmac::kTilesTwo) {
+    fail(TARMAC_ERR_INVALID, "tarmac_set_query_tiles: mode must be 0 to 2 (got %d)", mode);
+    return -1;
+  }
+  return tarmac::set_query_tiles_mode(mode);
+}
+
 int tarmac_noop(float* out, void* stream) {
   if (!out) return fail(TARMAC_ERR_INVALID, "tarmac_noop: null out");
   return hip_status(tarmac::run_noop(out, stream), "tarmac_noop");

@@ -397,8 +397,7 @@ static hipError_t launch_dense(const DenseArgs& a) {
     hipError_t e;
     if (dense_reg<D>(a, &e)) return e;
   }
-  const long waves2 = static_cast<long>(a.B) * ((a.N + 31) / 32);
-  if (waves2 < 4L * kCUs) return launch_dense_q<T, D, 1>(a);
+  if (one_query_tile(a.B, a.N)) return launch_dense_q<T, D, 1>(a);
   return launch_dense_q<T, D, kDenseQueryTiles>(a);
 }
 

@@ -134,6 +134,11 @@ constexpr int kFilterOff = 0, kFilterAuto = 1, kFilterAlways = 2, kFilterLegacy 
               kFilterPackedSplit = 4;
 int topk_filter_mode();
 int set_topk_filter_mode(int mode);  // returns the previous mode
+// tarmac_set_query_tiles modes: 16-query tiles per wave in the dense, packed
+// (k <= 4, N <= 1024) and bf16 filter kernels
+constexpr int kTilesAuto = 0, kTilesOne = 1, kTilesTwo = 2;
+int set_query_tiles_mode(int mode);  // returns the previous mode
+bool one_query_tile(int B, int N);   // the launch shape under the current mode
 hipError_t run_dense(const DenseArgs& a);
 hipError_t run_fixedset(const FixedsetArgs& a);
 hipError_t run_morton_window(const MortonArgs& a);

@@ -1060,6 +1060,22 @@ static std::atomic<int> g_topk_filter_mode{kFilterAuto};
 int topk_filter_mode() { return g_topk_filter_mode.load(std::memory_order_relaxed); }
 int set_topk_filter_mode(int mode) { return g_topk_filter_mode.exchange(mode); }
 
+// Process-wide override of the query tiles per wave (also exact either way).
+static std::atomic<int> g_query_tiles_mode{kTilesAuto};
+
+int set_query_tiles_mode(int mode) { return g_query_tiles_mode.exchange(mode); }
+
+bool one_query_tile(int B, int N) {
+  switch (g_query_tiles_mode.load(std::memory_order_relaxed)) {
+    case kTilesOne: return true;
+    case kTilesTwo: return false;
+    default: break;
+  }
+  // two tiles per wave halve the per-query staging and merge cost, unless the
+  // batch is then too small to give every SIMD a wave (B * N / 32 < 4 * kCUs)
+  return static_cast<long>(B) * ((N + 31) / 32) < 4L * kCUs;
+}
+
 enum TopkPath { kPathPacked, kPathPackedSplit, kPathFilter, kPathLists };
 
 // The implementation for k <= 8 (all return identical results). Automatic

@@ -476,8 +476,7 @@ static hipError_t launch_filter_q(const TopkArgs& a, int kc) {
 template <typename T, int D>
 static hipError_t launch_filter(const TopkArgs& a, int kc) {
   if constexpr (sizeof(T) == 2) {
-    const long waves2 = static_cast<long>(a.B) * ((a.N + 31) / 32);
-    if (waves2 < 4L * kCUs) return launch_filter_q<T, D, 1>(a, kc);
+    if (one_query_tile(a.B, a.N)) return launch_filter_q<T, D, 1>(a, kc);
   }
   return launch_filter_q<T, D, kTopkQueryTiles>(a, kc);
 }

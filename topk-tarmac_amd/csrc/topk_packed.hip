@@ -566,8 +566,7 @@ static hipError_t launch_packed_shape_q(const TopkArgs& a) {
 template <typename T, int D, int K, bool SPLIT>
 static hipError_t launch_packed_shape(const TopkArgs& a) {
   if constexpr (K <= 4) {
-    const long waves2 = static_cast<long>(a.B) * ((a.N + 31) / 32);
-    if (a.N <= 1024 && waves2 < 4L * kCUs) return launch_packed_shape_q<T, D, K, 1, SPLIT>(a);
+    if (a.N <= 1024 && one_query_tile(a.B, a.N)) return launch_packed_shape_q<T, D, K, 1, SPLIT>(a);
   }
   return launch_packed_shape_q<T, D, K, kTopkQueryTiles, SPLIT>(a);
 }

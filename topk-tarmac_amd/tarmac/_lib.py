@@ -48,6 +48,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tarmac_knn_grid": ([_P, _P, _I, _I, _I, _I, _P], _I),
     "tarmac_grid_knn_shape": ([_I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)], _I),
     "tarmac_set_topk_filter": ([_I], _I),
+    "tarmac_set_query_tiles": ([_I], _I),
     "tarmac_noop": ([_P, _P], _I),
 }
 
