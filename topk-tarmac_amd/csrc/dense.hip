@@ -12,20 +12,24 @@
 //                                         is its own probability p[u] -- no
 //                                         cross-lane data movement)
 // V is staged transposed in LDS so the A operand of the PV product is a
-// contiguous read. The running max is shared by the 4 lanes of a query
-// (two xor shuffles per 64-key block); the running sum stays per lane and is
+// contiguous read. Online softmax per 64-key block: a block's maximum is
+// shared by the 4 lanes of a query with two row swaps (VALU, no LDS), and the
+// running offset is raised -- rescaling the query's sum and accumulator --
+// only when the block's maximum exceeds it by more than 2^8, so after the
+// first block a score costs half a v_max3, one fma and one exp2 (plus, in
+// bf16, half a conversion and half a v_dot2 for the row sum, which adds the
+// bf16-rounded weights the PV product uses). The running sum stays per lane and is
 // combined once at the end. fp32 scores come out of the product already in
 // the log2 domain (q is pre-multiplied by scale*log2(e), exact for the
-// power-of-two scales); bf16 scores stay raw and the factor is applied inside
-// the exponent's argument, fma(s, c, -c*m), after a max taken on raw scores
-// (c > 0, so the max commutes with the scaling).
+// power-of-two scales; c = 1); bf16 scores stay raw and c = scale*log2(e) is
+// applied inside the exponent's argument, fma(s, c, -off).
 #include "frag.hpp"
 #include "tarmac_internal.hpp"
 
 namespace tarmac {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kDenseBlockTiles = 4;  // 64 keys per online-softmax step
+constexpr int kDenseBlockTiles = 4;  // 64 keys per score block
 constexpr int kDenseQueryTiles = 2;  // 16-query tiles per wavefront
 
 template <typename T, int D>
@@ -78,13 +82,12 @@ struct PvOperand<bf16, D> {
   static constexpr int NH = D / 16;
   static constexpr int CP = NH * 16;
   static constexpr int TILES = 2;  // 16-key tiles per step
+  // pb: each query tile's eight probabilities, packed (pack_p_pair)
   template <int QT>
-  __device__ __forceinline__ static void pv_step(f32x4 (&acc)[QT][NH], const bf16* Vt, int ldv,
-                                                 int kb, int lane, const float (&p)[QT][TILES][4]) {
+  __device__ __forceinline__ static void pv_step_packed(f32x4 (&acc)[QT][NH], const bf16* Vt,
+                                                        int ldv, int kb, int lane,
+                                                        const bf16x8 (&pb)[QT]) {
     const int col = lane & 15, grp = lane >> 4;
-    bf16x8 pb[QT];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) pb[qt] = pack_p_pair(p[qt][0], p[qt][1]);
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
       const bf16* r = Vt + (16 * h + col) * ldv + kb + 4 * grp;
@@ -95,6 +98,35 @@ struct PvOperand<bf16, D> {
     }
   }
 };
+
+// Row sum of eight bf16 probabilities (the PV operand) into an fp32 sum: four
+// v_dot2 against (1, 1). The softmax then normalises by the sum of exactly
+// the weights the PV product uses.
+__device__ __forceinline__ float sum_bf16x8(bf16x8 p, float acc) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const uint4 w = __builtin_bit_cast(uint4, p);
+  const bf16x2_t one = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.x), one, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.y), one, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.z), one, acc, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.w), one, acc, false);
+}
+
+// Maximum over the four lanes of a query (lanes l, l + 16, l + 32, l + 48):
+// two row swaps, VALU only.
+__device__ __forceinline__ float query_max4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// Softmax terms are 2^(c s - off) with off a running maximum of c s that is
+// only raised when a block's maximum exceeds it by more than 2^kDenseLag:
+// terms then stay below 2^kDenseLag (no overflow, no loss of precision in
+// fp32), and after the first block a raise -- a rescale of the query's sum
+// and accumulator -- is rare.
+constexpr float kDenseLag = 8.f;
 
 template <typename T, int D, int QT>
 __global__ void __launch_bounds__(256)
@@ -129,16 +161,16 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
     frag[qt].load_q(Q + boff + static_cast<size_t>(min(qi, N - 1)) * D, grp,
                     sizeof(T) == 4 ? scale * kLog2e : 1.f);
   }
-  // exponent factor: 1 for fp32 (folded into q), scale*log2(e) for bf16
+  // exponent factor c: 1 for fp32 (folded into q), scale*log2(e) for bf16
   const float post = (sizeof(T) == 4) ? 1.f : scale * kLog2e;
 
   f32x4 acc[QT][NH];
-  float m_run[QT], l_run[QT];
+  float off[QT], l_run[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
 #pragma unroll
     for (int h = 0; h < NH; ++h) acc[qt][h] = f32x4{0.f, 0.f, 0.f, 0.f};
-    m_run[qt] = -INFINITY;
+    off[qt] = -INFINITY;
     l_run[qt] = 0.f;
   }
 
@@ -169,7 +201,7 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
               if (key >= kend || key == q0 + 16 * qt + col) s[qt][t][r] = -INFINITY;
             }
       }
-      float neg[QT];  // -post * (running max): the exponent's offset
+      float neg[QT];  // the exponent's offset
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
         float mloc = -INFINITY;
@@ -177,16 +209,15 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
         for (int t = 0; t < BT; ++t)
 #pragma unroll
           for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[qt][t][r]);
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-        const float m_new = fmaxf(m_run[qt], mloc);
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        const float alpha = fast_exp2((m_run[qt] - m_use) * post);  // 0 while nothing has been seen
-        l_run[qt] *= alpha;
+        const float m_blk = query_max4(mloc) * post;
+        if (m_blk > off[qt] + kDenseLag) {  // rare after the first block
+          const float alpha = fast_exp2(off[qt] - m_blk);  // 0 while nothing has been seen
+          l_run[qt] *= alpha;
 #pragma unroll
-        for (int h = 0; h < NH; ++h) acc[qt][h] *= alpha;
-        m_run[qt] = m_new;
-        neg[qt] = -m_use * post;
+          for (int h = 0; h < NH; ++h) acc[qt][h] *= alpha;
+          off[qt] = m_blk;
+        }
+        neg[qt] = off[qt] == -INFINITY ? 0.f : -off[qt];  // a block of masked keys only
       }
       constexpr int TS = PV::TILES;
       static_assert(BT % TS == 0, "whole PV steps per block");
@@ -198,11 +229,24 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
 #pragma unroll
           for (int t = 0; t < TS; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              p[qt][t][r] = fast_exp2(fmaf(s[qt][t0 + t][r], post, neg[qt]));
-              l_run[qt] += p[qt][t][r];
-            }
-        PV::template pv_step<QT>(acc, Vt, ldv, kb0 + 16 * t0, lane, p);
+            for (int r = 0; r < 4; ++r) p[qt][t][r] = fast_exp2(fmaf(s[qt][t0 + t][r], post, neg[qt]));
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+            for (int t = 0; t < TS; ++t)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) l_run[qt] += p[qt][t][r];
+          PV::template pv_step<QT>(acc, Vt, ldv, kb0 + 16 * t0, lane, p);
+        } else {
+          bf16x8 pb[QT];
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) {
+            pb[qt] = pack_p_pair(p[qt][0], p[qt][1]);
+            l_run[qt] = sum_bf16x8(pb[qt], l_run[qt]);
+          }
+          PV::template pv_step_packed<QT>(acc, Vt, ldv, kb0 + 16 * t0, lane, pb);
+        }
       }
     }
   }
@@ -214,8 +258,7 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
     const int qi = q0 + 16 * qt + col;
     if (qi >= N) continue;
     // log2-domain logsumexp of the scaled scores, for the backward pass
-    if (lse != nullptr && grp == 0)
-      lse[static_cast<size_t>(b) * 2 * N + qi] = m_run[qt] * post + log2f(l_tot);
+    if (lse != nullptr && grp == 0) lse[static_cast<size_t>(b) * 2 * N + qi] = off[qt] + log2f(l_tot);
     // lane l holds O^T[c = 16h + 4*(l/16) + r][q = l%16]; one reciprocal
     // per row instead of a division per channel
     const float inv = 1.f / l_tot;

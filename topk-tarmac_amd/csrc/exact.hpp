@@ -1,7 +1,7 @@
 // Exact-selection helpers shared by the top-k kernels that select on packed
 // values and then prove (or repair) the result: canonical fp32 rescoring of
 // candidates, key staging with row norms (the error bound of bf16 scores),
-// and the exact per-tile fallback pass.
+// and the exact per-query fallback pass.
 #pragma once
 
 #include "frag.hpp"
@@ -239,79 +239,103 @@ __device__ __forceinline__ float bf16_frag_norm2(const Frag<bf16, D>& f) {
   return n2 + __shfl_xor(n2, 32);
 }
 
-// The exact top K of one query's canonical fp32 scores (score desc, index
-// asc), by the whole wavefront. The MFMA runs with its operands' roles
-// swapped: the query fills every row of the A operand and 16 keys the
-// columns of B, so lane (col, g) receives the score of key kb + col (in all
-// four of its elements); the products and their order are those of the
-// canonical chain, so the scores are bit-identical. Lane row g keeps the
-// keys of every fourth tile (t % 4 == g), each lane in ascending key order,
-// and the lists merge in six xor steps, after which every lane holds the
-// result. Key fragments come TB tiles per burst (16 VGPRs of fragments, at
-// most four tiles) from global memory or, where the kernel holds the whole
-// row as plain rows, from LDS (bf16 widened). The fallback for a query whose packed or
-// filtered selection could not be proven: the other queries of its tile keep
-// their proven sets, and the row costs N / (16 TB) memory round trips instead
-// of one per 16-key tile.
-// load_k(dst, row, g): elements g*E .. g*E+E-1 of key row `row` as fp32 (a
-// global row, or a plain row of the LDS copy).
-template <typename T, int D, int K, typename LoadK>
-__device__ __forceinline__ void exact_query_topk(const T* __restrict__ Qb, LoadK load_k, int N,
-                                                 int qi, float scale, int lane, float (&val)[K],
-                                                 int (&ix)[K]) {
-  using F = Frag<float, D>;
-  constexpr bool POW2 = pow2_scale<D>();
-  constexpr int E = F::E;
-  constexpr int TB = E >= 16 ? 1 : (E >= 8 ? 2 : 4);  // 16-key tiles per burst (<= 16 VGPRs)
-  const int col = lane & 15, grp = lane >> 4;
-  float qa[E];  // the query's elements g*E .. g*E+E-1, the same in every lane row
-  ld_row<T, E>(qa, Qb + static_cast<size_t>(qi) * D + grp * E);
-  if constexpr (POW2) {
+// ---------------------------------------------------------------------------
+// exact top K of one query on the VALU, one key row per lane
+// ---------------------------------------------------------------------------
+
+// One key row held raw in registers (D elements of T as 32-bit words).
+template <typename T, int D>
+struct RawRow {
+  static constexpr int W = D * static_cast<int>(sizeof(T)) / 4;
+  static_assert((D * sizeof(T)) % 16 == 0, "rows are read as 16-byte vectors");
+  uint32_t w[W];
+  // src: 16-byte aligned row (global memory or LDS)
+  __device__ __forceinline__ void load(const T* src) {
 #pragma unroll
-    for (int i = 0; i < E; ++i) qa[i] *= scale;
+    for (int v = 0; v < W / 4; ++v) {
+      const uint4 x = reinterpret_cast<const uint4*>(src)[v];
+      w[4 * v] = x.x; w[4 * v + 1] = x.y; w[4 * v + 2] = x.z; w[4 * v + 3] = x.w;
+    }
   }
+  // element c as fp32 (bf16 widens exactly)
+  __device__ __forceinline__ float at(int c) const {
+    if constexpr (sizeof(T) == 4) return __uint_as_float(w[c]);
+    else return __uint_as_float((c & 1) ? (w[c >> 1] & 0xffff0000u) : (w[c >> 1] << 16));
+  }
+};
+
+// Rows per lane per round for kernels whose register count bounds their
+// occupancy: one. Kernels that run at most two waves per SIMD (one query tile
+// per wave, small batches) take exact_wide_rows: 64 VGPRs of raw key data in
+// flight, so one round trip brings 64 G rows (fp32 d = 16: 256 keys; bf16
+// d = 64: 128 keys).
+template <typename T, int D>
+constexpr int exact_wide_rows() {
+  constexpr int words = D * static_cast<int>(sizeof(T)) / 4;
+  return words >= 64 ? 1 : 64 / words;
+}
+
+// The exact top K of one query's canonical fp32 scores (score desc, index
+// asc), by the whole wavefront on the VALU: lane l scores keys l, l + 64,
+// l + 128, ... each with the canonical fmaf chain itself (element
+// kk * (D/4) + t at step t, slot kk, from +0; the scale folded into the query
+// when it is a power of two), so the scores are the oracle's bit for bit.
+// Every product is one the answer needs -- an MFMA pass for a single query
+// would use a sixteenth of its products -- and each round trip fetches G whole
+// rows per lane (G = 1, or exact_wide_rows where registers are free). Each lane keeps a list of K over its keys, which arrive in
+// ascending order (strict '>' keeps the lower index on ties); the 64 lists
+// merge in six xor steps, after which every lane holds the result. The query
+// row is read in chunks of 16 elements from qrow (global memory, uniform)
+// inside each round, so at most 16 of its elements are live at a time.
+// row_at(j): pointer to key row j (global memory or an LDS copy; 16-byte
+// aligned).
+template <typename T, int D, int K, int G, typename RowAt>
+__device__ __forceinline__ void exact_query_topk_lanes(const T* __restrict__ qrow, RowAt row_at,
+                                                       int N, int qi, float scale, int lane,
+                                                       float (&val)[K], int (&ix)[K]) {
+  constexpr bool POW2 = pow2_scale<D>();
+  constexpr int QD = D / 4;
+  constexpr int TS = QD < 4 ? QD : 4;  // chain steps per query chunk
 #pragma unroll
   for (int m = 0; m < K; ++m) { val[m] = -INFINITY; ix[m] = kIdxSentinel; }
-  const int nt = (N + 15) / 16;
-  if constexpr (TB == 1) {
-    // one-tile bursts (D = 64): the next tile's fragment is in flight during
-    // this tile's MFMAs (a second buffer here does not raise the kernel's
-    // VGPR count, as it would for the multi-tile bursts of D <= 32)
-    float kb[E], kn[E];
-    load_k(kb, min(col, N - 1), grp);
 #pragma unroll 1
-    for (int t = 0; t < nt; ++t) {
-      load_k(kn, min(16 * (t + 1) + col, N - 1), grp);  // clamped: always a valid row
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < N; j0 += 64 * G) {
+    // re-read the query chunks every round (an opaque copy of the pointer
+    // keeps the loads from being hoisted out of the loop with all D elements
+    // held live across it)
+    const T* qr = qrow;
+    asm volatile("" : "+s"(qr));
+    RawRow<T, D> kr[G];
 #pragma unroll
-      for (int i = 0; i < E; ++i) acc = mfma_f32_16x16x4(qa[i], kb[i], acc);
-      const int j = 16 * t + col;
-      float v = POW2 ? acc[0] : acc[0] * scale;
-      if (j >= N || j == qi || (t & 3) != grp) v = -INFINITY;
-      topk_insert<K>(val, ix, v, j);
+    for (int g = 0; g < G; ++g) kr[g].load(row_at(min(j0 + 64 * g + lane, N - 1)));
+    float acc[G];
 #pragma unroll
-      for (int i = 0; i < E; ++i) kb[i] = kn[i];
+    for (int g = 0; g < G; ++g) acc[g] = 0.f;
+#pragma unroll
+    for (int t0 = 0; t0 < QD; t0 += TS) {
+      float qc[4][TS];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        ld_row<T, TS>(qc[kk], qr + kk * QD + t0);
+        if constexpr (POW2) {
+#pragma unroll
+          for (int t = 0; t < TS; ++t) qc[kk][t] *= scale;
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < TS; ++t)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+          for (int g = 0; g < G; ++g) acc[g] = fmaf(qc[kk][t], kr[g].at(kk * QD + t0 + t), acc[g]);
     }
-  } else {
-#pragma unroll 1
-  for (int t0 = 0; t0 < nt; t0 += TB) {
-    float kb[TB][E];
 #pragma unroll
-    for (int u = 0; u < TB; ++u)
-      load_k(kb[u], min(16 * (t0 + u) + col, N - 1), grp);
-#pragma unroll
-    for (int u = 0; u < TB; ++u) {
-      const int t = t0 + u;
-      if (t >= nt) break;  // uniform
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < E; ++i) acc = mfma_f32_16x16x4(qa[i], kb[u][i], acc);
-      const int j = 16 * t + col;
-      float v = POW2 ? acc[0] : acc[0] * scale;
-      if (j >= N || j == qi || (t & 3) != grp) v = -INFINITY;
-      topk_insert<K>(val, ix, v, j);
+    for (int g = 0; g < G; ++g) {
+      const int j = j0 + 64 * g + lane;
+      float s = POW2 ? acc[g] : acc[g] * scale;
+      if (j >= N || j == qi) s = -INFINITY;
+      topk_insert<K>(val, ix, s, j);
     }
-  }
   }
 #pragma unroll
   for (int step = 1; step < 64; step <<= 1) {
@@ -325,18 +349,6 @@ __device__ __forceinline__ void exact_query_topk(const T* __restrict__ Qb, LoadK
 #pragma unroll
     for (int m = 0; m < K; ++m) topk_insert_lex<K>(val, ix, pv[m], pi[m]);
   }
-}
-
-// exact_query_topk with the keys read from global memory.
-template <typename T, int D, int K>
-__device__ __forceinline__ void exact_query_topk_global(const T* __restrict__ Qb,
-                                                        const T* __restrict__ Kb, int N, int qi,
-                                                        float scale, int lane, float (&val)[K],
-                                                        int (&ix)[K]) {
-  constexpr int E = D / 4;
-  exact_query_topk<T, D, K>(
-      Qb, [&](float (&dst)[E], int row, int g) { ld_row<T, E>(dst, Kb + static_cast<size_t>(row) * D + g * E); },
-      N, qi, scale, lane, val, ix);
 }
 
 }  // namespace tarmac

@@ -137,8 +137,13 @@ template <>
 struct Frag<bf16, 16> {
   static constexpr int LDK = 16 + 8;
   i16x4 q;
+  // pre == 1 (a constant at every caller that passes it) takes the row as is
   __device__ __forceinline__ void load_q(const bf16* qrow, int grp, float pre) {
     uint2 v = *reinterpret_cast<const uint2*>(qrow + 4 * grp);
+    if (pre == 1.f) {
+      q = __builtin_bit_cast(i16x4, v);
+      return;
+    }
     bf16 e[4] = {static_cast<bf16>(v.x), static_cast<bf16>(v.x >> 16),
                  static_cast<bf16>(v.y), static_cast<bf16>(v.y >> 16)};
 #pragma unroll
@@ -171,6 +176,10 @@ struct FragBf16Wide {
 #pragma unroll
     for (int h = 0; h < NI; ++h) {
       const uint4 raw = *reinterpret_cast<const uint4*>(qrow + 32 * h + 8 * grp);
+      if (pre == 1.f) {  // a constant at every caller that passes it
+        q[h] = __builtin_bit_cast(bf16x8, raw);
+        continue;
+      }
       const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
       uint32_t o[4];
 #pragma unroll

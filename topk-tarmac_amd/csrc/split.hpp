@@ -20,6 +20,17 @@ constexpr float packed_eps() {
 }
 constexpr float kPackedNormLimit = 1.329228e36f;  // 2^120: |q| max|k| at or above fails the proof
 
+// An upper bound on |q| max_j |k_j| from the squared norms: one v_sqrt_f32
+// (within 1 ulp) of the product (one rounding), raised by 2^-21 (more than
+// both errors and the raise's own rounding). Products below 2^-100 give +inf,
+// which fails the proof (the exact pass decides such queries: their scores
+// could sit among denormals, where the MFMA and the fmaf chain may flush
+// differently); an overflowing product gives +inf too.
+__device__ __forceinline__ float proof_norm(float qn2, float kmax2) {
+  const float p = qn2 * kmax2;
+  return p >= 7.88860905e-31f ? __builtin_amdgcn_sqrtf(p) * 1.00000048f : INFINITY;
+}
+
 // ---------------------------------------------------------------------------
 // split-bf16 fragments: S^T tile (16 keys x 16 queries) of split products
 // ---------------------------------------------------------------------------

@@ -29,9 +29,9 @@
 //     settles near-ties between the k-th and (k+1)-th scores (duplicated keys
 //     included) without the fallback.
 //  3. fallback: an unproven query is recomputed exactly by the whole wave
-//     (exact_query_topk: its row's canonical scores, per-lane lists, a
-//     six-step merge), so the result never depends on the filter -- only
-//     the time does.
+//     (exact_query_topk_lanes: its row's canonical scores on the VALU, one
+//     key row per lane, per-lane lists, a six-step merge), so the result
+//     never depends on the filter -- only the time does.
 //
 // Reference behaviour: src/kernels/fused_topk_attention.py:211-333 and
 // src/kernels/streaming_topk_attention.py:66-258 (including the retained
@@ -335,7 +335,6 @@ topk_filter_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
   }
 
   // ---- verify: rescore the candidates exactly ---------------------------
-  const float kmax = sqrtf(kmax2);
   float val[QT][K];
   int ix[QT][K];
   bool ok[QT];
@@ -363,7 +362,7 @@ topk_filter_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
     sort_lex<C>(cv, cand[qt]);
 #pragma unroll
     for (int m = 0; m < K; ++m) { val[qt][m] = cv[m]; ix[qt][m] = cand[qt][m]; }
-    const float nprod = sqrtf(qn2[qt]) * kmax;
+    const float nprod = proof_norm(qn2[qt], kmax2);
     const float bound = (ceil_f[qt] + filter_eps<D>() * nprod) * scale;
     ok[qt] = self[qt] >= N || (nprod < kNormLimit && bound < val[qt][K - 1]);
   }
@@ -378,7 +377,10 @@ topk_filter_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
       todo &= todo - 1ull;
       float ev[K];
       int ei[K];
-      exact_query_topk_global<T, D, K>(Qb, Kb, N, q0 + 16 * qt + c, scale, lane, ev, ei);
+      const int qi = q0 + 16 * qt + c;
+      exact_query_topk_lanes<T, D, K, QT == 1 ? exact_wide_rows<T, D>() : 1>(
+          Qb + static_cast<size_t>(qi) * D, [&](int j) { return Kb + static_cast<size_t>(j) * D; }, N,
+          qi, scale, lane, ev, ei);
       if (col == c) {
 #pragma unroll
         for (int m = 0; m < K; ++m) { val[qt][m] = ev[m]; ix[qt][m] = ei[m]; }

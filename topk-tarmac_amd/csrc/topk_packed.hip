@@ -35,8 +35,8 @@
 //     softmax weights are then bit-for-bit those of the oracle's scores) and
 //     sorted by (score desc, index asc).
 //  5. fallback: an unproven query is recomputed exactly by the whole wave
-//     (exact_query_topk: its row's canonical scores, per-lane lists, a
-//     six-step merge) -- the result never depends on the packing, only the
+//     (exact_query_topk_lanes: its row's canonical scores on the VALU, one
+//     key row per lane, per-lane lists, a six-step merge) -- the result never depends on the packing, only the
 //     time does.
 //  6. k-softmax and the gathered aggregation over the K value rows.
 #include "exact.hpp"
@@ -382,7 +382,6 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
   // Lane row g rescores candidates g, g+4, g+8 from its query fragment (the
   // row is gathered across lane rows) and the key row, from LDS when one
   // chunk holds the whole row.
-  const float kmax = sqrtf(kmax2);
   float val[QT][K];
   int ix[QT][K];
   bool ok[QT];
@@ -394,7 +393,7 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
       ok[qt] = self >= N || trunc_bits(pl[qt][K], FM) < trunc_bits(pl[qt][K - 1], FM) ||
                trunc_bits(pl[qt][K + 1], FM) < trunc_bits(pl[qt][K], FM);
     } else {
-      const float nprod = sqrtf(qn2[qt]) * kmax;
+      const float nprod = proof_norm(qn2[qt], kmax2);
       const float e = packed_eps<D>() * nprod;
       bool sep[L - 1];  // entry m's interval (widened by e) lies above entry m+1's
 #pragma unroll
@@ -442,7 +441,7 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
       if constexpr (SPLIT) {
         // every key outside the candidates scores at most the (K+2)-th
         // entry's ceiling plus the split error
-        const float nprod = sqrtf(qn2[qt]) * kmax;
+        const float nprod = proof_norm(qn2[qt], kmax2);
         const float bound = (trunc_ceiling(pl[qt][K + 1], FM) + packed_eps<D>() * nprod) * scale;
         ok[qt] = self >= N || (nprod < kPackedNormLimit && bound < cv[K - 1]);
       }
@@ -473,15 +472,17 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
         todo &= todo - 1ull;
         float ev[K];
         int ei[K];
-        // plain rows of the whole row in LDS serve it there (split rows do not)
+        const int qi = q0 + 16 * qt + c;
+        // plain rows of the whole row in LDS serve it there (split rows do
+        // not); the select makes the row pointer generic (flat loads), which
+        // keeps one copy of this rare path
         const bool from_lds = lds_all && !SPLIT;  // uniform
-        exact_query_topk<T, D, K>(
-            Qb,
-            [&](float (&dst)[D / 4], int row, int g) {
-              if (from_lds) ld_row<T, D / 4>(dst, reinterpret_cast<const T*>(Ks) + row * LDK + g * (D / 4));
-              else ld_row<T, D / 4>(dst, Kb + static_cast<size_t>(row) * D + g * (D / 4));
+        exact_query_topk_lanes<T, D, K, QT == 1 ? exact_wide_rows<T, D>() : 1>(
+            Qb + static_cast<size_t>(qi) * D,
+            [&](int j) {
+              return from_lds ? reinterpret_cast<const T*>(Ks) + j * LDK : Kb + static_cast<size_t>(j) * D;
             },
-            N, q0 + 16 * qt + c, scale, lane, ev, ei);
+            N, qi, scale, lane, ev, ei);
         if (col == c) {
 #pragma unroll
           for (int m = 0; m < K; ++m) { val[qt][m] = ev[m]; ix[qt][m] = ei[m]; }
