@@ -56,7 +56,7 @@ VALUE_K = 2
 # The kernel the value call dispatches to at this shape (fp32, d=16, k=2,
 # N=256: the packed selection pass on split-bf16 scores). Its launch is what
 # rocprofv3 reports under this name.
-VALUE_KERNEL = "tarmac::topk_packed_kernel<float, 16, 2, 2, 1, 8, true, true>"
+VALUE_KERNEL = "tarmac::topk_packed_kernel<float, 16, 2, 2, 1, 10, true, true>"
 METRIC_FALLBACK = "µs/call attention core, top-k vs dense ratio, N=256 d=16 k=1,2,4; %HBM peak"
 
 

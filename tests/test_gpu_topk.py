@@ -4,11 +4,11 @@ fp32 bar: retained indices bit-exact against the canonical-order C oracle
 (same score rounding as the kernel), in the same (score desc, index asc) order
 for k <= 8; outputs within 1e-5 of max|ref| (normwise relative) against the
 float64 restatement of the reference's gather path wherever the k-th score is
-not a near-tie. bf16 bar: every retained set is admissible under the bf16-MFMA
-score error bound, and outputs are within 1e-2 of max|ref| against a float64
-evaluation over the kernel's own retained set; where bf16 runs the
-filter-and-verify kernel (d = 16, k >= 4, or forced), retained indices are
-bit-exact against the canonical-order C oracle on the bf16-rounded inputs.
+not a near-tie. bf16 bar: retained indices bit-exact against the
+canonical-order C oracle on the bf16-rounded inputs (the exact top k of the
+fp32 scores of the converted inputs, ties to the lower index) on every path
+and launch shape, and outputs within 1e-2 of max|ref| against a float64
+evaluation over that set.
 """
 
 from __future__ import annotations

@@ -108,6 +108,32 @@ __device__ __forceinline__ float quad_sum(float x) {
   return x + dpp_mov<kDppQuadXor2>(x);
 }
 
+// Sum over aligned groups of G consecutive lanes (G = 1, 2, 4, 8 or 16);
+// every lane of a group gets the group's sum. Within quads by DPP (VALU),
+// beyond by ds_swizzle in xor mode (no lane-index arithmetic).
+template <int G>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16, "group of 1..16 lanes");
+  if constexpr (G >= 2) x += dpp_mov<kDppQuadXor1>(x);
+  if constexpr (G >= 4) x += dpp_mov<kDppQuadXor2>(x);
+  if constexpr (G >= 8)
+    x += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1f | (4 << 10)));
+  if constexpr (G >= 16)
+    x += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1f | (8 << 10)));
+  return x;
+}
+
+// x of this lane plus x of the lane 16 (xor 16) or 32 (xor 32) away:
+// v_permlane16_swap / v_permlane32_swap, VALU only.
+__device__ __forceinline__ float add_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Reductions over the 16 lanes of a row (rotations by 8, 4, 2, 1: each step
 // adds a lane's partner's partial, so every lane ends with the same value).
 template <typename T, typename Op>

@@ -206,9 +206,7 @@ __device__ __forceinline__ float stage_bf16_norm(bf16* lds, const bf16* src, int
       if (v >= total) break;
       *reinterpret_cast<uint4*>(lds + row * LDK + cv * 8) = x[u];
       const uint32_t w[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
-      float n2 = sumsq_bf16x8(w);
-#pragma unroll
-      for (int o = 1; o < VPR; o <<= 1) n2 += __shfl_xor(n2, o);
+      const float n2 = group_sum<VPR>(sumsq_bf16x8(w));
       mx = fmaxf(mx, n2);
     }
   }
@@ -235,8 +233,7 @@ __device__ __forceinline__ float bf16_frag_norm2(const Frag<bf16, D>& f) {
       n2 += sumsq_bf16x8(a);
     }
   }
-  n2 += __shfl_xor(n2, 16);
-  return n2 + __shfl_xor(n2, 32);
+  return add_xor32(add_xor16(n2));
 }
 
 // ---------------------------------------------------------------------------

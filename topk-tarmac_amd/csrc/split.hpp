@@ -108,9 +108,7 @@ struct SplitFrag<16> {
     return n2;
   }
   // |q|^2 from the per-lane sums of load_q
-  __device__ __forceinline__ static float row_norm2(float part) {
-    return part + __shfl_xor(part, 16);
-  }
+  __device__ __forceinline__ static float row_norm2(float part) { return add_xor16(part); }
   struct KF { bf16x8 a[2]; };
   __device__ __forceinline__ static KF load_k(const bf16* krow, int grp) {
     KF f;
@@ -151,10 +149,7 @@ struct SplitFragWide {
     }
     return n2;
   }
-  __device__ __forceinline__ static float row_norm2(float part) {
-    part += __shfl_xor(part, 16);
-    return part + __shfl_xor(part, 32);
-  }
+  __device__ __forceinline__ static float row_norm2(float part) { return add_xor32(add_xor16(part)); }
   struct KF { bf16x8 hi[NH], mid[NH], lo[NH]; };
   __device__ __forceinline__ static KF load_k(const bf16* krow, int grp) {
     KF f;
@@ -203,14 +198,17 @@ __device__ __forceinline__ float stage_split(bf16* lds, const float* src, int ro
   constexpr int U = kStageBatch;
   float mx = 0.f;
   const int total = rows_pad * VPR;  // a multiple of 64: whole wavefronts agree on v < total
+  const int avail = rows * VPR;      // vectors backed by source rows
+  // the rows are contiguous: vector v sits at byte 16 v of the chunk (a 32-bit
+  // offset from the uniform base)
+  const char* base = reinterpret_cast<const char*>(src);
   for (int v0 = threadIdx.x; v0 < total; v0 += U * blockDim.x) {
     f32x4 x[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int v = v0 + u * blockDim.x, row = v / VPR, cv = v - row * VPR;
+      const int v = v0 + u * blockDim.x;
       x[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (v < total && row < rows)
-        x[u] = *reinterpret_cast<const f32x4*>(src + static_cast<size_t>(row) * D + 4 * cv);
+      if (v < avail) x[u] = *reinterpret_cast<const f32x4*>(base + static_cast<uint32_t>(v) * 16u);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -225,9 +223,8 @@ __device__ __forceinline__ float stage_split(bf16* lds, const float* src, int ro
       *reinterpret_cast<uint2*>(dst + SplitFrag<D>::OFF_H) = hi;
       *reinterpret_cast<uint2*>(dst + SplitFrag<D>::OFF_M) = mid;
       *reinterpret_cast<uint2*>(dst + SplitFrag<D>::OFF_L) = lo;
-      float n2 = x[u][0] * x[u][0] + x[u][1] * x[u][1] + x[u][2] * x[u][2] + x[u][3] * x[u][3];
-#pragma unroll
-      for (int o = 1; o < VPR; o <<= 1) n2 += __shfl_xor(n2, o);
+      const float n2 = group_sum<VPR>(
+          x[u][0] * x[u][0] + x[u][1] * x[u][1] + x[u][2] * x[u][2] + x[u][3] * x[u][3]);
       mx = fmaxf(mx, n2);
     }
   }

@@ -76,10 +76,7 @@ struct Bf16FilterFrag : Frag<bf16, D> {
       return n2;
     }
   }
-  __device__ __forceinline__ static float row_norm2(float part) {
-    part += __shfl_xor(part, 16);
-    return part + __shfl_xor(part, 32);
-  }
+  __device__ __forceinline__ static float row_norm2(float part) { return add_xor32(add_xor16(part)); }
 };
 
 // Per input type: the filter fragment, the LDS key row and its staging.

@@ -13,10 +13,12 @@
 // forms 16x16 S^T tiles with MFMA, so lane l owns query l % 16 and, per tile,
 // keys 4 * (l / 16) + r (r = 0..3).
 //
-//  1. scan: a score keeps its high bits and carries, in its low FB mantissa
-//     bits, a field naming the key within the current segment of 2^FB keys:
-//     bits [4, FB) the 16-key tile, bits 2..3 the row r, bits 0..1 left zero
-//     for the lane group (added at the merge). One bitfield insert per score,
+//  1. scan: a score keeps its high bits and carries, in its low fb mantissa
+//     bits, a field naming the key within the current segment of 2^fb keys:
+//     bits [4, fb) the 16-key tile, bits 2..3 the row r, bits 0..1 left zero
+//     for the lane group (added at the merge). A row of up to 1024 keys is one
+//     segment with the fewest bits that name its keys (fb = 8 at N = 256);
+//     longer rows use 10-bit segments. One bitfield insert per score,
 //     then a value-only insertion into a descending list of K + 1 entries
 //     (max / med3): K + 2 VALU operations per score and no index compares.
 //     Clearing low bits is a monotone map, so the list holds the K + 1 largest
@@ -163,11 +165,15 @@ __device__ __forceinline__ void finish_tile(const T* __restrict__ V, T* __restri
   }
 }
 
+// ONESEG: every key of the row fits one segment, and the field width is a
+// launch argument (fm_arg: the low-bit mask, 2^fb - 1 with 2^fb >= the row
+// rounded up to whole 16-key tiles), so short rows truncate less; FB is the
+// width of multi-segment rows.
 template <typename T, int D, int K, int QT, int NS, int FB, bool ONESEG, bool SPLIT>
 __global__ void __launch_bounds__(512)
 topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restrict__ V,
                    T* __restrict__ O, int32_t* __restrict__ Idx, int N, int n_qblk, int kc,
-                   float scale, int nblocks) {
+                   float scale, int nblocks, uint32_t fm_arg) {
   using PI = PackedIn<T, D, SPLIT>;
   using F = typename PI::F;
   using R = typename PI::R;  // LDS key row element
@@ -179,7 +185,7 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
   constexpr bool EXACT = sizeof(T) == 4 && !SPLIT;  // fp32 MFMA scores are the canonical scores
   constexpr bool RESCORE = sizeof(T) == 4;  // fp32 softmax needs the canonical scores
   constexpr bool POW2 = pow2_scale<D>();
-  constexpr uint32_t FM = (1u << FB) - 1u;
+  const uint32_t FM = ONESEG ? fm_arg : (1u << FB) - 1u;
   constexpr int SEGK = seg_keys<FB>();
   extern __shared__ __align__(16) unsigned char smem_raw[];
   unsigned* kmax_slot = reinterpret_cast<unsigned*>(smem_raw);  // approximate scores: max |k|^2
@@ -231,7 +237,9 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
     }
   float kmax2 = 0.f;
   int segbase = 0;  // first key of the current segment (uniform)
-  const uint32_t fmask = field_mask_vgpr<FB>();
+  uint32_t fmask;  // in a VGPR (see field_mask_vgpr)
+  if constexpr (ONESEG) asm volatile("v_mov_b32 %0, %1" : "=v"(fmask) : "s"(fm_arg));
+  else fmask = field_mask_vgpr<FB>();
 
   for (int c0 = 0; c0 < N; c0 += kc) {
     const int cn = min(kc, N - c0);
@@ -508,13 +516,25 @@ size_t packed_lds_bytes(int dtype, int d, int kc, bool split) {
   return 16 + static_cast<size_t>(kcb) * row;
 }
 
+// Field mask of a one-segment row of N keys: the fewest bits that name
+// every key of the row's whole 16-key tiles (at most 10: N <= 1024). Fewer
+// bits truncate scores less, so the proof fails on fewer near-ties; the width
+// depends on N alone, never on the key chunk, so a streamed row packs exactly
+// as a resident one.
+static uint32_t packed_field_mask(int N) {
+  const int n16 = (N + 15) / 16 * 16;
+  int fb = 4;
+  while ((1 << fb) < n16) ++fb;
+  return (1u << fb) - 1u;
+}
+
 template <typename T, int D, int K, int QT, int NS, int FB, bool ONESEG, bool SPLIT>
 static void launch_packed_k(const TopkArgs& a, int kc, int nblocks, int n_qblk, int nw, size_t lds) {
   hipLaunchKernelGGL((topk_packed_kernel<T, D, K, QT, NS, FB, ONESEG, SPLIT>), dim3(nblocks),
                      dim3(64 * nw), lds, static_cast<hipStream_t>(a.stream),
                      static_cast<const T*>(a.q), static_cast<const T*>(a.k),
                      static_cast<const T*>(a.v), static_cast<T*>(a.out), a.idx, a.N, n_qblk, kc,
-                     a.scale, nblocks);
+                     a.scale, nblocks, packed_field_mask(a.N));
 }
 
 template <typename T, int D, int K, int QT, bool SPLIT>
@@ -533,25 +553,18 @@ static hipError_t launch_packed_shape_q(const TopkArgs& a) {
   const int nblocks = a.B * n_qblk;
   const int kc = a.key_chunk;
   const size_t lds = packed_lds_bytes(a.dtype, D, kc, SPLIT);
-  // one segment when a single chunk holds the whole row: 8 field bits up to
-  // N = 256 (a truncation of 2^-15 of the score), 10 up to 1024. bf16 always
-  // packs 10 bits: its softmax runs on the truncated scores, which must not
-  // depend on whether the row is streamed.
-  if constexpr (sizeof(T) == 4) {
-    if (kc >= a.N && a.N <= 256) {
-      launch_packed_k<T, D, K, QT, NS, 8, true, SPLIT>(a, kc, nblocks, n_qblk, nw, lds);
-      return hipGetLastError();
-    }
-  }
+  // rows of up to 1024 keys are one segment whose field width follows N
+  // (packed_field_mask: 8 bits at N = 256, a truncation of 2^-15 of the
+  // score), resident or streamed alike
   if constexpr (QT == 1) {  // chosen for rows of up to 1024 keys only
     launch_packed_k<T, D, K, QT, NS, 10, true, SPLIT>(a, kc, nblocks, n_qblk, nw, lds);
     return hipGetLastError();
   } else {
-  // a row of up to 1024 keys is one segment of 10-bit fields whether it is
-  // resident or streamed in chunks (the fields hold absolute keys): the
-  // lists stay packed across chunks, with no per-chunk flush to (score, key)
-  // pairs (fp32 B=256 N=1024 in 576-key chunks, k = 1 / 2 / 4: 70.6 / 82.4 /
-  // 145.2 -> 65.1 / 72.0 / 90.4 us, identical results)
+  // a row of up to 1024 keys is one segment whether it is resident or
+  // streamed in chunks (the fields hold absolute keys): the lists stay packed
+  // across chunks, with no per-chunk flush to (score, key) pairs (fp32 B=256
+  // N=1024 in 576-key chunks, k = 1 / 2 / 4: 70.6 / 82.4 / 145.2 -> 65.1 /
+  // 72.0 / 90.4 us, identical results)
   if (a.N <= 1024)
     launch_packed_k<T, D, K, QT, NS, 10, true, SPLIT>(a, kc, nblocks, n_qblk, nw, lds);
   else
