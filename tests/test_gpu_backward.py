@@ -132,11 +132,42 @@ def test_dense_backward(N, d):
     _close(got, _ref_dense(q, k, v, g))
 
 
-def test_backward_rejects_bf16():
+HALF_TOL = {torch.bfloat16: 1e-2, torch.float16: 2e-3}
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("N,d,kk", [(6, 16, 2), (256, 16, 2), (300, 64, 12), (384, 32, 95)])
+def test_half_backward(dt, N, d, kk):
+    """bf16 / float16 heads: gradients (computed in fp32 on exact copies,
+    returned in the heads' dtype) against float64 autograd on the same
+    half-precision inputs, for the dense core (given the half-precision
+    forward output) and the top-k core (over the kernel's own retained
+    set). Bar: 1e-2 (bf16) / 2e-3 (float16) of the largest |ref| entry."""
+    from tarmac.kernels import (dense_attention_backward, fixedset_attention_backward,
+                                fused_dense_attention, topk_attention)
+    B = 2
+    q, k, v = qkv(13 * N + d, B, N, d)
+    g = np.random.default_rng(N + 7).standard_normal(q.shape).astype(np.float32)
+    qd, kd, vd, gd = (t.to(dt) for t in _dev(q, k, v, g))
+    q, k, v, g = (t.float().cpu().numpy() for t in (qd, kd, vd, gd))
+    out = fused_dense_attention(qd, kd, vd)
+    dense = dense_attention_backward(qd, kd, vd, out, gd)
+    _, idx = topk_attention(qd, kd, vd, kk, return_indices=True)
+    sets = fixedset_attention_backward(qd, kd, vd, idx, gd)
+    torch.cuda.synchronize()
+    assert all(x.dtype == dt for x in dense + sets)
+    for got, want in ((dense, _ref_dense(q, k, v, g)),
+                      (sets, _ref_set(q, k, v, idx.cpu().numpy(), g))):
+        scale = max(np.abs(b).max() for b in want)
+        for a, b in zip(got, want):
+            assert np.abs(a.float().cpu().numpy() - b).max() <= HALF_TOL[dt] * scale
+
+
+def test_backward_rejects_mixed_dtypes():
     from tarmac.kernels import dense_attention_backward
-    q, k, v = (t.to(torch.bfloat16) for t in _dev(*qkv(1, 2, 16, 16)))
-    with pytest.raises(NotImplementedError):
-        dense_attention_backward(q, k, v, q, q)
+    q, k, v = _dev(*qkv(1, 2, 16, 16))
+    with pytest.raises(TypeError):
+        dense_attention_backward(q, k, v, q, q.to(torch.bfloat16))
 
 
 @pytest.mark.parametrize("N,d", [(6, 16), (256, 16), (300, 64), (700, 16)])

@@ -13,7 +13,10 @@ kernels do not take directly, on the GPU.
   ``expected_k`` must carry gradient to the gate.
 * ``msg_dim`` 12, 24, 40 (heads zero-padded to 16, 32, 64): forward against
   float64 with the kernel's own retained sets (1e-5), backward against float64
-  autograd (1e-4).
+  autograd (1e-4); the retained sets against the exact top k of the unpadded
+  scores off near-ties, fp32 and bf16 heads.
+* bf16 and float16 modules: forward against float64 on the module's own
+  weights and heads, backward to the projections.
 """
 
 from __future__ import annotations
@@ -171,6 +174,73 @@ def test_any_msg_dim(msg_dim, mode, k):
         msg = O.prescore_attention(q64, k64, v64, peers.cpu().numpy().astype(np.int64))
     ref = _finish64(mod, msg)
     assert np.abs(out.cpu().numpy() - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("msg_dim", [12, 24, 40])
+def test_padded_width_selects_on_unpadded_scores(msg_dim, dt):
+    """The top-k peers the module takes on padded, pre-scaled heads are the
+    exact top k of q.k / sqrt(msg_dim) on the unpadded heads (float64 over
+    the heads' own values), on every row whose k-th and (k+1)-th scores are
+    further apart than four times the fp32 score error bound; bf16 heads are
+    padded and scaled in fp32, so the bound is the same."""
+    from tarmac.agents.mappo import _to_width
+    from tarmac.kernels import topk_attention
+    n_agents, k = 48, 3
+    mod = _module("topk_gather", k, n_agents, msg_dim).to(dt)
+    x = _x(8, n_agents).to(dt)
+    with torch.no_grad():
+        q, kh, v = (t.contiguous() for t in mod.qkv(x).chunk(3, dim=-1))
+        qw, kw, vw, _ = _to_width(q, kh, v)
+        assert qw.dtype == torch.float32
+        peers = topk_attention(qw, kw, vw, k, return_indices=True)[1].cpu().numpy()
+    q64, k64 = (t.double().cpu().numpy() for t in (q, kh))
+    s = O.scores(q64, k64)
+    want = O.topk_indices(s, k)
+    far = ~O.near_tie_rows(s, k, 4 * O.score_error_bound(q64, k64).max(-1))
+    assert far.mean() > 0.9
+    assert np.array_equal(np.sort(peers, -1)[far], np.sort(want, -1)[far])
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("msg_dim", [12, 16])
+@pytest.mark.parametrize("mode,k", [("dense", 0), ("topk_gather", 2), ("zorder_k", 2)])
+def test_half_precision_module(mode, k, msg_dim, dt):
+    """bf16 and float16 modules (the reference's half-precision arms): the
+    forward against a float64 evaluation of the same module (its own weights
+    and heads, the kernel's own retained set) within the dtype's rounding
+    (3e-2 bf16, 4e-3 float16, of max|ref|), and a backward that reaches the
+    projections with finite gradients."""
+    from tarmac.agents.mappo import _to_width
+    from tarmac.kernels import topk_attention
+    n_agents = 24
+    g = np.random.default_rng(2)
+    pos = torch.from_numpy(g.random((4, n_agents, 2)).astype(np.float32)).cuda()
+    mod = _module(mode, k, n_agents, msg_dim).to(dt).train()
+    mod.collect_info = False
+    x = _x(4, n_agents).to(dt)
+    out, _ = mod(x, pos if mode == "zorder_k" else None)
+    assert out.dtype == dt
+    with torch.no_grad():
+        q, kh, v = (t.contiguous() for t in mod.qkv(x).chunk(3, dim=-1))
+        q64, k64, v64 = (t.double().cpu().numpy() for t in (q, kh, v))
+        if mode == "dense":
+            msg = O.dense_unfused(q64, k64, v64)
+        else:
+            if mode == "topk_gather":
+                qw, kw, vw, _ = _to_width(q, kh, v)
+                peers = topk_attention(qw, kw, vw, k, return_indices=True)[1].cpu().numpy()
+            else:
+                peers = O.canon_morton_window(pos.cpu().numpy(), k, 10)
+            msg = O.prescore_attention(q64, k64, v64, peers.astype(np.int64))
+    ref = _finish64(mod, msg)
+    tol = 3e-2 if dt == torch.bfloat16 else 4e-3
+    err = np.abs(out.detach().double().cpu().numpy() - ref).max()
+    assert err <= tol * np.abs(ref).max(), err
+    out.float().square().sum().backward()
+    for name in ("qkv.weight", "proj.weight"):
+        grad = mod.get_parameter(name).grad
+        assert grad is not None and torch.isfinite(grad).all() and grad.abs().sum() > 0, name
 
 
 def test_padded_width_backward_matches_float64_autograd():

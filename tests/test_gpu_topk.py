@@ -497,3 +497,43 @@ def test_empty_batch_returns_empty_outputs():
     assert all(t.shape == (0, 6, 16) for t in dense_attention_backward(q, q, q, o, q, st))
     assert all(t.shape == (0, 6, 16) for t in fixedset_attention_backward(q, q, q, idx, q))
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("N,d,kk", [(6, 16, 2), (256, 16, 2), (300, 8, 4), (512, 64, 12), (96, 32, 23)])
+def test_float16_inputs(N, d, kk):
+    """float16 heads run the fp32 kernels on exact fp32 copies: retained
+    indices bit-exact against the canonical C oracle on the float16 values,
+    outputs float16 within 2e-3 of max|ref| (one rounding of the fp32
+    result), for top-k (resident and streamed), dense, fixed-set and
+    Z-order."""
+    from tarmac.kernels import (fused_dense_attention, fused_prescore_attention,
+                                topk_attention, zorder_attention)
+    B = 3
+    q, k, v = (x.astype(np.float16).astype(np.float32) for x in qkv(N + 3 * d + kk, B, N, d))
+    qd, kd, vd = dev(q, k, v, dtype=torch.float16)
+    want, idx_c = O.canon_topk(q, k, v, kk)
+    out, idx = topk_attention(qd, kd, vd, kk, return_indices=True)
+    out_s, idx_s = topk_attention(qd, kd, vd, kk, return_indices=True, key_chunk=64)
+    dense = fused_dense_attention(qd, kd, vd)
+    fixed = fused_prescore_attention(qd, kd, vd, idx)
+    pos = np.random.default_rng(N).random((B, N, 2)).astype(np.float32)
+    zo, zidx = zorder_attention(qd, kd, vd, torch.from_numpy(pos).cuda(), kk, 10,
+                                return_indices=True)
+    torch.cuda.synchronize()
+    assert all(t.dtype == torch.float16 for t in (out, out_s, dense, fixed, zo))
+    if kk > 8:  # k > 8 returns each set in ascending index order
+        idx_c = np.sort(idx_c, -1)
+    assert np.array_equal(idx.cpu().numpy(), idx_c)
+    assert np.array_equal(idx_s.cpu().numpy(), idx_c)
+
+    def close(got, ref):
+        assert np.abs(got.float().cpu().numpy() - ref).max() <= 2e-3 * np.abs(ref).max()
+
+    close(out, want)
+    close(out_s, want)
+    close(fixed, want)
+    close(dense, O.dense_unfused(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64)))
+    zi = zidx.cpu().numpy()
+    assert np.array_equal(zi, O.canon_morton_window(pos, kk, 10))
+    close(zo, O.prescore_attention(q.astype(np.float64), k.astype(np.float64),
+                                   v.astype(np.float64), zi.astype(np.int64)))

@@ -4,6 +4,7 @@ contiguity and alignment, stream handles. No compute happens here."""
 from __future__ import annotations
 
 import ctypes
+import functools
 
 import torch
 
@@ -16,7 +17,8 @@ def dtype_code(t: torch.Tensor) -> int:
     try:
         return _DTYPES[t.dtype]
     except KeyError:
-        raise TypeError(f"tarmac kernels take float32 or bfloat16 tensors, got {t.dtype}") from None
+        raise TypeError(f"tarmac kernels take float32 or bfloat16 tensors (float16 through "
+                        f"the Python wrappers), got {t.dtype}") from None
 
 
 def on_gpu(*ts: torch.Tensor) -> None:
@@ -54,3 +56,24 @@ def core(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
         raise TypeError("q, k and v must share a dtype")
     dtype_code(q)
     return ready(q), ready(k), ready(v)
+
+
+def half_on_f32(fn):
+    """Let a forward wrapper ``fn(q, k, v, ...)`` take float16 heads: they run
+    the fp32 kernels on fp32 copies. Every float16 value is an fp32 value, so
+    the scores and retained sets are those of the inputs themselves (the
+    exact top k of their canonical fp32 scores); the output comes back as
+    float16 (rounded once), indices unchanged."""
+
+    @functools.wraps(fn)
+    def wrapper(q, k, v, *args, **kwargs):
+        if q.dtype != torch.float16:
+            return fn(q, k, v, *args, **kwargs)
+        if not (k.dtype == v.dtype == torch.float16):
+            raise TypeError("q, k and v must share a dtype")
+        res = fn(q.float(), k.float(), v.float(), *args, **kwargs)
+        if isinstance(res, tuple):
+            return (res[0].to(torch.float16),) + tuple(res[1:])
+        return res.to(torch.float16)
+
+    return wrapper

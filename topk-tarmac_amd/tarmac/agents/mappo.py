@@ -31,14 +31,17 @@ core; their dense (B, N, N) formulations run as torch operations on the
 device, as in the reference. Any ``msg_dim`` up to 64 works: heads whose
 width the kernels do not take (fp32: 8, 16, 32, 64; bf16: 16, 32, 64) are
 zero-padded to the next width, with q pre-scaled by sqrt(width / msg_dim) so
-that scores keep the 1/sqrt(msg_dim) scale.
+that scores keep the 1/sqrt(msg_dim) scale; that padding and scaling happen
+in fp32 (bf16 heads are widened first, exactly), so the only perturbation of
+the scores is fp32 rounding. float16 heads run the fp32 kernels on exact
+fp32 copies. Messages return in the heads' dtype.
 
 The reference's Triton kernels are forward-only
 (``scripts/bench_attention_core.py:172-176``) and its training differentiates
 the PyTorch composition; here the core's backward runs on HIP kernels too
-(:mod:`tarmac.kernels.backward`, fp32): gradients reach q, k, v through the
-retained set of the top-k and Z-order cores, and through every pair of the
-dense core.
+(:mod:`tarmac.kernels.backward`, fp32 arithmetic for every head dtype):
+gradients reach q, k, v through the retained set of the top-k and Z-order
+cores, and through every pair of the dense core.
 """
 
 from __future__ import annotations
@@ -66,7 +69,8 @@ HIP_MODES = ("dense", "dense_sdpa", "topk", "topk_gather", "zorder_k", "random_k
 TORCH_MODES = ("entmax", "adaptive_topk")
 
 #: Head widths the HIP kernels take, per dtype.
-_WIDTHS = {torch.float32: (8, 16, 32, 64), torch.bfloat16: (16, 32, 64)}
+_WIDTHS = {torch.float32: (8, 16, 32, 64), torch.bfloat16: (16, 32, 64),
+           torch.float16: (8, 16, 32, 64)}
 
 
 @dataclass
@@ -91,13 +95,13 @@ def _ortho_init(layer: nn.Linear, gain: float = np.sqrt(2.0)) -> None:
 
 
 class _DenseCore(torch.autograd.Function):
-    """Dense core with the HIP backward (fp32)."""
+    """Dense core with the HIP backward (fp32 arithmetic)."""
 
     @staticmethod
     def forward(ctx, q, k, v):
         if q.dtype == torch.float32:
             out, stats = dense_attention_forward_stats(q, k, v)
-        else:  # the backward raises for bf16; nothing to keep
+        else:  # bf16 / float16: the backward recomputes the statistics in fp32
             out, stats = fused_dense_attention(q, k, v), None
         ctx.save_for_backward(q, k, v, out, stats)
         return out
@@ -142,11 +146,14 @@ def _kernel_width(d: int, dtype: torch.dtype) -> int:
 
 def _to_width(q, k, v):
     """Zero-pad the heads to a width the kernels take; q is scaled so that
-    q'.k' / sqrt(width) = q.k / sqrt(d). Returns (q', k', v', d)."""
+    q'.k' / sqrt(width) = q.k / sqrt(d). Padded heads are fp32 (bf16 and
+    float16 values widen exactly, so the scaling rounds once, at fp32).
+    Returns (q', k', v', d)."""
     d = q.shape[-1]
     w = _kernel_width(d, q.dtype)
     if w == d:
         return q, k, v, d
+    q, k, v = q.float(), k.float(), v.float()
     pad = (0, w - d)
     return (F.pad(q * math.sqrt(w / d), pad), F.pad(k, pad), F.pad(v, pad), d)
 
@@ -285,7 +292,7 @@ class AttentionComm(nn.Module):
             raise ValueError("attn_mode='zorder_k' needs agent positions")
         qw, kw, vw, d = _to_width(q, k, v)
         msg, info = self._core(mode, q, k, qw, kw, vw, pos, B, N)
-        return self.proj(F.gelu(msg[..., :d])), info
+        return self.proj(F.gelu(msg[..., :d].to(q.dtype))), info
 
     def _core(self, mode, q, k, qw, kw, vw, pos, B: int, N: int) -> tuple[torch.Tensor, dict]:
         """The HIP core on kernel-width heads (qw, kw, vw); q, k are the

@@ -1,4 +1,4 @@
-"""Backward passes of the attention core (fp32, HIP).
+"""Backward passes of the attention core (HIP, fp32 arithmetic).
 
 The reference's Triton kernels are forward-only
 (``scripts/bench_attention_core.py:172-176``); in training it differentiates
@@ -11,9 +11,18 @@ the GPU:
   the retained scores and value rows, as for ``torch.topk``'s gather), the
   Z-order core with its selector's set, and prescore attention.
 * ``dense_attention_backward`` -- the dense core (self pair excluded).
+
+bf16 and float16 heads are differentiated in fp32: every operand is copied to
+fp32 (exactly: bf16 and float16 values are fp32 values), the fp32 kernels run,
+and the gradients come back rounded once to the heads' dtype -- the gradient
+of the attention function at the given inputs, with fp32 accumulation, where
+autograd through the reference's half-precision composition would round its
+intermediates as well.
 """
 
 from __future__ import annotations
+
+import functools
 
 import torch
 
@@ -23,9 +32,34 @@ from .. import _launch, _lib
 def _f32(*ts):
     for t in ts:
         if t.dtype != torch.float32:
-            raise NotImplementedError("the backward kernels take fp32 tensors")
+            raise TypeError(f"q, out and dout must share the heads' dtype, got {t.dtype}")
 
 
+def _grads_on_f32(fn):
+    """Run a backward ``fn(q, k, v, ...) -> (dq, dk, dv)`` for bf16 / float16
+    heads on fp32 copies of its floating-point operands; gradients are
+    returned in the heads' dtype."""
+
+    @functools.wraps(fn)
+    def wrapper(q, k, v, *args, **kwargs):
+        dt = q.dtype
+        if dt == torch.float32:
+            return fn(q, k, v, *args, **kwargs)
+        if dt not in (torch.bfloat16, torch.float16):
+            raise TypeError(f"the backward takes float32, bfloat16 or float16 heads, got {dt}")
+
+        def up(t):
+            if isinstance(t, torch.Tensor) and t.is_floating_point() and t.dtype == dt:
+                return t.float()
+            return t
+
+        grads = fn(up(q), up(k), up(v), *map(up, args), **{n: up(a) for n, a in kwargs.items()})
+        return tuple(g.to(dt) for g in grads)
+
+    return wrapper
+
+
+@_grads_on_f32
 def fixedset_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                 idx: torch.Tensor, dout: torch.Tensor):
     """Gradients (dq, dk, dv) of ``softmax(q k_S^T / sqrt(d)) v_S`` over the
@@ -60,7 +94,10 @@ def dense_attention_forward_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
     backward needs: ``(out, stats)``, stats ``[B, 2, N]`` with plane 0 the
     log2-domain logsumexp of the scaled scores."""
     q, k, v = _launch.core(q, k, v)
-    _f32(q)
+    if q.dtype != torch.float32:
+        raise NotImplementedError(
+            "dense_attention_forward_stats takes fp32 heads; a bf16 / float16 forward is "
+            "fused_dense_attention, and dense_attention_backward without stats recomputes them")
     B, N, d = q.shape
     out = torch.empty_like(q)
     stats = torch.empty(B, 2, N, device=q.device, dtype=torch.float32)
@@ -73,6 +110,7 @@ def dense_attention_forward_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
     return out, stats
 
 
+@_grads_on_f32
 def dense_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                              out: torch.Tensor, dout: torch.Tensor,
                              stats: torch.Tensor | None = None):

@@ -14,6 +14,7 @@ import torch
 from .. import _launch, _lib
 
 
+@_launch.half_on_f32
 def fused_dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           block_m: int | None = None,
                           block_kn: int | None = None,

@@ -12,6 +12,7 @@ import torch
 from .. import _launch, _lib
 
 
+@_launch.half_on_f32
 def fused_prescore_attention(q: torch.Tensor, k: torch.Tensor,
                              v: torch.Tensor, idx: torch.Tensor,
                              block_m: int | None = None) -> torch.Tensor:

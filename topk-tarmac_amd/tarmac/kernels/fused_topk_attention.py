@@ -33,6 +33,7 @@ def _check_precision(precision: str) -> None:
         raise ValueError(f"precision={precision!r}: gfx950 has no TF32 mode; use 'ieee'")
 
 
+@_launch.half_on_f32
 def topk_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, topk: int,
                    return_indices: bool = False, key_chunk: int | None = None):
     """Exact top-k attention. ``topk`` is clamped to [1, N-1]. With
@@ -87,6 +88,7 @@ def fused_topk_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return topk_attention(q, k, v, topk)
 
 
+@_launch.half_on_f32
 def topk_variant_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, topk: int,
                            variant: int, bisect: int = 34,
                            return_indices: bool = False):

@@ -113,6 +113,7 @@ def prescore_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return fused_prescore_attention(q, k, v, idx)
 
 
+@_launch.half_on_f32
 def zorder_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.Tensor,
                      topk: int, bits: int = 10, return_indices: bool = False):
     """``prescore_attention(q, k, v, select_morton_window(pos, topk, bits))`` in
