@@ -54,9 +54,9 @@ B, N, D = 1024, 256, 16
 KS = (1, 2, 4)
 VALUE_K = 2
 # The kernel the value call dispatches to at this shape (fp32, d=16, k=2,
-# N=256: the packed selection pass on split-bf16 scores). Its launch is what
-# rocprofv3 reports under this name.
-VALUE_KERNEL = "tarmac::topk_packed_kernel<float, 16, 2, 2, 1, 10, true, true>"
+# N=256: packed selection on split-bf16 scores from 32 x 32 MFMA tiles). Its
+# launch is what rocprofv3 reports under this name.
+VALUE_KERNEL = "tarmac::topk_split32_kernel<2>"
 METRIC_FALLBACK = "µs/call attention core, top-k vs dense ratio, N=256 d=16 k=1,2,4; %HBM peak"
 
 
@@ -301,10 +301,10 @@ def main() -> int:
                              "fixedset2", "zorder", "stream2", "large95", "dense_small"],
                     help="run only this kernel (headline shape; zorder/stream at their configs) "
                          "--warmup + --steps times, for profiler counter passes")
-    ap.add_argument("--topk-filter", type=int, default=None, choices=[0, 1, 2, 3, 4],
+    ap.add_argument("--topk-filter", type=int, default=None, choices=[0, 1, 2, 3, 4, 5],
                     help="top-k implementation for --profile-kernel runs (tarmac_set_topk_filter: "
                          "0 packed, 1 automatic, 2 filter-and-verify, 3 register lists, "
-                         "4 packed on split-bf16 scores)")
+                         "4 packed on split-bf16 scores, 5 the same on 32 x 32 tiles)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 64 MiB device copy (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()

@@ -224,6 +224,8 @@ int tarmac_dense_bwd_noalloc(const float* q, const float* k, const float* v, con
  *   packed split -- the packed pass on split-bf16 scores (fp32 inputs,
  *                   d = 16: x = hi + mid + lo, six bf16 products per score),
  *                   proven against the split error bound;
+ *   split32      -- the same on 32-key x 32-query tiles (fp32, d = 16,
+ *                   k <= 4, N <= 1024): two lanes per query instead of four;
  *   filter       -- all pairs scored on split-bf16 MFMA (fp32 inputs) or
  *                   bf16 MFMA (bf16, d = 16), k+1 candidates rescored in the
  *                   canonical fp32 order and proven against the bf16 bound;
@@ -233,13 +235,17 @@ int tarmac_dense_bwd_noalloc(const float* q, const float* k, const float* v, con
  * recomputed by one wavefront from its canonical scores (per-lane lists
  * merged across the wave); the other queries of its tile keep their proven
  * sets. The lists path selects on canonical scores and needs no proof.
- * bf16 exactness rests on a stated bound for the bf16 MFMA accumulation
- * error (2^-21.9 of the sum of product magnitudes, measured on gfx950, with
- * eps = 2^-18 at d <= 32 and 2^-17 at d = 64 as the proof's margin).
+ * The exactness of the bf16 and split-bf16 proofs rests on a bound for the
+ * bf16 MFMA's fp32 accumulation error that is measured, not derived: at most
+ * 2^-20.25 of the sum of product magnitudes (worst seen on gfx950: 2^-20.5,
+ * one dominant product among small ones; tarmac_mfma_bf16_probe measures
+ * it), inside eps = 2^-18 at d <= 32 and 2^-17 at d = 64 together with the
+ * canonical chain's d 2^-24.
  * mode: 0 = packed always, 1 = automatic (default; the fastest measured on
  * MI355X for the shape), 2 = filter where supported (fp32 d = 16, 32, 64;
  * bf16 d = 16), 3 = lists for fp32 (bf16 runs packed), 4 = packed split where
- * supported (fp32 d = 16; packed elsewhere). bf16 retained sets are always
+ * supported (fp32 d = 16; packed elsewhere), 5 = split32 where supported
+ * (packed split, then packed, elsewhere). bf16 retained sets are always
  * the exact top k of the canonical fp32 scores of the inputs converted to
  * fp32. Process-wide (an atomic setting: concurrent calls stay safe and get
  * identical results). Returns the previous mode, or -1 (and sets the last
@@ -251,6 +257,7 @@ int tarmac_dense_bwd_noalloc(const float* q, const float* k, const float* v, con
 #define TARMAC_FILTER_ALWAYS 2
 #define TARMAC_FILTER_LISTS 3
 #define TARMAC_FILTER_PACKED_SPLIT 4
+#define TARMAC_FILTER_SPLIT32 5
 int tarmac_set_topk_filter(int mode);
 
 /*

@@ -121,7 +121,7 @@ def test_python_wrappers_mirror_reference_asserts():
 
 
 def test_filter_mode_switch():
-    """tarmac_set_topk_filter: modes 0 to 4 return the previous mode; anything
+    """tarmac_set_topk_filter: modes 0 to 5 return the previous mode; anything
     else is refused with -1 and a message, leaving the mode unchanged."""
     from tarmac import _lib
     lib = _lib.LIB
@@ -130,9 +130,10 @@ def test_filter_mode_switch():
         assert lib.tarmac_set_topk_filter(2) == 1
         assert lib.tarmac_set_topk_filter(3) == 2
         assert lib.tarmac_set_topk_filter(4) == 3
-        assert lib.tarmac_set_topk_filter(0) == 4
+        assert lib.tarmac_set_topk_filter(5) == 4
+        assert lib.tarmac_set_topk_filter(0) == 5
         assert lib.tarmac_set_topk_filter(7) == -1
-        assert "mode must be 0 to 4" in _lib.last_error()
+        assert "mode must be 0 to 5" in _lib.last_error()
         assert lib.tarmac_set_topk_filter(-1) == -1
         assert lib.tarmac_set_topk_filter(1) == 0
     finally:

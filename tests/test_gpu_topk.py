@@ -60,7 +60,8 @@ def check_f32(q, k, v, kk, out, idx, exact_order=True):
 def _set_filter(mode: int) -> int:
     """0 = packed pass (fp32 MFMA scores), 1 = automatic, 2 = split-bf16
     filter-and-verify wherever supported, 3 = register-list pass (fp32),
-    4 = packed pass on split-bf16 scores (fp32, d = 16)."""
+    4 = packed pass on split-bf16 scores (fp32, d = 16), 5 = the same on
+    32 x 32 score tiles (fp32, d = 16, k <= 4, N <= 1024)."""
     from tarmac import _lib
     return _lib.LIB.tarmac_set_topk_filter(mode)
 
@@ -81,7 +82,7 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("mode", [0, 2, 3, 4], ids=["packed", "filter", "lists", "split"])
+@pytest.mark.parametrize("mode", [0, 2, 3, 4, 5], ids=["packed", "filter", "lists", "split", "split32"])
 @pytest.mark.parametrize("N,d,kk", CASES)
 def test_fused_topk_f32_parity(N, d, kk, mode):
     B = max(2, min(16, 4096 // N))

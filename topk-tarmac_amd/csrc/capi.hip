@@ -358,8 +358,8 @@ int tarmac_dense_bwd_noalloc(const float* q, const float* k, const float* v, con
 }
 
 int tarmac_set_topk_filter(int mode) {
-  if (mode < tarmac::kFilterOff || mode > tarmac::kFilterPackedSplit) {
-    fail(TARMAC_ERR_INVALID, "tarmac_set_topk_filter: mode must be 0 to 4 (got %d)", mode);
+  if (mode < tarmac::kFilterOff || mode > tarmac::kFilterSplit32) {
+    fail(TARMAC_ERR_INVALID, "tarmac_set_topk_filter: mode must be 0 to 5 (got %d)", mode);
     return -1;
   }
   return tarmac::set_topk_filter_mode(mode);

@@ -132,6 +132,12 @@ __device__ __forceinline__ float pack8(float s, uint32_t u) {
   return __uint_as_float(__builtin_amdgcn_perm(__float_as_uint(s), u, 0x07060500u));
 }
 
+// Score s with its low bits (mask m) replaced by field f (f <= m): one
+// v_and_or_b32 (with m in a VGPR and f in an SGPR).
+__device__ __forceinline__ float pack_field(float s, uint32_t f, uint32_t m) {
+  return __uint_as_float((__float_as_uint(s) & ~m) | f);
+}
+
 // Value-only insertion into a descending list: L max/med3 operations.
 template <int L>
 __device__ __forceinline__ void vinsert(float (&v)[L], float s) {

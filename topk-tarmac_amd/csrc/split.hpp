@@ -9,11 +9,14 @@
 namespace tarmac {
 
 // bf16 score error bound, relative to |q| |k_j|: bf16 MFMA sums exact
-// products with an accumulation error measured <= 2^-21.9 of the sum of
-// their magnitudes; the canonical fp32 chain adds <= d 2^-24 of it (one
-// rounding per step); sum_c |q_c k_c| <= |q| |k_j|. 2^-18 (d <= 32) and
-// 2^-17 (d = 64) cover both with margin, including the fp32 rounding of the
-// bound itself.
+// products with an fp32 accumulation error that is measured, not derived
+// (at most 2^-20.25 of the sum of their magnitudes, the worst seen 2^-20.5:
+// one dominant product among small ones, on 16x16x32 and 32x32x16 chains of
+// up to 96 products); the canonical fp32 chain adds <= d 2^-24 of it (one
+// rounding per step); split scores drop three products of <= 2^-24 each;
+// sum_c |q_c k_c| <= |q| |k_j|. 2^-18 (d <= 32) and 2^-17 (d = 64) cover the
+// sum with a margin of 1.25 or more, including the fp32 rounding of the bound
+// itself.
 template <int D>
 constexpr float packed_eps() {
   return D <= 32 ? 1.0f / 262144.0f : 1.0f / 131072.0f;

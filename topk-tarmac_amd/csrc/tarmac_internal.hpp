@@ -125,13 +125,16 @@ struct KnnArgs {
 hipError_t run_topk(const TopkArgs& a);
 hipError_t run_topk_filter(const TopkArgs& a);
 hipError_t run_topk_packed(const TopkArgs& a, bool split);
+bool split32_supported(const TopkArgs& a);  // fp32, d = 16, k <= 4, N <= 256, top-k rule
+hipError_t run_topk_split32(const TopkArgs& a);
+size_t split32_lds_bytes(int kc);
 bool topk_hist_supported(const TopkArgs& a);  // fp32, d = 16, k > 8, N <= 512
 hipError_t run_topk_hist(const TopkArgs& a);
 bool packed_split_supported(int dtype, int d);
 bool topk_filter_supported(int dtype, int d, int topk);
 // tarmac_set_topk_filter modes
 constexpr int kFilterOff = 0, kFilterAuto = 1, kFilterAlways = 2, kFilterLegacy = 3,
-              kFilterPackedSplit = 4;
+              kFilterPackedSplit = 4, kFilterSplit32 = 5;
 int topk_filter_mode();
 int set_topk_filter_mode(int mode);  // returns the previous mode
 // tarmac_set_query_tiles modes: 16-query tiles per wave in the dense, packed

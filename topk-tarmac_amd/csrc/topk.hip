@@ -1076,12 +1076,14 @@ bool one_query_tile(int B, int N) {
   return static_cast<long>(B) * ((N + 31) / 32) < 4L * kCUs;
 }
 
-enum TopkPath { kPathPacked, kPathPackedSplit, kPathFilter, kPathLists };
+enum TopkPath { kPathPacked, kPathPackedSplit, kPathSplit32, kPathFilter, kPathLists };
 
 // The implementation for k <= 8 (all return identical results). Automatic
 // choice from interleaved timings on MI355X (B = 1024 for fp32 d = 16, the
 // configs[1] sweep; the configs[2] bf16 grid), us:
-//   fp32, d = 16: the packed pass on split-bf16 scores from N = 160, and
+//   fp32, d = 16: split-bf16 scores on 32 x 32 tiles (topk_split32.hip)
+//     for k <= 4 and N = 128 .. 256 at batches of two query tiles per wave;
+//     otherwise the packed pass on split-bf16 scores from N = 160, and
 //     at N = 128 for k >= 3 with B >= 1024 (see choose_path) (N=256
 //     k=1: 28.4 vs lists 30.4; k=2: 31.1 vs 37.1 lists, 34.5 filter; k=4:
 //     38.1 vs 44.1 filter, 56.5 lists; N=512 k=2: 83.5 vs 96.2 filter, 117.4
@@ -1103,6 +1105,8 @@ static TopkPath choose_path(const TopkArgs& a, int mode) {
     case kFilterAlways: return filt ? kPathFilter : kPathPacked;
     case kFilterLegacy: return a.dtype == kF32 ? kPathLists : kPathPacked;
     case kFilterPackedSplit: return split ? kPathPackedSplit : kPathPacked;
+    case kFilterSplit32:
+      return split32_supported(a) ? kPathSplit32 : (split ? kPathPackedSplit : kPathPacked);
     default: break;
   }
   if (a.dtype == kBf16) {
@@ -1119,6 +1123,12 @@ static TopkPath choose_path(const TopkArgs& a, int mode) {
     if (filt && a.N >= 256 && (a.topk >= 4 || (a.topk >= 2 && a.B <= 1024))) return kPathFilter;
     return kPathPacked;
   }
+  // split-bf16 scores on 32 x 32 tiles for rows of 128 to 256 keys once the
+  // batch gives every SIMD a wave of 32 queries (B=1024 N=256 k=1/2/4:
+  // 24.3/27.3/35.2 vs 26.2/28.6/35.9 on 16 x 16 tiles; N=128: 10.4/11.7/16.2
+  // vs 10.7 / 13.1 lists and 16.3 packed split; B=4096 N=256 k=2: 96.1 vs
+  // 99.5)
+  if (split32_supported(a) && a.N >= 128 && !one_query_tile(a.B, a.N)) return kPathSplit32;
   // split-bf16 scores from N = 160 at any k (B=1024 N=192 k=2/4: 26.0/32.3
   // vs 28.0 lists / 36.3 packed; B=4096 N=192 k=4: 111.2 vs 126.9), and at
   // N = 128 for k >= 3 once B >= 1024 (B=4096 N=128 k=3/4: 45.3/52.1 vs
@@ -1132,6 +1142,7 @@ hipError_t run_topk(const TopkArgs& a) {
     switch (choose_path(a, topk_filter_mode())) {
       case kPathPacked: return run_topk_packed(a, false);
       case kPathPackedSplit: return run_topk_packed(a, true);
+      case kPathSplit32: return run_topk_split32(a);
       case kPathFilter: return run_topk_filter(a);
       case kPathLists: break;
     }

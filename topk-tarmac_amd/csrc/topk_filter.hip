@@ -10,8 +10,9 @@
 //  1. filter: fp32 inputs: every (query, key) dot is formed from three-way
 //     split operands x = x_hi + x_mid + x_lo (bf16 each) with the six
 //     products of size >= 2^-16, which approximates the fp32 dot to
-//     |a - q.k| <= 2^-21 sum_c |q_c k_c| (representation 2^-22, bf16 MFMA
-//     accumulation measured <= 2^-21.9 of the term magnitudes). bf16 inputs:
+//     |a - q.k| < 2^-19.9 sum_c |q_c k_c| (three dropped products of
+//     <= 2^-24 each; the bf16 MFMA accumulation, measured at most 2^-20.25
+//     of the term magnitudes). bf16 inputs:
 //     one bf16 product (exact products, the same accumulation error). The
 //     canonical fp32 dot (d roundings) is within d 2^-24 sum_c |q_c k_c| of
 //     q.k. Selection runs on packed values (the
@@ -120,8 +121,8 @@ struct FilterIn<bf16, D> {
 // ---------------------------------------------------------------------------
 
 // Slack of the filter proof, relative to |q| max_j |k_j|: at least the
-// filter's error (2^-21) plus the canonical chain's (d 2^-24), with margin
-// for the fp32 arithmetic of the bound itself.
+// filter's error (< 2^-19.9) plus the canonical chain's (d 2^-24), with
+// margin for the fp32 arithmetic of the bound itself.
 template <int D>
 constexpr float filter_eps() {
   return D <= 32 ? 1.0f / 262144.0f : 1.0f / 131072.0f;  // 2^-18, 2^-17

@@ -19,13 +19,13 @@
 //     for the lane group (added at the merge). A row of up to 1024 keys is one
 //     segment with the fewest bits that name its keys (fb = 8 at N = 256);
 //     longer rows use 10-bit segments. One bitfield insert per score,
-//     then a value-only insertion into a descending list of K + 1 entries
-//     (max / med3): K + 2 VALU operations per score and no index compares.
-//     Clearing low bits is a monotone map, so the list holds the K + 1 largest
+//     then a value-only insertion into a descending list of K + 2 entries
+//     (max / med3): K + 3 VALU operations per score and no index compares.
+//     Clearing low bits is a monotone map, so the list holds the K + 2 largest
 //     truncated scores (distinct fields make distinct values).
 //  2. merge: the lane group goes into bits 0..1 and the four lane lists of a
 //     query merge with two xor-shuffle steps; every lane of the query ends with
-//     the same K + 1 entries.
+//     the same K + 2 entries.
 //  3. prove: fp32 scores come from fp32 MFMA and ARE the canonical scores, so
 //     if trunc(K-th) > trunc((K+1)-th) every key outside the first K has a
 //     strictly smaller score and the first K are exactly the top k. bf16 scores
@@ -70,12 +70,6 @@ __device__ __forceinline__ uint32_t field_mask_vgpr() {
   return m;
 }
 
-// Score s with its low bits (mask m) replaced by field f (f <= m): one
-// v_and_or_b32.
-__device__ __forceinline__ float pack_field(float s, uint32_t f, uint32_t m) {
-  return __uint_as_float((__float_as_uint(s) & ~m) | f);
-}
-
 // Key offset within its segment from a merged field (tile | r | grp).
 __device__ __forceinline__ int field_key(uint32_t w) {
   return static_cast<int>(16u * (w >> 4) + 4u * (w & 3u) + ((w >> 2) & 3u));
@@ -106,7 +100,7 @@ __device__ __forceinline__ void flush_packed(float (&pv)[QT][NS][L], float (&rv)
 // Scoring per input: the query fragment, the LDS key row (element type and
 // stride) and its staging. fp32: exact fp32 MFMA scores from plain rows, or
 // (SPLIT) bf16 MFMA on three-way split operands (x = hi + mid + lo), which
-// approximates the fp32 dot to 2^-21 sum_c |q_c k_c| at a third of the MFMA
+// approximates the fp32 dot to 2^-19.9 sum_c |q_c k_c| at a third of the MFMA
 // cycles; bf16: bf16 MFMA on the plain rows.
 template <typename T, int D, bool SPLIT>
 struct PackedIn;
