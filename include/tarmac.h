@@ -279,18 +279,22 @@ int tarmac_set_query_tiles(int mode);
 int tarmac_noop(float* out, void* stream);
 
 /*
- * Diagnostic: chains `chain` v_mfma_f32_16x16x32_bf16 instructions from +0
- * per tile and stores the 16 x 16 fp32 results, so a test can measure the
- * MFMA's fp32 accumulation error against exact sums -- the quantity the
- * bf16 and split-bf16 top-k proofs bound (see tarmac_set_topk_filter).
- * a, b: bf16 [tiles][chain][64 lanes][8] in the instruction's operand layout
- * (lane l: A row l % 16, columns 8 (l / 16) .. +7; B column l % 16, rows
- * 8 (l / 16) .. +7); out: fp32 [tiles][64 lanes][4] (lane l, element r:
- * row 4 (l / 16) + r, column l % 16). 16-byte aligned; 1 <= chain <= 64.
+ * Diagnostic: chains `chain` bf16 MFMA instructions from +0 per tile and
+ * stores the fp32 results, so a test can measure the MFMA's fp32 accumulation
+ * error against exact sums -- the quantity the bf16 and split-bf16 top-k
+ * proofs bound (see tarmac_set_topk_filter). shape 16:
+ * v_mfma_f32_16x16x32_bf16; a, b: bf16 [tiles][chain][64 lanes][8] in the
+ * instruction's operand layout (lane l: A row l % 16, columns 8 (l / 16) ..
+ * +7; B column l % 16, rows 8 (l / 16) .. +7); out: fp32 [tiles][64 lanes][4]
+ * (lane l, element r: row 4 (l / 16) + r, column l % 16). shape 32:
+ * v_mfma_f32_32x32x16_bf16; a, b as above with l % 32 and l / 32 (A row
+ * l % 32, columns 8 (l / 32) .. +7; B column l % 32, rows 8 (l / 32) .. +7);
+ * out: fp32 [tiles][64 lanes][16] (lane l, element i: row 8 (i / 4) +
+ * 4 (l / 32) + i % 4, column l % 32). 16-byte aligned; 1 <= chain <= 64.
  * No counterpart in the reference.
  */
 int tarmac_mfma_bf16_probe(const void* a, const void* b, float* out, int tiles, int chain,
-                           void* stream);
+                           int shape, void* stream);
 
 #ifdef __cplusplus
 }

@@ -7,10 +7,12 @@ E = eps(d) |q| max_j |k_j| (``packed_eps`` / ``filter_eps``: 2^-18 at d <= 32,
 
 * the MFMA's accumulation error, measured here on this device
   (``tarmac_mfma_bf16_probe``) against exact float64 sums, on random,
-  same-sign, mixed-magnitude and one-dominant-product operands, chained over
-  one, two and three 16x16x32 instructions (d = 32, 64 and the 96 products of
-  a split-bf16 score at d = 16): the bound asserted is 2^-20.25 (the worst
-  case seen is about 2^-20.5, one dominant product among small ones);
+  same-sign, mixed-magnitude, cancelling and one-dominant-product operands,
+  chained over one to three 16x16x32 instructions (d = 32, 64 and the 96
+  products of a split-bf16 score at d = 16 on 16 x 16 tiles) and one to six
+  32x32x16 instructions (the 32 x 32 split kernel chains six): the bound
+  asserted is 2^-20.25 (the worst case seen is about 2^-20.5, one dominant
+  product among small ones);
 * the canonical fmaf chain's error, at most d 2^-24 (one rounding per step);
 * for split-bf16 scores, the dropped products (mid.lo, lo.mid, lo.lo, each
   at most 2^-24 of |q_c k_c|).
@@ -45,31 +47,35 @@ def _bits_f64(b):
     return (b.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
 
 
-def _mfma_rel_error(Am, Bm):
-    """Am [T, chain, 16, 32], Bm [T, chain, 32, 16] (float32, rounded to bf16):
+def _mfma_rel_error(Am, Bm, shape=16):
+    """shape 16: Am [T, chain, 16, 32], Bm [T, chain, 32, 16]; shape 32:
+    Am [T, chain, 32, 16], Bm [T, chain, 16, 32] (float32, rounded to bf16):
     max over outputs of |MFMA - exact| / sum |products|."""
     from tarmac import _lib
     T, chain = Am.shape[:2]
+    M = Am.shape[2]  # 16 or 32 rows (= columns) of the result
     Ab, Bb = _bf16_bits(Am), _bf16_bits(Bm)
     la = np.zeros((T, chain, 64, 8), np.uint16)
     lb = np.zeros((T, chain, 64, 8), np.uint16)
     for lane in range(64):
-        i, g = lane % 16, lane // 16
+        i, g = lane % M, lane // M
         la[:, :, lane, :] = Ab[:, :, i, 8 * g:8 * g + 8]
         lb[:, :, lane, :] = Bb[:, :, 8 * g:8 * g + 8, i]
     da = torch.from_numpy(la.view(np.int16)).cuda()
     db = torch.from_numpy(lb.view(np.int16)).cuda()
-    out = torch.zeros(T, 64, 4, device="cuda")
+    per = 4 if shape == 16 else 16
+    out = torch.zeros(T, 64, per, device="cuda")
     rc = _lib.LIB.tarmac_mfma_bf16_probe(da.data_ptr(), db.data_ptr(), out.data_ptr(), T, chain,
-                                         None)
+                                         shape, None)
     _lib.check(rc)
     torch.cuda.synchronize()
     o = out.cpu().numpy()
-    got = np.zeros((T, 16, 16))
+    got = np.zeros((T, M, M))
     for lane in range(64):
-        j, g = lane % 16, lane // 16
-        for r in range(4):
-            got[:, 4 * g + r, j] = o[:, lane, r]
+        j, g = lane % M, lane // M
+        for r in range(per):
+            row = 4 * g + r if shape == 16 else 8 * (r // 4) + 4 * g + r % 4
+            got[:, row, j] = o[:, lane, r]
     Af, Bf = _bits_f64(Ab), _bits_f64(Bb)
     exact = np.einsum("tcik,tckj->tij", Af, Bf)
     mag = np.einsum("tcik,tckj->tij", np.abs(Af), np.abs(Bf))
@@ -85,14 +91,15 @@ PATTERNS = {
 }
 
 
-@pytest.mark.parametrize("chain", [1, 2, 3])
+@pytest.mark.parametrize("shape,chain", [(16, 1), (16, 2), (16, 3), (32, 1), (32, 2), (32, 6)])
 @pytest.mark.parametrize("pattern", list(PATTERNS))
-def test_mfma_accumulation_error_within_bound(pattern, chain):
-    g = np.random.default_rng(10 * list(PATTERNS).index(pattern) + chain)
-    T = 1024
-    Am = PATTERNS[pattern](g, (T, chain, 16, 32)).astype(np.float32)
-    Bm = PATTERNS[pattern](g, (T, chain, 32, 16)).astype(np.float32)
-    err = _mfma_rel_error(Am, Bm)
+def test_mfma_accumulation_error_within_bound(pattern, shape, chain):
+    g = np.random.default_rng(10 * list(PATTERNS).index(pattern) + chain + shape)
+    T = 1024 if shape == 16 else 256
+    rows, inner = (16, 32) if shape == 16 else (32, 16)
+    Am = PATTERNS[pattern](g, (T, chain, rows, inner)).astype(np.float32)
+    Bm = PATTERNS[pattern](g, (T, chain, inner, rows)).astype(np.float32)
+    err = _mfma_rel_error(Am, Bm, shape)
     assert err <= MFMA_ACC_BOUND, f"MFMA accumulation error {err:.3e} above the bound"
 
 
@@ -108,16 +115,21 @@ def test_proof_margins_cover_the_error_sources():
     assert split <= EPS[16] / 1.25
 
 
+@pytest.mark.parametrize("mode", [1, 4, 5], ids=["auto", "split16", "split32"])
 @pytest.mark.parametrize("d", [16, 32, 64])
 @pytest.mark.parametrize("dtype", ["bf16", "fp32"])
-def test_topk_exact_on_one_dominant_coordinate(d, dtype):
+def test_topk_exact_on_one_dominant_coordinate(d, dtype, mode):
     """Every score carries one dominant product (q_0 k_0 = 4096) and the
     ranking is decided by the small ones: the accumulation pattern with the
     largest MFMA error. Retained indices bit-exact against the canonical
-    oracle (bf16: on the bf16 inputs; fp32 d = 16 runs the split-bf16 pass)."""
+    oracle (bf16: on the bf16 inputs; fp32 d = 16 runs the split-bf16 pass
+    on 16 x 16 tiles (mode 4) and on 32 x 32 tiles (mode 5))."""
+    from tarmac import _lib
     from tarmac.kernels import topk_attention
     if dtype == "fp32" and d != 16:
         pytest.skip("split-bf16 scoring serves fp32 at d = 16")
+    if mode != 1 and not (dtype == "fp32" and d == 16):
+        pytest.skip("modes 4 and 5 select split-bf16 kernels (fp32, d = 16)")
     B, N = 8, 256
     g = np.random.default_rng(d)
     q = g.standard_normal((B, N, d)).astype(np.float32) / 8
@@ -129,8 +141,12 @@ def test_topk_exact_on_one_dominant_coordinate(d, dtype):
         q, k, v = (O.bf16_round(x) for x in (q, k, v))
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
     qd, kd, vd = (torch.from_numpy(x).cuda().to(tdt) for x in (q, k, v))
-    for kk in (1, 2, 4):
-        out, idx = topk_attention(qd, kd, vd, kk, return_indices=True)
-        torch.cuda.synchronize()
-        _, idx_c = O.canon_topk(q, k, v, kk)
-        assert np.array_equal(idx.cpu().numpy(), idx_c), f"k={kk}: indices differ from the oracle"
+    prev = _lib.LIB.tarmac_set_topk_filter(mode)
+    try:
+        for kk in (1, 2, 4):
+            out, idx = topk_attention(qd, kd, vd, kk, return_indices=True)
+            torch.cuda.synchronize()
+            _, idx_c = O.canon_topk(q, k, v, kk)
+            assert np.array_equal(idx.cpu().numpy(), idx_c), f"k={kk}: indices differ from the oracle"
+    finally:
+        _lib.LIB.tarmac_set_topk_filter(prev)

@@ -374,14 +374,15 @@ int tarmac_set_query_tiles(int mode) {
 }
 
 int tarmac_mfma_bf16_probe(const void* a, const void* b, float* out, int tiles, int chain,
-                           void* stream) {
+                           int shape, void* stream) {
   const char* fn = "tarmac_mfma_bf16_probe";
   if (!a || !b || !out) return fail(TARMAC_ERR_INVALID, "%s: null pointer", fn);
   if (!aligned(a, 16) || !aligned(b, 16) || !aligned(out, 16))
     return fail(TARMAC_ERR_INVALID, "%s: operands must be 16-byte aligned", fn);
   if (tiles < 1 || chain < 1 || chain > 64)
     return fail(TARMAC_ERR_INVALID, "%s: need tiles >= 1 and 1 <= chain <= 64", fn);
-  return hip_status(tarmac::run_mfma_bf16_probe(a, b, out, tiles, chain, stream), fn);
+  if (shape != 16 && shape != 32) return fail(TARMAC_ERR_INVALID, "%s: shape must be 16 or 32", fn);
+  return hip_status(tarmac::run_mfma_bf16_probe(a, b, out, tiles, chain, shape, stream), fn);
 }
 
 int tarmac_noop(float* out, void* stream) {

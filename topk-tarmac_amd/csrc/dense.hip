@@ -24,6 +24,7 @@
 // power-of-two scales; c = 1); bf16 scores stay raw and c = scale*log2(e) is
 // applied inside the exponent's argument, fma(s, c, -off).
 #include "frag.hpp"
+#include "select.hpp"
 #include "tarmac_internal.hpp"
 
 namespace tarmac {
@@ -112,13 +113,22 @@ __device__ __forceinline__ float sum_bf16x8(bf16x8 p, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.w), one, acc, false);
 }
 
+// max of two floats that are scores or -inf (never NaN): one v_max_f32,
+// without the canonicalising copies fmaxf adds for operands the compiler
+// cannot prove canonical (lane-swap results)
+__device__ __forceinline__ float max_plain(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 // Maximum over the four lanes of a query (lanes l, l + 16, l + 32, l + 48):
 // two row swaps, VALU only.
 __device__ __forceinline__ float query_max4(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  x = max_plain(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return max_plain(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 // Softmax terms are 2^(c s - off) with off a running maximum of c s that is
@@ -163,6 +173,9 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
   }
   // exponent factor c: 1 for fp32 (folded into q), scale*log2(e) for bf16
   const float post = (sizeof(T) == 4) ? 1.f : scale * kLog2e;
+  bool self_r[4];  // element r of a diagonal tile is this lane's self pair
+#pragma unroll
+  for (int r = 0; r < 4; ++r) self_r[r] = (4 * grp + r == col);
 
   f32x4 acc[QT][NH];
   float off[QT], l_run[QT];
@@ -190,17 +203,9 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
       f32x4 s[QT][BT];
       block_scores<F, QT, BT>(frag, Ks, kb0, LDK, lane, s);
       const int kabs = c0 + kb0;
-      if ((q0 < kabs + BK && kabs < q0 + 16 * QT) || kabs + BK > kend) {  // wave-uniform
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-          for (int t = 0; t < BT; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int key = kabs + 16 * t + 4 * grp + r;
-              if (key >= kend || key == q0 + 16 * qt + col) s[qt][t][r] = -INFINITY;
-            }
-      }
+      // the self pair (one select per element of a diagonal tile, on the
+      // loop-invariant lane predicates) and keys past the chunk end
+      mask_block<QT, BT>(s, self_r, q0, kabs, kend, grp, -INFINITY);
       float neg[QT];  // the exponent's offset
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {

@@ -16,30 +16,53 @@ hipError_t run_noop(float* out, void* stream) {
   return hipGetLastError();
 }
 
-// One wave per tile: chain v_mfma_f32_16x16x32_bf16 products from +0 and
-// store the 16 x 16 result. a, b: [T][chain][64 lanes][8] bf16 operands in
-// the instruction's lane layout; out: [T][64 lanes][4].
+typedef float f32x16_probe __attribute__((ext_vector_type(16)));
+
+// One wave per tile: chain bf16 MFMA products from +0 and store the result.
+// a, b: [T][chain][64 lanes][8] bf16 operands in the instruction's lane
+// layout; out: [T][64 lanes][4] (16x16x32) or [T][64 lanes][16] (32x32x16).
+template <int SHAPE>
 __global__ void __launch_bounds__(64)
 mfma_bf16_probe_kernel(const bf16* __restrict__ a, const bf16* __restrict__ b,
                        float* __restrict__ out, int T, int chain) {
   const int lane = threadIdx.x;
   for (int t = blockIdx.x; t < T; t += gridDim.x) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int c = 0; c < chain; ++c) {
-      const size_t off = (static_cast<size_t>(t) * chain + c) * 64 * 8 + static_cast<size_t>(lane) * 8;
-      acc = mfma_bf16_16x16x32(*reinterpret_cast<const bf16x8*>(a + off),
-                               *reinterpret_cast<const bf16x8*>(b + off), acc);
+    if constexpr (SHAPE == 16) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < chain; ++c) {
+        const size_t off = (static_cast<size_t>(t) * chain + c) * 64 * 8 + static_cast<size_t>(lane) * 8;
+        acc = mfma_bf16_16x16x32(*reinterpret_cast<const bf16x8*>(a + off),
+                                 *reinterpret_cast<const bf16x8*>(b + off), acc);
+      }
+      *reinterpret_cast<f32x4*>(out + (static_cast<size_t>(t) * 64 + lane) * 4) = acc;
+    } else {
+      f32x16_probe acc = {};
+      for (int c = 0; c < chain; ++c) {
+        const size_t off = (static_cast<size_t>(t) * chain + c) * 64 * 8 + static_cast<size_t>(lane) * 8;
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(a + off),
+                                                      *reinterpret_cast<const bf16x8*>(b + off),
+                                                      acc, 0, 0, 0);
+      }
+      float* dst = out + (static_cast<size_t>(t) * 64 + lane) * 16;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<f32x4*>(dst + 4 * q) =
+            f32x4{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
     }
-    *reinterpret_cast<f32x4*>(out + (static_cast<size_t>(t) * 64 + lane) * 4) = acc;
   }
 }
 
 hipError_t run_mfma_bf16_probe(const void* a, const void* b, float* out, int T, int chain,
-                               void* stream) {
+                               int shape, void* stream) {
   const int grid = T < 4096 ? T : 4096;
-  hipLaunchKernelGGL(mfma_bf16_probe_kernel, dim3(grid), dim3(64), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const bf16*>(a),
-                     static_cast<const bf16*>(b), out, T, chain);
+  if (shape == 32)
+    hipLaunchKernelGGL(mfma_bf16_probe_kernel<32>, dim3(grid), dim3(64), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const bf16*>(a),
+                       static_cast<const bf16*>(b), out, T, chain);
+  else
+    hipLaunchKernelGGL(mfma_bf16_probe_kernel<16>, dim3(grid), dim3(64), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const bf16*>(a),
+                       static_cast<const bf16*>(b), out, T, chain);
   return hipGetLastError();
 }
 

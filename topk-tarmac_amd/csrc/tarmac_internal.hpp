@@ -148,7 +148,7 @@ hipError_t run_morton_window(const MortonArgs& a);
 hipError_t run_zorder(const ZorderArgs& a);
 hipError_t run_noop(float* out, void* stream);
 hipError_t run_mfma_bf16_probe(const void* a, const void* b, float* out, int T, int chain,
-                               void* stream);
+                               int shape, void* stream);
 hipError_t run_fixedset_bwd(const FixedsetBwdArgs& a);
 hipError_t run_dense_bwd(const DenseBwdArgs& a);
 // Library-held device workspace (one per GPU, kScratchBytes): the current

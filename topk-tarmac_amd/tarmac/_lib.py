@@ -50,7 +50,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tarmac_set_topk_filter": ([_I], _I),
     "tarmac_set_query_tiles": ([_I], _I),
     "tarmac_noop": ([_P, _P], _I),
-    "tarmac_mfma_bf16_probe": ([_P, _P, _P, _I, _I, _P], _I),
+    "tarmac_mfma_bf16_probe": ([_P, _P, _P, _I, _I, _I, _P], _I),
 }
 
 
