@@ -150,6 +150,14 @@ __device__ __forceinline__ T row16_reduce_stride4(T x, Op op) {
   return op(x, dpp_mov<dpp_row_ror(4)>(x));
 }
 
+// max of two non-NaN floats: one v_max_f32, without the canonicalising copies
+// fmaxf adds for operands the compiler cannot prove canonical (lane moves)
+__device__ __forceinline__ float max_plain(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 // (a, ia) ranks before (b, ib): higher score first, lower index on ties.
 __device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
   return a > b || (a == b && ia < ib);

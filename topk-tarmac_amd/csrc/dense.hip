@@ -113,15 +113,6 @@ __device__ __forceinline__ float sum_bf16x8(bf16x8 p, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.w), one, acc, false);
 }
 
-// max of two floats that are scores or -inf (never NaN): one v_max_f32,
-// without the canonicalising copies fmaxf adds for operands the compiler
-// cannot prove canonical (lane-swap results)
-__device__ __forceinline__ float max_plain(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-
 // Maximum over the four lanes of a query (lanes l, l + 16, l + 32, l + 48):
 // two row swaps, VALU only.
 __device__ __forceinline__ float query_max4(float x) {

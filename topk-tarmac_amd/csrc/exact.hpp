@@ -69,13 +69,13 @@ __device__ __forceinline__ void gather_rows(uint32_t x, uint32_t (&v)[4]) {
 }
 
 // Maximum of x over the wave, in every lane: four DPP row rotations and two
-// row swaps (no LDS round trip). x >= 0 or NaN-free.
+// row swaps (no LDS round trip). x NaN-free.
 __device__ __forceinline__ float wave_max_rows(float x) {
-  x = row16_reduce(x, [](float a, float b) { return fmaxf(a, b); });
+  x = row16_reduce(x, [](float a, float b) { return max_plain(a, b); });
   const LanePair p = swap_rows16(__float_as_uint(x));
-  x = fmaxf(__uint_as_float(p.a), __uint_as_float(p.b));
+  x = max_plain(__uint_as_float(p.a), __uint_as_float(p.b));
   const LanePair q = swap_rows32(__float_as_uint(x));
-  return fmaxf(__uint_as_float(q.a), __uint_as_float(q.b));
+  return max_plain(__uint_as_float(q.a), __uint_as_float(q.b));
 }
 
 // ---------------------------------------------------------------------------

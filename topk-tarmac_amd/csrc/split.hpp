@@ -57,9 +57,13 @@ __device__ __forceinline__ void split3_pair(float x0, float x1, uint32_t& hi, ui
                                             uint32_t& lo, bool& exact) {
   bf16x2_t h = {static_cast<__bf16>(x0), static_cast<__bf16>(x1)};
   hi = __builtin_bit_cast(uint32_t, h);
+  // the halves come from the packed word (an opaque copy keeps the compiler
+  // from converting x0 a second time for the low half): 11 VALU per pair
+  asm("" : "+v"(hi));
   const float r0 = x0 - __uint_as_float(hi << 16), r1 = x1 - __uint_as_float(hi & 0xffff0000u);
   bf16x2_t m = {static_cast<__bf16>(r0), static_cast<__bf16>(r1)};
   mid = __builtin_bit_cast(uint32_t, m);
+  asm("" : "+v"(mid));
   const float s0 = r0 - __uint_as_float(mid << 16), s1 = r1 - __uint_as_float(mid & 0xffff0000u);
   bf16x2_t l = {static_cast<__bf16>(s0), static_cast<__bf16>(s1)};
   lo = __builtin_bit_cast(uint32_t, l);
@@ -210,8 +214,11 @@ __device__ __forceinline__ float stage_split(bf16* lds, const float* src, int ro
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int v = v0 + u * blockDim.x;
-      x[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (v < avail) x[u] = *reinterpret_cast<const f32x4*>(base + static_cast<uint32_t>(v) * 16u);
+      // zero only padding rows (the branch is skipped when no lane pads)
+      if (v < avail)
+        x[u] = *reinterpret_cast<const f32x4*>(base + static_cast<uint32_t>(v) * 16u);
+      else
+        x[u] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {

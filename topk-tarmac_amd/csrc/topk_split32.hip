@@ -187,16 +187,18 @@ topk_split32_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
           for (int i = 0; i < 16; ++i)
             s[t][i] = pack_field(s[t][i],
                                  static_cast<uint32_t>(kabs + 32 * t + 8 * (i >> 2) + (i & 3)), fmask);
-        // the self pair (in the blocks that overlap the wave's queries; a
-        // chunk may start at any multiple of 16 keys) and keys past the
-        // chunk end
-        if (kabs < q0 + 32 && q0 < kabs + 32 * BT) {
-          const int dq = qi - kabs - 4 * half;
+        // the self pair (in the tiles that overlap the wave's queries: one
+        // when the chunk starts at a multiple of 32 keys, two otherwise) and
+        // keys past the chunk end
 #pragma unroll
-          for (int t = 0; t < BT; ++t)
+        for (int t = 0; t < BT; ++t) {
+          const int kt = kabs + 32 * t;
+          if (kt < q0 + 32 && q0 < kt + 32) {  // wave-uniform
+            const int dq = qi - kt - 4 * half;
 #pragma unroll
             for (int i = 0; i < 16; ++i)
-              if (32 * t + 8 * (i >> 2) + (i & 3) == dq) s[t][i] = kMasked;
+              if (8 * (i >> 2) + (i & 3) == dq) s[t][i] = kMasked;
+          }
         }
         if (kabs + 32 * BT > kend) {
 #pragma unroll
