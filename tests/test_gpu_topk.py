@@ -107,6 +107,26 @@ def test_streaming_topk_matches_fused_bitwise(N, d, kk, chunk):
     check_f32(q, k, v, kk, out_s, idx_s)
 
 
+@pytest.mark.parametrize("N,kk,chunk", [(256, 2, 16), (256, 4, 64), (256, 1, 128), (200, 3, 48),
+                                        (256, 2, 80)])
+def test_split32_streamed_matches_resident_bitwise(N, kk, chunk):
+    """The 32 x 32 kernel (mode 5) over key chunks that start at any multiple
+    of 16 keys (the self pair then straddles two 32-key tiles, and rows end
+    inside a tile): identical indices and outputs to the resident row, and
+    to the oracle."""
+    B = 3
+    q, k, v = qkv(11 * N + kk + chunk, B, N, 16)
+    prev = _set_filter(5)
+    try:
+        out_s, idx_s = run_topk(q, k, v, kk, chunk=chunk)
+        out_f, idx_f = run_topk(q, k, v, kk)
+    finally:
+        _set_filter(prev)
+    assert np.array_equal(idx_s, idx_f)
+    assert np.array_equal(out_s, out_f)
+    check_f32(q, k, v, kk, out_s, idx_s)
+
+
 @pytest.mark.parametrize("N,d,kk", [(12, 16, 11), (24, 8, 23), (64, 16, 9), (200, 32, 40),
                                     (300, 16, 299)])
 def test_wide_k_parity(N, d, kk):
@@ -407,6 +427,38 @@ def test_sort_variant_keeps_higher_index_on_ties(N, d, kk, ties):
     assert np.abs(out.cpu().numpy() - ref).max() <= F32_TOL * np.abs(ref).max()
     if ties:  # the tie rule is visible: rows of +0 scores keep the top indices
         assert np.all(idx.cpu().numpy()[:, 0] == np.arange(N - kk, N))
+
+
+@pytest.mark.parametrize("N,d,kk,ties", [(6, 16, 2, False), (24, 16, 3, True), (256, 16, 2, True),
+                                         (256, 64, 8, False), (300, 32, 12, True),
+                                         (1024, 16, 4, True)])
+@pytest.mark.parametrize("rule", ["masked34", "masked32", "masked20", "masked5", "sort"])
+def test_bf16_variants_match_oracle(N, d, kk, ties, rule):
+    """bf16 heads: the masked and sort rules on the canonical fp32 scores of
+    the bf16 values (the list kernel on widened copies for sort / masked with
+    >= 32 halvings at k <= 8, the wide kernels otherwise), outputs within 1e-2
+    of the float64 softmax over the oracle's kept set; sort indices
+    bit-exact."""
+    from tarmac import _lib
+    from tarmac.kernels import topk_variant_attention
+    B = 3
+    q, k, v = (O.bf16_round(x) for x in _variant_inputs(5 * N + kk, B, N, d, ties))
+    qd, kd, vd = dev(q, k, v, dtype=torch.bfloat16)
+    s = O.canon_scores(q, k)
+    if rule == "sort":
+        out, idx = topk_variant_attention(qd, kd, vd, kk, _lib.VARIANT_SORT, return_indices=True)
+        want = O.sort_select(s, kk)
+        assert np.array_equal(idx.cpu().numpy(), np.sort(want, -1))
+        keep = np.zeros_like(s, dtype=bool)
+        np.put_along_axis(keep, want, True, -1)
+    else:
+        bis = int(rule[6:])
+        out = topk_variant_attention(qd, kd, vd, kk, _lib.VARIANT_MASKED, bis)
+        keep = O.masked_threshold_keep(s, kk, bis)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16
+    ref = O.weights_attention(s, keep, v)
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= BF16_TOL * np.abs(ref).max()
 
 
 @pytest.mark.parametrize("variant", ["masked", "sort"])

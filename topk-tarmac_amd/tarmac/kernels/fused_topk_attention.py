@@ -94,10 +94,24 @@ def topk_variant_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, to
                            return_indices: bool = False):
     """The reference's other two resident selection rules (one HIP launch):
     ``_lib.VARIANT_MASKED`` (threshold bisection) or ``_lib.VARIANT_SORT``
-    (ties keep the higher index). ``topk`` is clamped to [1, N-1]."""
+    (ties keep the higher index). ``topk`` is clamped to [1, N-1].
+
+    bf16 heads whose rule the fp32 register-list kernel serves (sort, or
+    masked with ``bisect`` >= 32; k <= 8; N <= 1024) run it on fp32 copies:
+    bf16 values widen exactly, so the kept sets are the rules' sets on the
+    canonical fp32 scores of the inputs, as the bf16 kernels define them, and
+    the output is the fp32 result rounded once to bf16."""
+    B, N = q.shape[0], q.shape[1]
+    kk = max(1, min(int(topk), N - 1))
+    if (q.dtype == torch.bfloat16 and k.dtype == v.dtype == torch.bfloat16 and kk <= 8
+            and N <= 1024 and (variant == _lib.VARIANT_SORT or int(bisect) >= 32)):
+        res = topk_variant_attention(q.float(), k.float(), v.float(), topk, variant, bisect,
+                                     return_indices)
+        if return_indices:
+            return res[0].to(torch.bfloat16), res[1]
+        return res.to(torch.bfloat16)
     q, k, v = _launch.core(q, k, v)
     B, N, d = q.shape
-    kk = max(1, min(int(topk), N - 1))
     out = torch.empty_like(q)
     idx = torch.empty(B, N, kk, device=q.device, dtype=torch.int32) if return_indices else None
     if B == 0:
