@@ -515,6 +515,21 @@ def main() -> int:
     si = {n: harness.stats(s) for n, s in
           harness.time_interleaved(fi, max(10, args.reps // 2), 3, 2).items()}
     detail["impls_bf16_B1024_N256_d16_us"] = {n: round(s["min_us"], 3) for n, s in si.items()}
+    # head width 128 (msg_dim 65 .. 128 after the module's padding), B=256 N=256
+    g8 = np.random.default_rng(1234 + 8 * 256 + 128)
+    q8, k8, v8 = (torch.from_numpy(g8.standard_normal((256, 256, 128)).astype(np.float32)).to(dev)
+                  for _ in range(3))
+    fi = {}
+    for tag, dt in (("f32", torch.float32), ("bf16", torch.bfloat16)):
+        qa, ka, va = (t.to(dt) for t in (q8, k8, v8))
+        fi[f"{tag}_dense_fused"] = (lambda qa=qa, ka=ka, va=va: fused_dense_attention(qa, ka, va))
+        for kk in (2, 4, 12):
+            fi[f"{tag}_topk_fused_gather_k{kk}"] = (
+                lambda qa=qa, ka=ka, va=va, kk=kk: topk_attention(qa, ka, va, kk))
+    si = {n: harness.stats(s) for n, s in
+          harness.time_interleaved(fi, max(10, args.reps // 2), 3, 2).items()}
+    detail["d128_B256_N256_us"] = {n: round(s["min_us"], 3) for n, s in si.items()}
+    del q8, k8, v8
     del fi, q7, k7, v7, qh, kh, vh
 
     # ---- streaming top-k, B=256, N in {512, 1024}, fp32 and bf16

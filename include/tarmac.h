@@ -10,6 +10,11 @@
  * exception: tarmac_dense_bwd_noalloc shares one library-held array per GPU,
  * so its calls that overlap on one GPU race (see its declaration).
  *
+ * Head widths d: 8, 16, 32, 64 or 128 for fp32, 16, 32, 64 or 128 for bf16
+ * (the module pads other msg_dim up to 128 with zeros). At d = 128, top-k
+ * with k <= 8 runs the packed kernel under every mode of
+ * tarmac_set_topk_filter, and larger k and the variants the wide kernels.
+ *
  * Scores are q.k / sqrt(d) with the self pair (i == i) excluded, as in every
  * path of the reference. Retained sets are the topk largest scores, ties to
  * the lower agent index. fp32 scores are formed in a fixed fmaf order
@@ -163,10 +168,10 @@ int tarmac_zorder_fwd(const void* q, const void* k, const void* v, const float* 
  * gather), of the Z-order core with its selector's set, and of prescore
  * attention. dq, dk and dv are written. Each key's dk, dv are summed over
  * the queries that retain it in ascending query order, so they are bitwise
- * reproducible, except in a batch row whose sets name a peer twice, or when N is too large for the
- * row's N x N bitmask in LDS (N above about 1100 at d = 16): there they are
- * summed with fp32 atomics, whose low bits depend on the order the adds land
- * in. No kernel counterpart in the reference (its Triton kernels are
+ * reproducible, except in a batch row whose sets name a peer twice, when N
+ * is too large for the row's N x N bitmask in LDS (N above about 1100 at
+ * d = 16), or at d = 128: there they are summed with fp32 atomics, whose low
+ * bits depend on the order the adds land in. No kernel counterpart in the reference (its Triton kernels are
  * forward-only, scripts/bench_attention_core.py:172-176); replaces autograd
  * through src/agents/mappo.py:192-231 in src/training/train_mappo.py:366.
  */
@@ -239,8 +244,8 @@ int tarmac_dense_bwd_noalloc(const float* q, const float* k, const float* v, con
  * bf16 MFMA's fp32 accumulation error that is measured, not derived: at most
  * 2^-20.25 of the sum of product magnitudes (worst seen on gfx950: 2^-20.5,
  * one dominant product among small ones; tarmac_mfma_bf16_probe measures
- * it), inside eps = 2^-18 at d <= 32 and 2^-17 at d = 64 together with the
- * canonical chain's d 2^-24.
+ * it), inside eps = 2^-18 at d <= 32, 2^-17 at d = 64 and 2^-16 at d = 128
+ * together with the canonical chain's d 2^-24.
  * mode: 0 = packed always, 1 = automatic (default; the fastest measured on
  * MI355X for the shape), 2 = filter where supported (fp32 d = 16, 32, 64;
  * bf16 d = 16), 3 = lists for fp32 (bf16 runs packed), 4 = packed split where

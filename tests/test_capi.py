@@ -59,6 +59,8 @@ def _fake(addr=256):
     ((1, 1, 16, 1, 0), 1, "N >= 2"),
     ((1, 8, 12, 1, 0), 2, "head dim"),
     ((1, 8, 8, 1, 1), 2, "bf16 head dim"),
+    ((1, 8, 96, 1, 0), 2, "head dim"),
+    ((1, 8, 256, 1, 1), 2, "bf16 head dim"),
     ((1, 8, 16, 1, 7), 1, "dtype"),
     ((1, 8, 16, 0, 0), 1, "topk"),
     ((1, 8, 16, 8, 0), 1, "topk"),

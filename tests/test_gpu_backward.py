@@ -8,8 +8,8 @@ retained sets. Bar: 1e-4 of the largest |ref| gradient entry (normwise).
 
 The fixed-set backward sums each key's dk, dv over the queries that retain
 it in ascending query order (bitwise reproducible), except where a set names
-a peer twice or the row's bitmask does not fit LDS (N above about 1100 at
-d = 16): those rows are summed with fp32 atomics.
+a peer twice, the row's bitmask does not fit LDS (N above about 1100 at
+d = 16) or d = 128: those rows are summed with fp32 atomics.
 """
 
 from __future__ import annotations
@@ -64,7 +64,7 @@ def _dev(*xs):
 @pytest.mark.parametrize("N,d,kk", [(6, 16, 2), (24, 8, 5), (100, 16, 3), (256, 16, 2),
                                     (256, 32, 4), (300, 64, 12), (512, 16, 8), (96, 16, 23),
                                     (384, 16, 95), (384, 32, 95), (300, 8, 30), (1000, 16, 40),
-                                    (1500, 8, 3)])
+                                    (1500, 8, 3), (100, 128, 3), (300, 128, 12)])
 def test_topk_backward(N, d, kk):
     from tarmac.kernels import fixedset_attention_backward, topk_attention
     B = 3
@@ -77,7 +77,7 @@ def test_topk_backward(N, d, kk):
     _close(got, _ref_set(q, k, v, idx.cpu().numpy(), g))
 
 
-@pytest.mark.parametrize("N,d,kk", [(40, 16, 6), (300, 16, 30), (300, 8, 7)])
+@pytest.mark.parametrize("N,d,kk", [(40, 16, 6), (300, 16, 30), (300, 8, 7), (200, 128, 9)])
 @pytest.mark.parametrize("idx_dtype", [torch.int32, torch.int64])
 def test_fixedset_backward_any_sets(idx_dtype, N, d, kk):
     """Arbitrary peer sets, repeated peers and the self pair included (rows
@@ -119,7 +119,7 @@ def test_fixedset_backward_is_reproducible(N, d, kk):
 
 
 @pytest.mark.parametrize("N,d", [(2, 16), (6, 16), (24, 8), (100, 32), (129, 8), (256, 16), (300, 64),
-                                 (700, 16), (1000, 32)])
+                                 (700, 16), (1000, 32), (6, 128), (100, 128), (300, 128)])
 def test_dense_backward(N, d):
     from tarmac.kernels import dense_attention_backward, fused_dense_attention
     B = 2
@@ -136,7 +136,8 @@ HALF_TOL = {torch.bfloat16: 1e-2, torch.float16: 2e-3}
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("N,d,kk", [(6, 16, 2), (256, 16, 2), (300, 64, 12), (384, 32, 95)])
+@pytest.mark.parametrize("N,d,kk", [(6, 16, 2), (256, 16, 2), (300, 64, 12), (384, 32, 95),
+                                    (256, 128, 4)])
 def test_half_backward(dt, N, d, kk):
     """bf16 / float16 heads: gradients (computed in fp32 on exact copies,
     returned in the heads' dtype) against float64 autograd on the same
@@ -170,7 +171,7 @@ def test_backward_rejects_mixed_dtypes():
         dense_attention_backward(q, k, v, q, q.to(torch.bfloat16))
 
 
-@pytest.mark.parametrize("N,d", [(6, 16), (256, 16), (300, 64), (700, 16)])
+@pytest.mark.parametrize("N,d", [(6, 16), (256, 16), (300, 64), (700, 16), (300, 128)])
 def test_dense_forward_stats_and_saved_backward(N, d):
     """tarmac_dense_fwd_stats: the same output as the plain forward, plane 0
     of stats the log2-domain logsumexp of the scaled scores (float64

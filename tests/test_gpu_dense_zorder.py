@@ -40,7 +40,8 @@ def normwise(got, ref):
 
 @pytest.mark.parametrize("N,d", [(2, 16), (6, 16), (6, 8), (17, 16), (64, 32), (100, 16),
                                  (128, 64), (256, 16), (384, 16), (512, 32), (1024, 16),
-                                 (1024, 64), (32, 64), (40, 8), (33, 32), (64, 16), (48, 64)])
+                                 (1024, 64), (32, 64), (40, 8), (33, 32), (64, 16), (48, 64),
+                                 (6, 128), (100, 128), (256, 128), (1024, 128)])
 def test_dense_f32(N, d):
     from tarmac.kernels import fused_dense_attention
     B = max(2, min(16, 4096 // N))
@@ -50,7 +51,8 @@ def test_dense_f32(N, d):
     assert normwise(out, ref) <= F32_TOL
 
 
-@pytest.mark.parametrize("N,d,chunk", [(256, 16, 64), (1000, 16, 128), (512, 64, 64), (64, 16, 32)])
+@pytest.mark.parametrize("N,d,chunk", [(256, 16, 64), (1000, 16, 128), (512, 64, 64), (64, 16, 32),
+                                       (300, 128, 64)])
 def test_dense_streamed_chunks(N, d, chunk):
     from tarmac.kernels import fused_dense_attention
     q, k, v = qkv(N + chunk, 3, N, d)
@@ -58,7 +60,7 @@ def test_dense_streamed_chunks(N, d, chunk):
     assert normwise(out, O.canon_dense(q, k, v)) <= F32_TOL
 
 
-@pytest.mark.parametrize("N,d", [(64, 16), (256, 16), (256, 32), (512, 64), (100, 16)])
+@pytest.mark.parametrize("N,d", [(64, 16), (256, 16), (256, 32), (512, 64), (100, 16), (300, 128)])
 def test_dense_bf16(N, d):
     from tarmac.kernels import fused_dense_attention
     q, k, v = qkv(77 + N + d, 8, N, d)
@@ -84,7 +86,7 @@ def test_dense_headline_shape():
 
 @pytest.mark.parametrize("N,d,kk,itype", [(6, 16, 2, torch.int64), (64, 8, 3, torch.int32),
                                           (512, 16, 2, torch.int64), (200, 64, 7, torch.int32),
-                                          (33, 32, 1, torch.int64)])
+                                          (33, 32, 1, torch.int64), (300, 128, 5, torch.int32)])
 def test_fixedset_f32(N, d, kk, itype):
     from tarmac.kernels import fused_prescore_attention
     B = 6
@@ -94,9 +96,10 @@ def test_fixedset_f32(N, d, kk, itype):
     assert normwise(out, O.canon_fixedset(q, k, v, idx)) <= F32_TOL
 
 
-def test_fixedset_bf16():
+@pytest.mark.parametrize("d", [32, 128])
+def test_fixedset_bf16(d):
     from tarmac.kernels import fused_prescore_attention
-    B, N, d, kk = 4, 128, 32, 4
+    B, N, kk = 4, 128, 4
     q, k, v = qkv(3, B, N, d)
     idx = np.random.default_rng(3).integers(0, N, (B, N, kk))
     out = host(fused_prescore_attention(*dev(q, k, v, dtype=torch.bfloat16),
@@ -163,7 +166,7 @@ def test_morton_window_vs_oracle(B, N, kk, bits):
 
 @pytest.mark.parametrize("B,N,d,kk,bits", [(8, 6, 16, 2, 10), (16, 512, 16, 2, 16),
                                            (4, 512, 32, 4, 16), (4, 100, 8, 3, 10),
-                                           (2, 2048, 64, 1, 16)])
+                                           (2, 2048, 64, 1, 16), (4, 300, 128, 3, 10)])
 def test_zorder_fused_f32(B, N, d, kk, bits):
     from tarmac.kernels import zorder_attention
     q, k, v = qkv(4242 + N, B, N, d)
@@ -178,9 +181,10 @@ def test_zorder_fused_f32(B, N, d, kk, bits):
     assert normwise(out, ref) <= F32_TOL
 
 
-def test_zorder_fused_bf16():
+@pytest.mark.parametrize("d", [16, 128])
+def test_zorder_fused_bf16(d):
     from tarmac.kernels import zorder_attention
-    B, N, d, kk = 4, 512, 16, 2
+    B, N, kk = 4, 512, 2
     q, k, v = qkv(9, B, N, d)
     pos = np.random.default_rng(9).random((B, N, 2)).astype(np.float32)
     out = host(zorder_attention(*dev(q, k, v, dtype=torch.bfloat16),

@@ -11,7 +11,8 @@ kernels do not take directly, on the GPU.
 * ``adaptive_topk`` (:383-414) is random through its Gumbel gate: with the
   gate forced to one bin it must equal top-k attention at that k, and
   ``expected_k`` must carry gradient to the gate.
-* ``msg_dim`` 12, 24, 40 (heads zero-padded to 16, 32, 64): forward against
+* ``msg_dim`` 12, 24, 40, 100 (heads zero-padded to 16, 32, 64, 128) and
+  128: forward against
   float64 with the kernel's own retained sets (1e-5), backward against float64
   autograd (1e-4); the retained sets against the exact top k of the unpadded
   scores off near-ties, fp32 and bf16 heads.
@@ -143,7 +144,7 @@ def test_adaptive_topk_expected_k_reaches_the_gate():
     assert mod.k_gate.weight.grad is not None and mod.k_gate.weight.grad.abs().sum() > 0
 
 
-@pytest.mark.parametrize("msg_dim", [12, 24, 40])
+@pytest.mark.parametrize("msg_dim", [12, 24, 40, 100, 128])
 @pytest.mark.parametrize("mode,k", [("dense", 0), ("topk_gather", 2), ("zorder_k", 2),
                                     ("random_k", 2)])
 def test_any_msg_dim(msg_dim, mode, k):
@@ -159,7 +160,7 @@ def test_any_msg_dim(msg_dim, mode, k):
         out, _ = mod(x, pos if mode == "zorder_k" else None)
         q, kh, v = (t.contiguous() for t in mod.qkv(x).chunk(3, dim=-1))
         qw, kw, vw, _ = _to_width(q, kh, v)
-        assert qw.shape[-1] in (16, 32, 64)
+        assert qw.shape[-1] in (16, 32, 64, 128)
         if mode == "topk_gather":
             peers = topk_attention(qw, kw, vw, k, return_indices=True)[1]
         elif mode == "zorder_k":
@@ -177,7 +178,7 @@ def test_any_msg_dim(msg_dim, mode, k):
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("msg_dim", [12, 24, 40])
+@pytest.mark.parametrize("msg_dim", [12, 24, 40, 100])
 def test_padded_width_selects_on_unpadded_scores(msg_dim, dt):
     """The top-k peers the module takes on padded, pre-scaled heads are the
     exact top k of q.k / sqrt(msg_dim) on the unpadded heads (float64 over
@@ -203,7 +204,7 @@ def test_padded_width_selects_on_unpadded_scores(msg_dim, dt):
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("msg_dim", [12, 16])
+@pytest.mark.parametrize("msg_dim", [12, 16, 128])
 @pytest.mark.parametrize("mode,k", [("dense", 0), ("topk_gather", 2), ("zorder_k", 2)])
 def test_half_precision_module(mode, k, msg_dim, dt):
     """bf16 and float16 modules (the reference's half-precision arms): the
@@ -243,10 +244,12 @@ def test_half_precision_module(mode, k, msg_dim, dt):
         assert grad is not None and torch.isfinite(grad).all() and grad.abs().sum() > 0, name
 
 
-def test_padded_width_backward_matches_float64_autograd():
-    """msg_dim 12 (padded to 16): gradients of the whole module through the
-    dense HIP core and the padding, against float64 autograd."""
-    mod = _module("dense", 0, 10, 12).train()
+@pytest.mark.parametrize("msg_dim", [12, 100])
+def test_padded_width_backward_matches_float64_autograd(msg_dim):
+    """msg_dim 12 and 100 (padded to 16 and 128): gradients of the whole
+    module through the dense HIP core and the padding, against float64
+    autograd."""
+    mod = _module("dense", 0, 10, msg_dim).train()
     mod.collect_info = False
     x = _x(3, 10).requires_grad_(True)
     out, _ = mod(x)
@@ -255,7 +258,7 @@ def test_padded_width_backward_matches_float64_autograd():
     W = {n: p.detach().double().cpu().requires_grad_(True) for n, p in mod.named_parameters()}
     xr = x.detach().double().cpu().requires_grad_(True)
     q, k, v = (xr @ W["qkv.weight"].T + W["qkv.bias"]).chunk(3, dim=-1)
-    s = q @ k.transpose(-1, -2) / 12 ** 0.5
+    s = q @ k.transpose(-1, -2) / msg_dim ** 0.5
     s = s.masked_fill(torch.eye(10, dtype=torch.bool), float("-inf"))
     ref = F.gelu(torch.softmax(s, -1) @ v) @ W["proj.weight"].T + W["proj.bias"]
     (ref * g.double().cpu()).sum().backward()
@@ -266,6 +269,6 @@ def test_padded_width_backward_matches_float64_autograd():
 
 
 def test_wide_messages_are_refused():
-    mod = _module("dense", 0, 6, 96)
-    with pytest.raises(NotImplementedError, match="up to 64"):
+    mod = _module("dense", 0, 6, 160)
+    with pytest.raises(NotImplementedError, match="up to 128"):
         mod(_x(2, 6))

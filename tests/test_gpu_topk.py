@@ -78,7 +78,7 @@ CASES = [
     (6, 16, 2), (6, 16, 1), (6, 8, 5), (2, 16, 1), (17, 16, 3), (32, 16, 1), (32, 16, 4),
     (64, 8, 2), (64, 32, 2), (100, 16, 2), (128, 64, 1), (256, 16, 1), (256, 16, 2),
     (256, 16, 4), (256, 32, 4), (384, 16, 2), (512, 16, 8), (512, 64, 3), (1024, 16, 2),
-    (1024, 16, 7),
+    (1024, 16, 7), (6, 128, 1), (64, 128, 2), (256, 128, 4), (300, 128, 8), (1024, 128, 1),
 ]
 
 
@@ -95,8 +95,34 @@ def test_fused_topk_f32_parity(N, d, kk, mode):
     check_f32(q, k, v, kk, out, idx)
 
 
+@pytest.mark.parametrize("tiles", [1, 2], ids=["one_tile", "two_tiles"])
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("N,chunk", [(256, None), (1100, None), (700, 128)])
+def test_d128_launch_shapes(N, chunk, dtype, tiles):
+    """Head width 128 (msg_dim 65 .. 128 after the module's zero padding)
+    under both query-tile launch shapes (forced: the automatic choice
+    depends on the batch), on resident and streamed rows and rows of more
+    than 1024 keys (several packing segments): indices bit-exact against the
+    canonical oracle for k = 1, 2, 4, 8."""
+    from tarmac import _lib
+    B = 2
+    q, k, v = qkv(13 * N + tiles, B, N, 128)
+    prev = _lib.LIB.tarmac_set_query_tiles(tiles)
+    try:
+        for kk in (1, 2, 4, 8):
+            if dtype == "fp32":
+                out, idx = run_topk(q, k, v, kk, chunk)
+                check_f32(q, k, v, kk, out, idx)
+            else:
+                out, idx = run_topk_bf16(q, k, v, kk, chunk)
+                check_bf16_exact(q, k, v, kk, out, idx)
+    finally:
+        _lib.LIB.tarmac_set_query_tiles(prev)
+
+
 @pytest.mark.parametrize("N,d,kk,chunk", [(256, 16, 2, 16), (256, 16, 4, 64), (300, 32, 1, 128),
-                                          (1024, 16, 2, 256), (2048, 16, 1, 256)])
+                                          (1024, 16, 2, 256), (2048, 16, 1, 256), (300, 128, 2, 64),
+                                          (1024, 128, 4, 128)])
 def test_streaming_topk_matches_fused_bitwise(N, d, kk, chunk):
     B = 4
     q, k, v = qkv(7 * N + kk, B, N, d)
@@ -128,7 +154,7 @@ def test_split32_streamed_matches_resident_bitwise(N, kk, chunk):
 
 
 @pytest.mark.parametrize("N,d,kk", [(12, 16, 11), (24, 8, 23), (64, 16, 9), (200, 32, 40),
-                                    (300, 16, 299)])
+                                    (300, 16, 299), (200, 128, 40), (600, 128, 12)])
 def test_wide_k_parity(N, d, kk):
     q, k, v = qkv(N + 3 * kk, 3, N, d)
     out, idx = run_topk(q, k, v, kk)
@@ -158,7 +184,7 @@ def test_exact_ties_keep_lower_index():
         assert idx[:, 0].tolist() == [list(range(1, kk + 1))] * B
 
 
-@pytest.mark.parametrize("N,d", [(256, 32), (300, 64), (200, 8)])
+@pytest.mark.parametrize("N,d", [(256, 32), (300, 64), (200, 8), (256, 128)])
 def test_exact_ties_fp32_wide_heads(N, d):
     """fp32 at d = 8, 32, 64 (the packed pass on fp32 MFMA scores for k >= 3):
     duplicated keys and zero queries leave the packed proof unsettled, and
@@ -203,7 +229,8 @@ def test_headline_shape_properties():
 
 @pytest.mark.parametrize("N,d,kk", [(64, 16, 1), (256, 16, 2), (256, 32, 4), (512, 64, 2),
                                     (100, 16, 3), (1024, 16, 1), (256, 64, 12), (6, 16, 2),
-                                    (32, 16, 5), (17, 16, 8), (48, 16, 2)])
+                                    (32, 16, 5), (17, 16, 8), (48, 16, 2), (256, 128, 2),
+                                    (512, 128, 8), (64, 128, 12)])
 def test_topk_bf16(N, d, kk):
     from tarmac.kernels import topk_attention
     B = 8
@@ -240,7 +267,7 @@ def check_bf16_exact(q, k, v, kk, out, idx):
     assert np.abs(out - out_c).max() <= BF16_TOL * max(np.abs(out_c).max(), 1e-30)
 
 
-@pytest.mark.parametrize("N,d", [(64, 16), (256, 32), (300, 64), (32, 16), (24, 16)])
+@pytest.mark.parametrize("N,d", [(64, 16), (256, 32), (300, 64), (32, 16), (24, 16), (256, 128)])
 def test_topk_bf16_exact_with_ties(N, d):
     """bf16 with exact ties (duplicated keys, zero and repeated queries): the
     retained set and its order are the canonical oracle's, ties to the lower
@@ -274,7 +301,7 @@ def test_topk_bf16_configs2_exact(N, d, kk):
 @pytest.mark.parametrize("N,d,kk,chunk", [(256, 16, 1, 64), (256, 16, 2, 16), (512, 32, 2, 128),
                                           (1024, 64, 2, 256), (700, 16, 3, 128), (1500, 16, 4, 256),
                                           (64, 16, 2, 16), (32, 16, 4, 16), (64, 32, 2, 32),
-                                          (40, 64, 3, 16)])
+                                          (40, 64, 3, 16), (512, 128, 2, 128), (300, 128, 4, 64)])
 def test_streaming_topk_bf16_matches_fused_bitwise(N, d, kk, chunk):
     """bf16: the streamed kernel (key chunks) returns exactly the resident
     kernel's indices and outputs, on every bf16 selection path."""
@@ -387,7 +414,7 @@ def _variant_inputs(seed, B, N, d, ties):
 
 @pytest.mark.parametrize("N,d,kk,ties", [(6, 16, 2, False), (24, 16, 3, True), (100, 32, 4, False),
                                          (256, 16, 2, True), (256, 64, 8, False), (513, 16, 5, True),
-                                         (1024, 16, 1, True), (1024, 64, 7, True)])
+                                         (1024, 16, 1, True), (1024, 64, 7, True), (300, 128, 4, True)])
 @pytest.mark.parametrize("bisect", [34, 32, 20, 5, 0])
 def test_masked_variant_matches_bisection_oracle(N, d, kk, ties, bisect):
     """fused_topk_attention_masked: the kept set is the reference's bisection
@@ -407,7 +434,7 @@ def test_masked_variant_matches_bisection_oracle(N, d, kk, ties, bisect):
 
 @pytest.mark.parametrize("N,d,kk,ties", [(6, 16, 2, True), (24, 8, 5, True), (100, 32, 4, False),
                                          (256, 16, 2, True), (256, 64, 8, True), (300, 16, 12, True),
-                                         (1024, 16, 3, True), (1024, 32, 8, True)])
+                                         (1024, 16, 3, True), (1024, 32, 8, True), (300, 128, 6, True)])
 def test_sort_variant_keeps_higher_index_on_ties(N, d, kk, ties):
     from tarmac.kernels import fused_topk_attention_sort, topk_variant_attention
     from tarmac import _lib
@@ -431,7 +458,7 @@ def test_sort_variant_keeps_higher_index_on_ties(N, d, kk, ties):
 
 @pytest.mark.parametrize("N,d,kk,ties", [(6, 16, 2, False), (24, 16, 3, True), (256, 16, 2, True),
                                          (256, 64, 8, False), (300, 32, 12, True),
-                                         (1024, 16, 4, True)])
+                                         (1024, 16, 4, True), (256, 128, 3, True)])
 @pytest.mark.parametrize("rule", ["masked34", "masked32", "masked20", "masked5", "sort"])
 def test_bf16_variants_match_oracle(N, d, kk, ties, rule):
     """bf16 heads: the masked and sort rules on the canonical fp32 scores of
@@ -552,7 +579,8 @@ def test_empty_batch_returns_empty_outputs():
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("N,d,kk", [(6, 16, 2), (256, 16, 2), (300, 8, 4), (512, 64, 12), (96, 32, 23)])
+@pytest.mark.parametrize("N,d,kk", [(6, 16, 2), (256, 16, 2), (300, 8, 4), (512, 64, 12), (96, 32, 23),
+                                    (256, 128, 4)])
 def test_float16_inputs(N, d, kk):
     """float16 heads run the fp32 kernels on exact fp32 copies: retained
     indices bit-exact against the canonical C oracle on the float16 values,

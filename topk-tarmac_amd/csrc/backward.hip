@@ -948,31 +948,35 @@ static hipError_t launch_fixedset_bwd_t(const FixedsetBwdArgs& a) {
   using G2 = std::integral_constant<int, 2>;
   using G4 = std::integral_constant<int, 4>;
   const bool pairs = D <= 16 && a.N > 256 && a.N <= 512;
-  if (mask_stage <= kMaskLdsBudget) {  // statistics, bitmask and the row's K, V fit LDS
-    if constexpr (D <= 16)
-      if (pairs) return launch_mask(G2{}, std::true_type{}, mask_stage);
-    return launch_mask(G4{}, std::true_type{}, mask_stage);
-  }
-  if (mask_plain <= kMaskLdsBudget) {  // statistics and bitmask fit LDS
-    if constexpr (D <= 16)
-      if (pairs) return launch_mask(G2{}, std::false_type{}, mask_plain);
-    return launch_mask(G4{}, std::false_type{}, mask_plain);
-  }
-  const size_t gather_lds = fixedset_gather_lds_bytes(a.N, D, a.kk);
-  if (gather_lds <= kBwdLdsBudget) {  // rows and per-entry lists fit LDS
-    hipLaunchKernelGGL((fixedset_bwd_gather_kernel<D, I>), dim3(a.B), dim3(1024), gather_lds, st,
-                       a.q, a.k, a.v, a.dout, idx, a.dq, a.dk, a.dv, a.N, a.kk, a.scale);
-    return hipGetLastError();
-  }
-  if (4 * row_bytes <= kBwdLdsBudget) {  // dK, dV and the staged K, V fit LDS
-    hipLaunchKernelGGL((fixedset_bwd_lds_kernel<D, I, true>), dim3(a.B), dim3(1024), 4 * row_bytes,
-                       st, a.q, a.k, a.v, a.dout, idx, a.dq, a.dk, a.dv, a.N, a.kk, a.scale);
-    return hipGetLastError();
-  }
-  if (2 * row_bytes <= kBwdLdsBudget) {  // the batch row's dK, dV fit LDS
-    hipLaunchKernelGGL((fixedset_bwd_lds_kernel<D, I, false>), dim3(a.B), dim3(1024), 2 * row_bytes,
-                       st, a.q, a.k, a.v, a.dout, idx, a.dq, a.dk, a.dv, a.N, a.kk, a.scale);
-    return hipGetLastError();
+  // d = 128: a lane's share of a row exceeds the 128 VGPRs of a 1024-thread
+  // workgroup, so those rows take the per-query kernel below
+  if constexpr (D <= 64) {
+    if (mask_stage <= kMaskLdsBudget) {  // statistics, bitmask and the row's K, V fit LDS
+      if constexpr (D <= 16)
+        if (pairs) return launch_mask(G2{}, std::true_type{}, mask_stage);
+      return launch_mask(G4{}, std::true_type{}, mask_stage);
+    }
+    if (mask_plain <= kMaskLdsBudget) {  // statistics and bitmask fit LDS
+      if constexpr (D <= 16)
+        if (pairs) return launch_mask(G2{}, std::false_type{}, mask_plain);
+      return launch_mask(G4{}, std::false_type{}, mask_plain);
+    }
+    const size_t gather_lds = fixedset_gather_lds_bytes(a.N, D, a.kk);
+    if (gather_lds <= kBwdLdsBudget) {  // rows and per-entry lists fit LDS
+      hipLaunchKernelGGL((fixedset_bwd_gather_kernel<D, I>), dim3(a.B), dim3(1024), gather_lds, st,
+                         a.q, a.k, a.v, a.dout, idx, a.dq, a.dk, a.dv, a.N, a.kk, a.scale);
+      return hipGetLastError();
+    }
+    if (4 * row_bytes <= kBwdLdsBudget) {  // dK, dV and the staged K, V fit LDS
+      hipLaunchKernelGGL((fixedset_bwd_lds_kernel<D, I, true>), dim3(a.B), dim3(1024), 4 * row_bytes,
+                         st, a.q, a.k, a.v, a.dout, idx, a.dq, a.dk, a.dv, a.N, a.kk, a.scale);
+      return hipGetLastError();
+    }
+    if (2 * row_bytes <= kBwdLdsBudget) {  // the batch row's dK, dV fit LDS
+      hipLaunchKernelGGL((fixedset_bwd_lds_kernel<D, I, false>), dim3(a.B), dim3(1024), 2 * row_bytes,
+                         st, a.q, a.k, a.v, a.dout, idx, a.dq, a.dk, a.dv, a.N, a.kk, a.scale);
+      return hipGetLastError();
+    }
   }
   const long n4 = static_cast<long>(a.B) * a.N * D / 4;
   const int zgrid = static_cast<int>(std::min<long>((n4 + 255) / 256, 4096));
@@ -996,6 +1000,7 @@ hipError_t run_fixedset_bwd(const FixedsetBwdArgs& a) {
     case 16: return launch_fixedset_bwd<16>(a);
     case 32: return launch_fixedset_bwd<32>(a);
     case 64: return launch_fixedset_bwd<64>(a);
+    case 128: return launch_fixedset_bwd<128>(a);
   }
   return hipErrorInvalidValue;
 }
@@ -1011,9 +1016,14 @@ static hipError_t launch_dense_bwd(const DenseBwdArgs& a) {
   const int nblocks = a.B * nblk;
   // largest chunk (multiple of the block) within the LDS budget, capped at N
   const int npad = (a.N + BQ - 1) / BQ * BQ;
+  // d = 128: one 32-row block of the dK/dV pass needs 71 KB, so those rows
+  // take up to 80 KB (two workgroups per CU)
+  constexpr size_t budget = D > 64 ? 80 * 1024 : kBwdLdsBudget;
+  static_assert(dq_lds_bytes<D>(BQ) <= budget && dkv_lds_bytes<D>(BQ) <= budget,
+                "one block of each backward pass fits LDS");
   int kc = BQ, qc = BQ;
-  while (kc + BQ <= npad && dq_lds_bytes<D>(kc + BQ) <= kBwdLdsBudget) kc += BQ;
-  while (qc + BQ <= npad && dkv_lds_bytes<D>(qc + BQ) <= kBwdLdsBudget) qc += BQ;
+  while (kc + BQ <= npad && dq_lds_bytes<D>(kc + BQ) <= budget) kc += BQ;
+  while (qc + BQ <= npad && dkv_lds_bytes<D>(qc + BQ) <= budget) qc += BQ;
   if (kc >= a.N) kc = a.N;
   if (qc >= a.N) qc = a.N;
   hipStream_t st = static_cast<hipStream_t>(a.stream);
@@ -1035,6 +1045,7 @@ hipError_t run_dense_bwd(const DenseBwdArgs& a) {
     case 16: return launch_dense_bwd<16>(a);
     case 32: return launch_dense_bwd<32>(a);
     case 64: return launch_dense_bwd<64>(a);
+    case 128: return launch_dense_bwd<128>(a);
   }
   return hipErrorInvalidValue;
 }

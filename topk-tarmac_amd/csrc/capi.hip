@@ -36,6 +36,10 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 
 constexpr size_t kLdsBudget = 64 * 1024;
 constexpr size_t kBf16TopkLds = 49 * 1024;
+// Head width 128: a 64-key block of fp32 keys and transposed values takes
+// 69 KB, so those rows may use up to 80 KB (two workgroups per CU; gfx950
+// has 160 KB of LDS per CU).
+size_t lds_budget(int d) { return d > 64 ? 80 * 1024 : kLdsBudget; }
 constexpr int kZorderMaxN = 4096;  // agents per row the Morton selector sorts
 constexpr size_t kZorderLds = 160 * 1024;  // LDS per workgroup on gfx950
 
@@ -49,11 +53,13 @@ int check_core(const void* q, const void* k, const void* v, const void* out, int
   if (B < 1 || N < 2)
     return fail(TARMAC_ERR_INVALID, "%s: need B >= 1 and N >= 2 (got B=%d, N=%d)", fn, B, N);
   if (dtype == tarmac::kF32) {
-    if (d != 8 && d != 16 && d != 32 && d != 64)
-      return fail(TARMAC_ERR_UNSUPPORTED, "%s: fp32 head dim must be 8, 16, 32 or 64 (got %d)", fn, d);
+    if (d != 8 && d != 16 && d != 32 && d != 64 && d != 128)
+      return fail(TARMAC_ERR_UNSUPPORTED, "%s: fp32 head dim must be 8, 16, 32, 64 or 128 (got %d)",
+                  fn, d);
   } else if (dtype == tarmac::kBf16) {
-    if (d != 16 && d != 32 && d != 64)
-      return fail(TARMAC_ERR_UNSUPPORTED, "%s: bf16 head dim must be 16, 32 or 64 (got %d)", fn, d);
+    if (d != 16 && d != 32 && d != 64 && d != 128)
+      return fail(TARMAC_ERR_UNSUPPORTED, "%s: bf16 head dim must be 16, 32, 64 or 128 (got %d)",
+                  fn, d);
   } else {
     return fail(TARMAC_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
   }
@@ -65,7 +71,7 @@ int check_core(const void* q, const void* k, const void* v, const void* out, int
 // Largest multiple of 64 keys whose padded LDS copy fits the budget.
 int max_topk_chunk(int dtype, int d) {
   int kc = 64;
-  while (tarmac::topk_lds_bytes(dtype, d, kc + 64) <= kLdsBudget) kc += 64;
+  while (tarmac::topk_lds_bytes(dtype, d, kc + 64) <= lds_budget(d)) kc += 64;
   return kc;
 }
 
@@ -91,7 +97,7 @@ int topk_common(const void* q, const void* k, const void* v, void* out, int32_t*
   } else {
     if (key_chunk % 16 != 0)
       return fail(TARMAC_ERR_INVALID, "%s: key_chunk must be a multiple of 16 (got %d)", fn, key_chunk);
-    if (tarmac::topk_lds_bytes(dtype, d, key_chunk) > kLdsBudget)
+    if (tarmac::topk_lds_bytes(dtype, d, key_chunk) > lds_budget(d))
       return fail(TARMAC_ERR_UNSUPPORTED, "%s: key_chunk %d exceeds the LDS budget (max %d at d=%d)",
                   fn, key_chunk, kmax, d);
     kc = key_chunk;
@@ -120,11 +126,11 @@ int dense_common(const void* q, const void* k, const void* v, void* out, float* 
   int kc = key_chunk;
   if (kc <= 0) {
     kc = (N + 63) / 64 * 64;
-    while (kc > 64 && tarmac::dense_lds_bytes(dtype, d, kc) > kLdsBudget) kc -= 64;
+    while (kc > 64 && tarmac::dense_lds_bytes(dtype, d, kc) > lds_budget(d)) kc -= 64;
   } else if (kc % 16 != 0) {
     return fail(TARMAC_ERR_INVALID, "%s: key_chunk must be a multiple of 16 (got %d)", fn, kc);
   }
-  if (tarmac::dense_lds_bytes(dtype, d, kc) > kLdsBudget)
+  if (tarmac::dense_lds_bytes(dtype, d, kc) > lds_budget(d))
     return fail(TARMAC_ERR_UNSUPPORTED, "%s: key_chunk %d exceeds the LDS budget at d=%d", fn, kc, d);
   tarmac::DenseArgs a{q, k, v, out, B, N, d, dtype, kc, inv_sqrt(d), stream, stats};
   return hip_status(tarmac::run_dense(a), fn);

@@ -402,14 +402,18 @@ static hipError_t launch_dense_reg(const DenseArgs& a) {
 // B=1024 d=16, rocprof average: N = 32 5.7 -> 3.5 us, N = 64 7.1 -> 6.5 us.
 template <int D>
 static bool dense_reg(const DenseArgs& a, hipError_t* e) {
-  if (a.N > (D <= 32 ? 64 : 32) || a.key_chunk < a.N) return false;  // an explicit smaller chunk keeps LDS
-  switch ((a.N + 15) / 16) {
-    case 1: *e = launch_dense_reg<D, 1>(a); return true;
-    case 2: *e = launch_dense_reg<D, 2>(a); return true;
-    case 3: *e = launch_dense_reg<D, 3>(a); return true;
-    case 4: if constexpr (D <= 32) { *e = launch_dense_reg<D, 4>(a); return true; }
+  if constexpr (D > 64) {
+    return false;  // d = 128 rows take the LDS kernel
+  } else {
+    if (a.N > (D <= 32 ? 64 : 32) || a.key_chunk < a.N) return false;  // an explicit smaller chunk keeps LDS
+    switch ((a.N + 15) / 16) {
+      case 1: *e = launch_dense_reg<D, 1>(a); return true;
+      case 2: *e = launch_dense_reg<D, 2>(a); return true;
+      case 3: *e = launch_dense_reg<D, 3>(a); return true;
+      case 4: if constexpr (D <= 32) { *e = launch_dense_reg<D, 4>(a); return true; }
+    }
+    return false;
   }
-  return false;
 }
 
 template <typename T, int D, int QT>
@@ -456,12 +460,14 @@ hipError_t run_dense(const DenseArgs& a) {
       case 16: return launch_dense<float, 16>(a);
       case 32: return launch_dense<float, 32>(a);
       case 64: return launch_dense<float, 64>(a);
+      case 128: return launch_dense<float, 128>(a);
     }
   } else {
     switch (a.d) {
       case 16: return launch_dense<bf16, 16>(a);
       case 32: return launch_dense<bf16, 32>(a);
       case 64: return launch_dense<bf16, 64>(a);
+      case 128: return launch_dense<bf16, 128>(a);
     }
   }
   return hipErrorInvalidValue;

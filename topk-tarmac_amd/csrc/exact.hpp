@@ -96,11 +96,15 @@ struct FragWord<float, D> {  // Frag<float, D>: row g holds g*E + t in word t
 };
 template <int D>
 struct FragWord<bf16, D> {
-  // d = 16, 32: row g holds g*E + e (e < E) as E/2 packed words;
-  // d = 64: word 4h + w of row g holds elements 32h + 8g + 2w, +1
-  static constexpr int word(int kk, int t) { return D == 64 ? 4 * (kk >> 1) + ((t & 7) >> 1) : t >> 1; }
-  static constexpr int row(int kk, int t) { return D == 64 ? 2 * (kk & 1) + (t >> 3) : kk; }
-  static constexpr int half(int, int t) { return t & 1; }
+  // d = 16: row g holds 4g .. 4g+3 as two packed words; d >= 32: word
+  // 4h + w of row g holds elements 32h + 8g + 2w, +1 (element c = kk*(d/4)
+  // + t sits in word 4 (c / 32) + (c % 8) / 2 of row (c % 32) / 8)
+  static constexpr int elem(int kk, int t) { return kk * (D / 4) + t; }
+  static constexpr int word(int kk, int t) {
+    return D == 16 ? t >> 1 : 4 * (elem(kk, t) >> 5) + ((elem(kk, t) & 7) >> 1);
+  }
+  static constexpr int row(int kk, int t) { return D == 16 ? kk : (elem(kk, t) & 31) >> 3; }
+  static constexpr int half(int kk, int t) { return elem(kk, t) & 1; }
 };
 
 template <int D>

@@ -9,7 +9,7 @@
 // contiguous elements of its row. The resulting rounding is the "canonical"
 // score order restated in oracle/tarmac_oracle.c.
 // bf16: v_mfma_f32_16x16x16_bf16 (d = 16) or v_mfma_f32_16x16x32_bf16
-// (d = 32, 64), fp32 accumulation.
+// (d = 32, 64, 128), fp32 accumulation.
 #pragma once
 
 #include "common.hpp"
@@ -96,7 +96,7 @@ struct Frag;
 // ---- fp32 -----------------------------------------------------------------
 template <int D>
 struct Frag<float, D> {
-  static_assert(D % 4 == 0 && D >= 8 && D <= 64, "fp32 head dim must be 8..64, multiple of 4");
+  static_assert(D % 4 == 0 && D >= 8 && D <= 128, "fp32 head dim must be 8..128, multiple of 4");
   static constexpr int E = D / 4;       // elements per lane = MFMAs per tile
   static constexpr int LDK = D + 4;     // padded LDS row stride, in elements
   float q[E];
@@ -165,7 +165,7 @@ struct Frag<bf16, 16> {
 
 template <int D>
 struct FragBf16Wide {
-  static_assert(D == 32 || D == 64, "bf16 wide fragment");
+  static_assert(D == 32 || D == 64 || D == 128, "bf16 wide fragment");
   static constexpr int NI = D / 32;     // 16x16x32 instructions per tile
   static constexpr int LDK = D + 8;
   bf16x8 q[NI];
@@ -214,6 +214,8 @@ template <>
 struct Frag<bf16, 32> : FragBf16Wide<32> {};
 template <>
 struct Frag<bf16, 64> : FragBf16Wide<64> {};
+template <>
+struct Frag<bf16, 128> : FragBf16Wide<128> {};
 
 // 1/sqrt(d) is a power of two (d = 4^m): it can be folded into q exactly.
 template <int D>

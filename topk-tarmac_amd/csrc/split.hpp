@@ -12,14 +12,15 @@ namespace tarmac {
 // products with an fp32 accumulation error that is measured, not derived
 // (at most 2^-20.25 of the sum of their magnitudes, the worst seen 2^-20.5:
 // one dominant product among small ones, on 16x16x32 and 32x32x16 chains of
-// up to 96 products); the canonical fp32 chain adds <= d 2^-24 of it (one
+// up to 128 products); the canonical fp32 chain adds <= d 2^-24 of it (one
 // rounding per step); split scores drop three products of <= 2^-24 each;
-// sum_c |q_c k_c| <= |q| |k_j|. 2^-18 (d <= 32) and 2^-17 (d = 64) cover the
-// sum with a margin of 1.25 or more, including the fp32 rounding of the bound
-// itself.
+// sum_c |q_c k_c| <= |q| |k_j|. 2^-18 (d <= 32), 2^-17 (d = 64) and 2^-16
+// (d = 128) cover the sum with a margin of 1.25 or more, including the fp32
+// rounding of the bound itself.
 template <int D>
 constexpr float packed_eps() {
-  return D <= 32 ? 1.0f / 262144.0f : 1.0f / 131072.0f;
+  static_assert(D <= 128, "the bound covers chains of up to 128 products");
+  return D <= 32 ? 1.0f / 262144.0f : (D <= 64 ? 1.0f / 131072.0f : 1.0f / 65536.0f);
 }
 constexpr float kPackedNormLimit = 1.329228e36f;  // 2^120: |q| max|k| at or above fails the proof
 

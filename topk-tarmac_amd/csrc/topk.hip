@@ -1138,6 +1138,12 @@ static TopkPath choose_path(const TopkArgs& a, int mode) {
 }
 
 hipError_t run_topk(const TopkArgs& a) {
+  if (a.d == 128) {
+    // head width 128: the packed pass for k <= 8 under every filter mode,
+    // the wide kernels for larger k and the other selection rules
+    if (a.select == kSelTopk && a.topk <= kTopkSmallMax) return run_topk_packed_d128(a);
+    return a.dtype == kF32 ? launch_wide<float, 128>(a) : launch_wide<bf16, 128>(a);
+  }
   if (a.select == kSelTopk && a.topk <= kTopkSmallMax) {
     switch (choose_path(a, topk_filter_mode())) {
       case kPathPacked: return run_topk_packed(a, false);

@@ -125,6 +125,7 @@ struct FilterIn<bf16, D> {
 // margin for the fp32 arithmetic of the bound itself.
 template <int D>
 constexpr float filter_eps() {
+  static_assert(D <= 64, "the filter serves d <= 64");
   return D <= 32 ? 1.0f / 262144.0f : 1.0f / 131072.0f;  // 2^-18, 2^-17
 }
 

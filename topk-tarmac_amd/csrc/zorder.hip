@@ -541,12 +541,14 @@ hipError_t run_fixedset(const FixedsetArgs& a) {
       case 16: return launch_fixedset<float, 16>(a);
       case 32: return launch_fixedset<float, 32>(a);
       case 64: return launch_fixedset<float, 64>(a);
+      case 128: return launch_fixedset<float, 128>(a);
     }
   } else {
     switch (a.d) {
       case 16: return launch_fixedset<bf16, 16>(a);
       case 32: return launch_fixedset<bf16, 32>(a);
       case 64: return launch_fixedset<bf16, 64>(a);
+      case 128: return launch_fixedset<bf16, 128>(a);
     }
   }
   return hipErrorInvalidValue;
@@ -614,12 +616,14 @@ hipError_t run_zorder(const ZorderArgs& a) {
       case 16: return launch_zorder<float, 16>(a);
       case 32: return launch_zorder<float, 32>(a);
       case 64: return launch_zorder<float, 64>(a);
+      case 128: return launch_zorder<float, 128>(a);
     }
   } else {
     switch (a.d) {
       case 16: return launch_zorder<bf16, 16>(a);
       case 32: return launch_zorder<bf16, 32>(a);
       case 64: return launch_zorder<bf16, 64>(a);
+      case 128: return launch_zorder<bf16, 128>(a);
     }
   }
   return hipErrorInvalidValue;

@@ -28,10 +28,11 @@ adaptive_topk  the Gumbel-softmax k gate over dense weights
 
 ``entmax`` and ``adaptive_topk`` are training-study arms outside the timed
 core; their dense (B, N, N) formulations run as torch operations on the
-device, as in the reference. Any ``msg_dim`` up to 64 works: heads whose
-width the kernels do not take (fp32: 8, 16, 32, 64; bf16: 16, 32, 64) are
-zero-padded to the next width, with q pre-scaled by sqrt(width / msg_dim) so
-that scores keep the 1/sqrt(msg_dim) scale; that padding and scaling happen
+device, as in the reference. Any ``msg_dim`` up to 128 works: heads whose
+width the kernels do not take (fp32: 8, 16, 32, 64, 128; bf16: 16, 32, 64,
+128) are zero-padded to the next width, with q pre-scaled by
+sqrt(width / msg_dim) so that scores keep the 1/sqrt(msg_dim) scale; that
+padding and scaling happen
 in fp32 (bf16 heads are widened first, exactly), so the only perturbation of
 the scores is fp32 rounding. float16 heads run the fp32 kernels on exact
 fp32 copies. Messages return in the heads' dtype.
@@ -69,8 +70,8 @@ HIP_MODES = ("dense", "dense_sdpa", "topk", "topk_gather", "zorder_k", "random_k
 TORCH_MODES = ("entmax", "adaptive_topk")
 
 #: Head widths the HIP kernels take, per dtype.
-_WIDTHS = {torch.float32: (8, 16, 32, 64), torch.bfloat16: (16, 32, 64),
-           torch.float16: (8, 16, 32, 64)}
+_WIDTHS = {torch.float32: (8, 16, 32, 64, 128), torch.bfloat16: (16, 32, 64, 128),
+           torch.float16: (8, 16, 32, 64, 128)}
 
 
 @dataclass
@@ -141,7 +142,7 @@ def _kernel_width(d: int, dtype: torch.dtype) -> int:
         if w >= d:
             return w
     raise NotImplementedError(
-        f"msg_dim={d} ({dtype}): the HIP attention core takes head widths up to 64")
+        f"msg_dim={d} ({dtype}): the HIP attention core takes head widths up to 128")
 
 
 def _to_width(q, k, v):
