@@ -49,7 +49,7 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(jobs: int = 4, verbose: bool = True) -> Path:
+def build(jobs: int = min(8, os.cpu_count() or 1), verbose: bool = True) -> Path:
     OBJ.mkdir(exist_ok=True)
     srcs = sorted(CSRC.glob("*.hip"))
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
@@ -65,5 +65,5 @@ def build(jobs: int = 4, verbose: bool = True) -> Path:
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
-    ap.add_argument("--jobs", type=int, default=4)
+    ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
     build(ap.parse_args().jobs)
