@@ -150,12 +150,20 @@ __device__ __forceinline__ T row16_reduce_stride4(T x, Op op) {
   return op(x, dpp_mov<dpp_row_ror(4)>(x));
 }
 
-// max of two non-NaN floats: one v_max_f32, without the canonicalising copies
-// fmaxf adds for operands the compiler cannot prove canonical (lane moves)
-__device__ __forceinline__ float max_plain(float a, float b) {
+// +inf in an SGPR, from an instruction the compiler cannot fold (a scalar
+// copy: VALU work stays visible to the compiler, which inserts the wait
+// states that DPP, lane swaps and MFMA results need after it).
+__device__ __forceinline__ float opaque_inf() {
   float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  asm("s_mov_b32 %0, 0x7f800000" : "=s"(r));
   return r;
+}
+
+// max of two non-NaN floats as one v_med3_f32 against an opaque +inf,
+// without the canonicalising copies fmaxf adds for operands the compiler
+// cannot prove canonical (lane moves, MFMA results).
+__device__ __forceinline__ float max_plain(float a, float b) {
+  return __builtin_amdgcn_fmed3f(a, b, opaque_inf());
 }
 
 // (a, ia) ranks before (b, ib): higher score first, lower index on ties.

@@ -12,13 +12,6 @@ namespace tarmac {
 
 constexpr int kIdxSentinel = 0x3fffffff;
 
-// +inf in an SGPR, from an instruction the compiler cannot fold.
-__device__ __forceinline__ float opaque_inf() {
-  float r;
-  asm("s_mov_b32 %0, 0x7f800000" : "=s"(r));
-  return r;
-}
-
 // max(a, b) as one v_med3_f32. The compiler's maxnum (fmaxf, or fmed3
 // against a literal +inf, which it folds to maxnum) first canonicalises every
 // operand it cannot prove canonical: one extra instruction per score here.
@@ -136,6 +129,22 @@ __device__ __forceinline__ float pack8(float s, uint32_t u) {
 // v_and_or_b32 (with m in a VGPR and f in an SGPR).
 __device__ __forceinline__ float pack_field(float s, uint32_t f, uint32_t m) {
   return __uint_as_float((__float_as_uint(s) & ~m) | f);
+}
+
+// A wave-uniform value in an SGPR the compiler cannot fold into the
+// instructions that read it (a scalar copy).
+__device__ __forceinline__ uint32_t opaque_sgpr(uint32_t x) {
+  uint32_t r;
+  asm("s_mov_b32 %0, %1" : "=s"(r) : "s"(x));
+  return r;
+}
+
+// The same with the complement of the mask in a VGPR (notm = ~m) and a
+// wave-uniform field f: one v_and_or_b32 reading f from an SGPR. With f
+// visible the compiler forms it on the VALU instead (an and, then an or3
+// with the element's offset: two operations per score).
+__device__ __forceinline__ float pack_field_u(float s, uint32_t f, uint32_t notm) {
+  return __uint_as_float((__float_as_uint(s) & notm) | opaque_sgpr(f));
 }
 
 // Value-only insertion into a descending list: L max/med3 operations.

@@ -65,14 +65,14 @@ constexpr int seg_keys() {
   return 1 << FB;
 }
 
-// The field mask as a VGPR value the compiler cannot fold: the packing
-// instruction then takes the mask from a VGPR and the (wave-uniform) field
-// from an SGPR, within the one scalar operand a VOP3 instruction may read;
-// with a literal mask the field would need a v_mov per score.
+// The field mask's complement as a VGPR value the compiler cannot fold: the
+// packing instruction (pack_field_u) then takes it from a VGPR and the
+// (wave-uniform) field from an SGPR, within the one scalar operand a VOP3
+// instruction may read.
 template <int FB>
-__device__ __forceinline__ uint32_t field_mask_vgpr() {
+__device__ __forceinline__ uint32_t field_nmask_vgpr() {
   uint32_t m;
-  asm volatile("v_mov_b32 %0, %1" : "=v"(m) : "i"((1u << FB) - 1u));
+  asm volatile("v_mov_b32 %0, %1" : "=v"(m) : "i"(~((1u << FB) - 1u)));
   return m;
 }
 
@@ -237,9 +237,9 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
     }
   float kmax2 = 0.f;
   int segbase = 0;  // first key of the current segment (uniform)
-  uint32_t fmask;  // in a VGPR (see field_mask_vgpr)
-  if constexpr (ONESEG) asm volatile("v_mov_b32 %0, %1" : "=v"(fmask) : "s"(fm_arg));
-  else fmask = field_mask_vgpr<FB>();
+  uint32_t nfmask;  // the field mask's complement in a VGPR (pack_field_u)
+  if constexpr (ONESEG) asm volatile("v_mov_b32 %0, %1" : "=v"(nfmask) : "s"(~fm_arg));
+  else nfmask = field_nmask_vgpr<FB>();
 
   for (int c0 = 0; c0 < N; c0 += kc) {
     const int cn = min(kc, N - c0);
@@ -288,7 +288,7 @@ topk_packed_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* _
           for (int t = 0; t < BT; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-              s[qt][t][r] = pack_field(s[qt][t][r], f0 + 16u * t + 4u * r, fmask);
+              s[qt][t][r] = pack_field_u(s[qt][t][r], f0 + 16u * t + 4u * r, nfmask);
         mask_block<QT, BT>(s, self_r, q0, kabs, kend, grp, kMasked);
 #pragma unroll
         for (int t = 0; t < BT; ++t)

@@ -146,8 +146,8 @@ topk_split32_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
 #pragma unroll
   for (int m = 0; m < L; ++m) pv[m] = kMasked;
   float kmax2 = 0.f;
-  uint32_t fmask;  // the field mask in a VGPR, the field from an SGPR (one v_and_or_b32)
-  asm volatile("v_mov_b32 %0, %1" : "=v"(fmask) : "s"(fm_arg));
+  uint32_t nfmask;  // the field mask's complement in a VGPR (pack_field_u)
+  asm volatile("v_mov_b32 %0, %1" : "=v"(nfmask) : "s"(~fm_arg));
 
   // one key chunk: stage it (split rows and the chunk's max |k|^2), then scan
   // it. The first chunk is peeled so the query's split can wait on the
@@ -185,8 +185,8 @@ topk_split32_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
         for (int t = 0; t < BT; ++t)
 #pragma unroll
           for (int i = 0; i < 16; ++i)
-            s[t][i] = pack_field(s[t][i],
-                                 static_cast<uint32_t>(kabs + 32 * t + 8 * (i >> 2) + (i & 3)), fmask);
+            s[t][i] = pack_field_u(
+                s[t][i], static_cast<uint32_t>(kabs + 32 * t + 8 * (i >> 2) + (i & 3)), nfmask);
         // the self pair (in the tiles that overlap the wave's queries: one
         // when the chunk starts at a multiple of 32 keys, two otherwise) and
         // keys past the chunk end
