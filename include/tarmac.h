@@ -229,8 +229,10 @@ int tarmac_dense_bwd_noalloc(const float* q, const float* k, const float* v, con
  *   packed split -- the packed pass on split-bf16 scores (fp32 inputs,
  *                   d = 16: x = hi + mid + lo, six bf16 products per score),
  *                   proven against the split error bound;
- *   split32      -- the same on 32-key x 32-query tiles (fp32, d = 16,
- *                   k <= 4, N <= 1024): two lanes per query instead of four;
+ *   split32      -- the same on 32-key x 32-query tiles (d = 16, k <= 4,
+ *                   N <= 256): two lanes per query instead of four; bf16
+ *                   inputs take one bf16 product per tile (the inputs as
+ *                   they are) instead of six split products;
  *   filter       -- all pairs scored on split-bf16 MFMA (fp32 inputs) or
  *                   bf16 MFMA (bf16, d = 16), k+1 candidates rescored in the
  *                   canonical fp32 order and proven against the bf16 bound;
@@ -250,7 +252,8 @@ int tarmac_dense_bwd_noalloc(const float* q, const float* k, const float* v, con
  * MI355X for the shape), 2 = filter where supported (fp32 d = 16, 32, 64;
  * bf16 d = 16), 3 = lists for fp32 (bf16 runs packed), 4 = packed split where
  * supported (fp32 d = 16; packed elsewhere), 5 = split32 where supported
- * (packed split, then packed, elsewhere). bf16 retained sets are always
+ * (fp32 and bf16, d = 16, k <= 4, N <= 256; packed split, then packed,
+ * elsewhere). bf16 retained sets are always
  * the exact top k of the canonical fp32 scores of the inputs converted to
  * fp32. Process-wide (an atomic setting: concurrent calls stay safe and get
  * identical results). Returns the previous mode, or -1 (and sets the last

@@ -124,13 +124,16 @@ def test_topk_exact_on_one_dominant_coordinate(d, dtype, mode):
     ranking is decided by the small ones: the accumulation pattern with the
     largest MFMA error. Retained indices bit-exact against the canonical
     oracle (bf16: on the bf16 inputs; fp32 d = 16 runs the split-bf16 pass
-    on 16 x 16 tiles (mode 4) and on 32 x 32 tiles (mode 5))."""
+    on 16 x 16 tiles (mode 4) and on 32 x 32 tiles (mode 5), bf16 d = 16
+    the 32 x 32 kernel's single-product form (mode 5))."""
     from tarmac import _lib
     from tarmac.kernels import topk_attention
     if dtype == "fp32" and d != 16:
         pytest.skip("split-bf16 scoring serves fp32 at d = 16")
-    if mode != 1 and not (dtype == "fp32" and d == 16):
-        pytest.skip("modes 4 and 5 select split-bf16 kernels (fp32, d = 16)")
+    if mode == 4 and not (dtype == "fp32" and d == 16):
+        pytest.skip("mode 4 selects the split-bf16 16 x 16 kernel (fp32, d = 16)")
+    if mode == 5 and d != 16:
+        pytest.skip("mode 5 selects the 32 x 32 kernel (d = 16)")
     B, N = 8, 256
     g = np.random.default_rng(d)
     q = g.standard_normal((B, N, d)).astype(np.float32) / 8

@@ -313,6 +313,45 @@ def test_streaming_topk_bf16_matches_fused_bitwise(N, d, kk, chunk):
     assert np.array_equal(out_s, out_f)
 
 
+@pytest.mark.parametrize("N,kk,chunk", [(6, 2, None), (33, 4, None), (128, 1, None), (200, 3, None),
+                                        (256, 2, None), (256, 4, None), (256, 2, 80), (256, 4, 16),
+                                        (130, 3, 64), (256, 1, 128)])
+def test_bf16_split32_exact(N, kk, chunk):
+    """bf16 heads at d = 16 on the 32 x 32 kernel (mode 5: one bf16 MFMA per
+    tile, the bf16 accumulation bound in the proof): indices bit-exact against
+    the canonical oracle on the bf16 inputs, resident and streamed (a
+    streamed row equals the resident one bitwise), outputs within 1e-2."""
+    B = 4
+    q, k, v = qkv(71 * N + kk + (chunk or 0), B, N, 16)
+    prev = _set_filter(5)
+    try:
+        out, idx = run_topk_bf16(q, k, v, kk, chunk)
+        out_r, idx_r = run_topk_bf16(q, k, v, kk)
+    finally:
+        _set_filter(prev)
+    check_bf16_exact(q, k, v, kk, out, idx)
+    assert np.array_equal(idx, idx_r) and np.array_equal(out, out_r)
+
+
+@pytest.mark.parametrize("N", [64, 256])
+def test_bf16_split32_exact_with_ties(N):
+    """The 32 x 32 bf16 kernel on exact ties (duplicated keys, zero and
+    repeated queries): the canonical order, ties to the lower index."""
+    B = 4
+    q, k, v = (O.bf16_round(x) for x in qkv(900 + N, B, N, 16))
+    k[:, 1::2] = k[:, 0::2]
+    q[:, :5] = 0.0
+    q[:, 5:10] = q[:, 5:6]
+    prev = _set_filter(5)
+    try:
+        for kk in (1, 2, 3, 4):
+            out, idx = run_topk_bf16(q, k, v, kk)
+            check_bf16_exact(q, k, v, kk, out, idx)
+            assert idx[:, 0].tolist() == [list(range(1, kk + 1))] * B
+    finally:
+        _set_filter(prev)
+
+
 @pytest.mark.parametrize("N,kk,chunk", [(256, 4, None), (256, 8, None), (512, 5, None),
                                         (1024, 4, None), (700, 6, 128), (1500, 4, 256)])
 def test_topk_bf16_filter_exact(N, kk, chunk):

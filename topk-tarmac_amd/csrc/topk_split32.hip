@@ -48,6 +48,7 @@ namespace {
 constexpr int kS32Waves = 4;     // waves per workgroup (128 queries)
 constexpr int kS32Tiles = 2;     // 32-key tiles per scan block (64 keys = kBlockKeys)
 constexpr int kS32LDK = SplitFrag<16>::LDK;  // split row: lo[16] hi[16] mid[16] pad[8]
+constexpr int kB32LDK = 16 + 8;              // bf16 row: x[16] pad[8]
 
 // Split key fragment of one 32-key tile: row kb + l % 32, elements
 // 8 (l / 32) .. +7 of each part.
@@ -79,10 +80,11 @@ __device__ __forceinline__ f32x16 split32_score(const KSplit32& k, bf16x8 qh, bf
 
 // Canonical fp32 score (split.hpp / exact.hpp order: element kk*4 + t at step
 // t, slot kk) of the query row qs (scaled by the power-of-two 1/4 already)
-// against key row krow.
-__device__ __forceinline__ float canon16(const float (&qs)[16], const float* krow) {
+// against key row krow (fp32, or bf16 widened exactly).
+template <typename T>
+__device__ __forceinline__ float canon16(const float (&qs)[16], const T* krow) {
   float k[16];
-  ld_f32<16>(k, krow);
+  ld_row<T, 16>(k, krow);
   float acc = 0.f;
 #pragma unroll
   for (int t = 0; t < 4; ++t)
@@ -95,12 +97,17 @@ __device__ __forceinline__ float canon16(const float (&qs)[16], const float* kro
 
 // One wave: 32 queries q0 .. q0 + 31 of batch row b; the workgroup's waves
 // share one staged copy of the key row. kc: keys per LDS chunk (kc >= N:
-// resident row). fm: the field mask of the row (2^fb - 1).
-template <int K>
+// resident row). fm: the field mask of the row (2^fb - 1). T = float: the
+// split-bf16 scores above; T = bf16: the inputs are bf16 already, so a score
+// is one 32x32x16 product of the rows as they are (exact products, fp32
+// accumulation) and the same packing, proof (the bf16 accumulation bound)
+// and canonical rescoring of the inputs widened to fp32 follow.
+template <int K, typename T>
 __global__ void __launch_bounds__(64 * kS32Waves)
-topk_split32_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
-                    const float* __restrict__ V, float* __restrict__ O, int32_t* __restrict__ Idx,
+topk_split32_kernel(const T* __restrict__ Q, const T* __restrict__ Kx,
+                    const T* __restrict__ V, T* __restrict__ O, int32_t* __restrict__ Idx,
                     int N, int n_qblk, int kc, float scale, int nblocks, uint32_t fm_arg) {
+  constexpr bool BF = sizeof(T) == 2;
   constexpr int D = 16;
   constexpr int C = K + 1;   // candidates rescored
   constexpr int L = K + 2;   // lane and merged lists: the candidates and the (K+2)-th
@@ -117,24 +124,33 @@ topk_split32_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   const int qc = lane & 31, half = lane >> 5;
   const int qi = q0 + qc;
   const size_t boff = static_cast<size_t>(b) * N * D;
-  const float* Qb = Q + boff;
-  const float* Kb = Kx + boff;
+  const T* Qb = Q + boff;
+  const T* Kb = Kx + boff;
   const uint32_t FM = fm_arg;
 
   // query fragment: elements 8 half .. +7 of row qi, read now and split after
   // the first chunk's keys are staged (their loads overlap)
   float qx[8];
-  ld_f32<8>(qx, Qb + static_cast<size_t>(min(qi, N - 1)) * D + 8 * half);
+  ld_row<T, 8>(qx, Qb + static_cast<size_t>(min(qi, N - 1)) * D + 8 * half);
   bf16x8 qh, qm, ql;
   float qn2 = 0.f;
   auto split_query = [&]() {
     const float(&x)[8] = qx;
-    uint32_t h4[4], m4[4], l4[4];
+    if constexpr (BF) {
+      // bf16 values widened exactly: the fragment is the row as it is
+      uint32_t h4[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) split3_pair(x[2 * e], x[2 * e + 1], h4[e], m4[e], l4[e]);
-    qh = __builtin_bit_cast(bf16x8, h4);
-    qm = __builtin_bit_cast(bf16x8, m4);
-    ql = __builtin_bit_cast(bf16x8, l4);
+      for (int e = 0; e < 4; ++e)
+        h4[e] = (__float_as_uint(x[2 * e]) >> 16) | (__float_as_uint(x[2 * e + 1]) & 0xffff0000u);
+      qh = __builtin_bit_cast(bf16x8, h4);
+    } else {
+      uint32_t h4[4], m4[4], l4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) split3_pair(x[2 * e], x[2 * e + 1], h4[e], m4[e], l4[e]);
+      qh = __builtin_bit_cast(bf16x8, h4);
+      qm = __builtin_bit_cast(bf16x8, m4);
+      ql = __builtin_bit_cast(bf16x8, l4);
+    }
     float n2 = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) n2 = fmaf(x[e], x[e], n2);
@@ -157,8 +173,13 @@ topk_split32_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
     const int cnb = (cn + kBlockKeys - 1) / kBlockKeys * kBlockKeys;
     __syncthreads();
     if (threadIdx.x == 0) *kmax_slot = 0u;
-    bool exact_split = true;  // unused: rescoring reads the global rows
-    const float mine = stage_split<D>(Ks, Kb + static_cast<size_t>(c0) * D, cn, cnb, exact_split);
+    float mine;
+    if constexpr (BF) {
+      mine = stage_bf16_norm<D, kB32LDK>(Ks, Kb + static_cast<size_t>(c0) * D, cn, cnb);
+    } else {
+      bool exact_split = true;  // unused: rescoring reads the global rows
+      mine = stage_split<D>(Ks, Kb + static_cast<size_t>(c0) * D, cn, cnb, exact_split);
+    }
     const float wmax = wave_max_rows(mine);
     if constexpr (decltype(first)::value) {
       // tie the query's split to the staged keys, so the compiler cannot
@@ -176,8 +197,14 @@ topk_split32_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
         f32x16 s[BT];
 #pragma unroll
         for (int t = 0; t < BT; ++t) {
-          const KSplit32 kf = load_ksplit32(Ks, kb0 + 32 * t + qc, half);
-          s[t] = split32_score(kf, qh, qm, ql);
+          if constexpr (BF) {
+            const bf16x8 kf =
+                *reinterpret_cast<const bf16x8*>(Ks + (kb0 + 32 * t + qc) * kB32LDK + 8 * half);
+            s[t] = mfma_bf16_32x32x16(kf, qh, f32x16{});
+          } else {
+            const KSplit32 kf = load_ksplit32(Ks, kb0 + 32 * t + qc, half);
+            s[t] = split32_score(kf, qh, qm, ql);
+          }
         }
         // element i of tile t: key kabs + 32 t + 8 (i / 4) + 4 half + i % 4;
         // the field leaves bit 2 (half) for the merge
@@ -247,17 +274,17 @@ topk_split32_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   // Lane half h rescores candidates h, h + 2, ...; a row swap shares them.
   // The value rows (this lane's 8 channels) of every candidate are read with
   // the query and key rows, so the aggregation waits on no further trip.
-  const float* Vb = V + boff + 8 * half;
+  const T* Vb = V + boff + 8 * half;
   float vpre[C][8];
 #pragma unroll
   for (int m = 0; m < C; ++m)
-    ld_f32<8>(vpre[m], Vb + static_cast<size_t>(min(max(cand[m], 0), N - 1)) * D);
+    ld_row<T, 8>(vpre[m], Vb + static_cast<size_t>(min(max(cand[m], 0), N - 1)) * D);
   float val[K];
   int ix[K];
   bool ok;
   {
     float qs[16];
-    ld_f32<16>(qs, Qb + static_cast<size_t>(min(qi, N - 1)) * D);
+    ld_row<T, 16>(qs, Qb + static_cast<size_t>(min(qi, N - 1)) * D);
 #pragma unroll
     for (int e = 0; e < 16; ++e) qs[e] *= scale;  // 1/4: exact
     float cv[C];
@@ -278,7 +305,7 @@ topk_split32_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
     for (int m = 0; m < C; ++m) ci[m] = cand[m];
     sort_lex<C>(cv, ci);
     // every key outside the candidates scores at most the (K+2)-th entry's
-    // ceiling plus the split error
+    // ceiling plus the split (or bf16 accumulation) error
     const float nprod = proof_norm(qn2, kmax2);
     const float bound = (trunc_ceiling(pl[K + 1], FM) + packed_eps<D>() * nprod) * scale;
     ok = qi >= N || (nprod < kPackedNormLimit && bound < cv[K - 1]);
@@ -298,7 +325,7 @@ topk_split32_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
       float ev[K];
       int ei[K];
       const int qx = q0 + c;
-      exact_query_topk_lanes<float, D, K, 1>(
+      exact_query_topk_lanes<T, D, K, 1>(
           Qb + static_cast<size_t>(qx) * D,
           [&](int j) { return Kb + static_cast<size_t>(j) * D; }, N, qx, scale, lane, ev, ei);
       if (qc == c) {
@@ -332,14 +359,14 @@ topk_split32_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
       for (int e = 0; e < 8; ++e) vr[e] = hit ? vpre[c][e] : vr[e];
       found = found || hit;
     }
-    if (!found) ld_f32<8>(vr, Vb + static_cast<size_t>(min(max(ix[m], 0), N - 1)) * D);
+    if (!found) ld_row<T, 8>(vr, Vb + static_cast<size_t>(min(max(ix[m], 0), N - 1)) * D);
 #pragma unroll
     for (int c = 0; c < 8; ++c) acc[c] = fmaf(w, vr[c], acc[c]);
   }
   const float inv = 1.f / den;
 #pragma unroll
   for (int c = 0; c < 8; ++c) acc[c] *= inv;
-  st_row<float, 8>(O + boff + static_cast<size_t>(qi) * D + 8 * half, acc);
+  st_row<T, 8>(O + boff + static_cast<size_t>(qi) * D + 8 * half, acc);
   if (Idx != nullptr && half == 0) {
     int32_t* dst = Idx + (static_cast<size_t>(b) * N + qi) * K;
 #pragma unroll
@@ -351,25 +378,32 @@ topk_split32_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
 // launcher
 // ---------------------------------------------------------------------------
 
-size_t split32_lds_bytes(int kc) {
+size_t split32_lds_bytes(int dtype, int kc) {
   const int kcb = (kc + kBlockKeys - 1) / kBlockKeys * kBlockKeys;
-  return 16 + static_cast<size_t>(kcb) * kS32LDK * 2;
+  return 16 + static_cast<size_t>(kcb) * (dtype == kBf16 ? kB32LDK : kS32LDK) * 2;
 }
 
 // Rows of up to 256 keys: a longer row's split copy (112 bytes a key) would
 // leave a CU fewer than four four-wave workgroups (N = 512: two), where the
 // 16 x 16 kernel's eight-wave workgroups keep sixteen waves per CU.
 bool split32_supported(const TopkArgs& a) {
-  return a.dtype == kF32 && a.d == 16 && a.topk <= 4 && a.N <= 256 && a.select == kSelTopk;
+  return (a.dtype == kF32 || a.dtype == kBf16) && a.d == 16 && a.topk <= 4 && a.N <= 256 &&
+         a.select == kSelTopk;
+}
+
+template <int K, typename T>
+static void launch_split32_t(const TopkArgs& a, int nblocks, int n_qblk, uint32_t fm) {
+  hipLaunchKernelGGL((topk_split32_kernel<K, T>), dim3(nblocks), dim3(64 * kS32Waves),
+                     split32_lds_bytes(a.dtype, a.key_chunk), static_cast<hipStream_t>(a.stream),
+                     static_cast<const T*>(a.q), static_cast<const T*>(a.k),
+                     static_cast<const T*>(a.v), static_cast<T*>(a.out), a.idx, a.N, n_qblk,
+                     a.key_chunk, a.scale, nblocks, fm);
 }
 
 template <int K>
 static void launch_split32_k(const TopkArgs& a, int nblocks, int n_qblk, uint32_t fm) {
-  hipLaunchKernelGGL(topk_split32_kernel<K>, dim3(nblocks), dim3(64 * kS32Waves),
-                     split32_lds_bytes(a.key_chunk), static_cast<hipStream_t>(a.stream),
-                     static_cast<const float*>(a.q), static_cast<const float*>(a.k),
-                     static_cast<const float*>(a.v), static_cast<float*>(a.out), a.idx, a.N,
-                     n_qblk, a.key_chunk, a.scale, nblocks, fm);
+  if (a.dtype == kBf16) launch_split32_t<K, bf16>(a, nblocks, n_qblk, fm);
+  else launch_split32_t<K, float>(a, nblocks, n_qblk, fm);
 }
 
 hipError_t run_topk_split32(const TopkArgs& a) {
