@@ -56,7 +56,7 @@ VALUE_K = 2
 # The kernel the value call dispatches to at this shape (fp32, d=16, k=2,
 # N=256: packed selection on split-bf16 scores from 32 x 32 MFMA tiles). Its
 # launch is what rocprofv3 reports under this name.
-VALUE_KERNEL = "tarmac::topk_split32_kernel<2>"
+VALUE_KERNEL = "tarmac::topk_split32_kernel<2, float>"
 METRIC_FALLBACK = "µs/call attention core, top-k vs dense ratio, N=256 d=16 k=1,2,4; %HBM peak"
 
 
