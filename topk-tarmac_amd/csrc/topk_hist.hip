@@ -1,7 +1,9 @@
-// Exact top-k attention for large k (fp32, d = 16, N <= 512): every score of
-// a query stays in registers, a histogram of them locates the k-th largest,
-// and the kept keys' softmax weights drive the MFMA aggregation of the dense
-// kernel (every other key weighs 0).
+// Exact top-k attention for large k (fp32 and bf16 inputs; d = 16 and 32
+// with N <= 512, d = 64 with N <= 256): every score of a query stays in
+// registers, a histogram of them locates the k-th largest, and the kept
+// keys' softmax weights drive the MFMA aggregation of the dense kernel (every
+// other key weighs 0). bf16 rows are widened to fp32 as they are staged, so
+// the scores are the canonical fp32 scores of the widened inputs.
 //
 // Reference behaviour: the top-k core (src/agents/mappo.py:192-231 topk_gather,
 // src/kernels/fused_topk_attention.py:296-355) at the module's k = 0.25 (N - 1)
@@ -119,16 +121,24 @@ __device__ __forceinline__ float rows_min(float x) {
   return fminf(__uint_as_float(q.a), __uint_as_float(q.b));
 }
 
-// Canonical fp32 score (the order of canon_pair<float, 16, true>) from the
-// query row pre-multiplied by the power-of-two scale, held in registers.
-__device__ __forceinline__ float canon_row16(const float (&qs)[16], const float* krow) {
-  float k[16];
-  ld_f32<16>(k, krow);
+// The canonical fp32 chain (element kk*(D/4) + t at step t, slot kk) of the
+// query row held in registers (pre-multiplied by a power-of-two scale, or
+// not: the caller then scales the result) against key row krow, read in
+// chunks of 16 elements.
+template <typename T, int D>
+__device__ __forceinline__ float canon_row(const float (&qs)[D], const T* krow) {
+  constexpr int QD = D / 4, TS = QD < 4 ? QD : 4;
   float acc = 0.f;
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int t0 = 0; t0 < QD; t0 += TS) {
+    float k[4][TS];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) acc = fmaf(qs[kk * 4 + t], k[kk * 4 + t], acc);
+    for (int kk = 0; kk < 4; ++kk) ld_row<T, TS>(k[kk], krow + kk * QD + t0);
+#pragma unroll
+    for (int t = 0; t < TS; ++t)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) acc = fmaf(qs[kk * QD + t0 + t], k[kk][t], acc);
+  }
   return acc;
 }
 
@@ -137,16 +147,58 @@ constexpr size_t hist_scratch_bytes() {
   return static_cast<size_t>(kHistWaves) * 16 * kHistQWords * 4 + kHistWaves * 32 * 4;
 }
 
-template <int NT>
+template <int NT, int D>
 constexpr size_t hist_region_a_bytes() {
-  const size_t ks = static_cast<size_t>(16 * NT) * Frag<float, 16>::LDK * sizeof(float);
+  const size_t ks = static_cast<size_t>(16 * NT) * Frag<float, D>::LDK * sizeof(float);
   const size_t sc = hist_scratch_bytes<NT>();
   return ks > sc ? ks : sc;
 }
 
-template <int NT>
+// The key rows (fp32, then the waves' scratch) and the transposed value rows
+// (fp32, D channels).
+template <int NT, int D>
 constexpr size_t hist_lds_bytes() {
-  return 16 + hist_region_a_bytes<NT>() + static_cast<size_t>(16) * (16 * NT + 4) * sizeof(float);
+  return 16 + hist_region_a_bytes<NT, D>() + static_cast<size_t>(D) * (16 * NT + 4) * sizeof(float);
+}
+
+// Stage `rows` bf16 rows of D elements as fp32 into LDS (row stride LDK
+// floats), zero rows up to rows_pad: every score of the kernel then comes
+// from the fp32 MFMA chain on the exactly widened inputs, the canonical
+// score of bf16 inputs.
+template <int D, int LDK>
+__device__ __forceinline__ void stage_rows_widen(float* lds, const bf16* src, int rows, int rows_pad) {
+  constexpr int VPR = D / 8;  // 16-byte source vectors per row
+  const int total = rows_pad * VPR, avail = rows * VPR;
+  for (int v = threadIdx.x; v < total; v += blockDim.x) {
+    const int row = v / VPR, cv = v - row * VPR;
+    uint4 x = make_uint4(0u, 0u, 0u, 0u);
+    if (v < avail) x = reinterpret_cast<const uint4*>(src)[v];
+    const f32x4 a = {__uint_as_float(x.x << 16), __uint_as_float(x.x & 0xffff0000u),
+                     __uint_as_float(x.y << 16), __uint_as_float(x.y & 0xffff0000u)};
+    const f32x4 c = {__uint_as_float(x.z << 16), __uint_as_float(x.z & 0xffff0000u),
+                     __uint_as_float(x.w << 16), __uint_as_float(x.w & 0xffff0000u)};
+    *reinterpret_cast<f32x4*>(lds + row * LDK + 8 * cv) = a;
+    *reinterpret_cast<f32x4*>(lds + row * LDK + 8 * cv + 4) = c;
+  }
+}
+
+// Stage V[rows, D] (bf16) transposed into Vt[c][key] as fp32 (row stride
+// ldv), zero keys [rows, rows_pad).
+template <int D>
+__device__ __forceinline__ void stage_vt_widen(float* Vt, int ldv, const bf16* src, int rows,
+                                               int rows_pad) {
+  constexpr int VPR = D / 8;
+  const int total = rows_pad * VPR;
+  for (int v = threadIdx.x; v < total; v += blockDim.x) {
+    const int row = v / VPR, cv = v - row * VPR;
+    uint4 x = make_uint4(0u, 0u, 0u, 0u);
+    if (row < rows) x = reinterpret_cast<const uint4*>(src)[v];
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      Vt[(8 * cv + e) * ldv + row] =
+          __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+  }
 }
 
 // Sums and maximum over the whole wave (DPP row reductions, then row swaps).
@@ -163,28 +215,34 @@ __device__ __forceinline__ float wave_sum(float x) {
 // bisection over the 32-bit range, ties at it to the lowest indices (a
 // ballot prefix in ascending key order), the kept value rows summed across
 // the wave. Writes out (and the ascending indices) itself.
-template <int NT>
-__device__ __forceinline__ void hist_fallback_wave(const float* Qb, const float* Kb,
-                                                   const float* Vb, float* Ob, int32_t* Ib,
-                                                   int N, int q0, int topk, float scale,
-                                                   int lane) {
+template <int NT, typename T, int D>
+__device__ __forceinline__ void hist_fallback_wave(const T* Qb, const T* Kb, const T* Vb, T* Ob,
+                                                   int32_t* Ib, int N, int q0, int topk,
+                                                   float scale, int lane) {
+  constexpr bool POW2 = pow2_scale<D>();
   constexpr int NI = (16 * NT + 63) / 64;  // keys per lane
   const unsigned kq = static_cast<unsigned>(topk);
   const uint64_t below = (1ull << lane) - 1ull;
   for (int qq = 0; qq < 16; ++qq) {
     const int qi = q0 + qq;
     if (qi >= N) break;  // uniform
-    float qs[16];
-    ld_f32<16>(qs, Qb + static_cast<size_t>(qi) * 16);
+    float qs[D];
+    ld_row<T, D>(qs, Qb + static_cast<size_t>(qi) * D);
+    if constexpr (POW2) {
 #pragma unroll
-    for (int c = 0; c < 16; ++c) qs[c] *= scale;
+      for (int c = 0; c < D; ++c) qs[c] *= scale;
+    }
     int key[NI];
     float mloc = -INFINITY;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int j = lane + 64 * i;
       const bool valid = j < N && j != qi;
-      const float c = valid ? canon_row16(qs, Kb + static_cast<size_t>(j) * 16) : masked_score();
+      float c = masked_score();
+      if (valid) {
+        c = canon_row<T, D>(qs, Kb + static_cast<size_t>(j) * D);
+        if constexpr (!POW2) c *= scale;
+      }
       mloc = fmaxf(mloc, c);
       key[i] = ordered_key(c);
     }
@@ -206,9 +264,8 @@ __device__ __forceinline__ void hist_fallback_wave(const float* Qb, const float*
     for (int i = 0; i < NI; ++i) gt += key[i] > thr ? 1u : 0u;
     const unsigned need_ties = kq - wave_sum(gt);
     unsigned ties = 0u, base = 0u;
-    float acc[16], lsum = 0.f;
-#pragma unroll
-    for (int c = 0; c < 16; ++c) acc[c] = 0.f;
+    float lsum = 0.f;
+    float pw[NI];  // this lane's weights (0: not selected)
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int j = lane + 64 * i;
@@ -216,15 +273,12 @@ __device__ __forceinline__ void hist_fallback_wave(const float* Qb, const float*
       const uint64_t tmask = __ballot(tie);
       const bool sel = key[i] > thr || (tie && ties + __popcll(tmask & below) < need_ties);
       const uint64_t smask = __ballot(sel);
+      pw[i] = 0.f;
       if (sel) {
         // the ordered key maps back to the score by the same xor
         const float c = __int_as_float(ordered_key(__int_as_float(key[i])));
-        const float p = fast_exp2((c - mq) * kLog2eF);  // subtract first: exact near the max
-        lsum += p;
-        float vr[16];
-        ld_f32<16>(vr, Vb + static_cast<size_t>(j) * 16);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[e] = fmaf(p, vr[e], acc[e]);
+        pw[i] = fast_exp2((c - mq) * kLog2eF);  // subtract first: exact near the max
+        lsum += pw[i];
         if (Ib != nullptr) {
           const unsigned pos = base + static_cast<unsigned>(__popcll(smask & below));
           if (pos < kq) Ib[static_cast<size_t>(qi) * topk + pos] = j;
@@ -234,19 +288,36 @@ __device__ __forceinline__ void hist_fallback_wave(const float* Qb, const float*
       base += static_cast<unsigned>(__popcll(smask));
     }
     const float il = 1.f / wave_sum(lsum);
+    // the kept value rows summed across the wave, 16 channels at a time
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] = wave_sum(acc[e]);
-    if (lane < 4) {
-      f32x4 o;
+    for (int c0 = 0; c0 < D; c0 += 16) {
+      float acc[16];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float v = 0.f;
+      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          if (e == 4 * lane + r) v = acc[e];
-        o[r] = v * il;
+      for (int i = 0; i < NI; ++i) {
+        const int j = lane + 64 * i;
+        if (pw[i] != 0.f) {
+          float vr[16];
+          ld_row<T, 16>(vr, Vb + static_cast<size_t>(j) * D + c0);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[e] = fmaf(pw[i], vr[e], acc[e]);
+        }
       }
-      *reinterpret_cast<f32x4*>(Ob + static_cast<size_t>(qi) * 16 + 4 * lane) = o;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = wave_sum(acc[e]);
+      if (lane < 4) {
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = 0.f;
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (e == 4 * lane + r) v = acc[e];
+          o[r] = v * il;
+        }
+        st_row<T, 4>(Ob + static_cast<size_t>(qi) * D + c0 + 4 * lane, o);
+      }
     }
   }
 }
@@ -256,25 +327,31 @@ __device__ __forceinline__ void hist_fallback_wave(const float* Qb, const float*
 // Waves per SIMD the register budget is held to (the scores of a query tile
 // take NT x 4 registers); without the cap the compiler parks a second copy
 // of them in AGPRs and drops to one wave.
-template <int NT>
+template <int NT, int D>
 constexpr int hist_waves_per_eu() {
-  return NT <= 8 ? 4 : (NT <= 16 ? 3 : 2);
+  // wider heads add D/4 query and 12 D/16 value-block registers per lane
+  if constexpr (D >= 64) return 2;
+  return NT <= 8 ? (D <= 16 ? 4 : 3) : (NT <= 16 ? 3 : 2);
 }
 
-template <int NT, bool WITH_IDX>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(hist_waves_per_eu<NT>(), hist_waves_per_eu<NT>())))
-topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
-                 const float* __restrict__ V, float* __restrict__ O, int32_t* __restrict__ Idx,
+// T: the inputs' type (bf16 rows are widened to fp32 as they are staged, so
+// every score is the canonical fp32 chain of the widened values); D: the head
+// width (16, 32 or 64: D/16 output blocks of 16 channels).
+template <int NT, bool WITH_IDX, typename T, int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(hist_waves_per_eu<NT, D>(), hist_waves_per_eu<NT, D>())))
+topk_hist_kernel(const T* __restrict__ Q, const T* __restrict__ Kx,
+                 const T* __restrict__ V, T* __restrict__ O, int32_t* __restrict__ Idx,
                  int N, int n_qblk, int topk, float scale, int nblocks) {
-  using F = Frag<float, 16>;
-  constexpr int D = 16, LDK = F::LDK, NP = 16 * NT, LDV = NP + 4;
+  using F = Frag<float, D>;
+  constexpr int LDK = F::LDK, NP = 16 * NT, LDV = NP + 4, NH = D / 16;
+  static_assert(D % 16 == 0, "whole 16-channel output blocks");
   constexpr int BT = 4;  // tiles per score block
   static_assert(NT % BT == 0 && NP <= 32 * kHistSel, "tile count");
   extern __shared__ __align__(16) unsigned char smem_raw[];
   unsigned* flags = reinterpret_cast<unsigned*>(smem_raw);  // [0] a non-finite key element
   unsigned char* region_a = smem_raw + 16;
   float* Ks = reinterpret_cast<float*>(region_a);            // key rows, then scratch
-  float* Vt = reinterpret_cast<float*>(region_a + hist_region_a_bytes<NT>());
+  float* Vt = reinterpret_cast<float*>(region_a + hist_region_a_bytes<NT, D>());
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -285,22 +362,35 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   const bool live = q0 + col < N;
   const int qi = live ? q0 + col : N - 1;
   const size_t boff = static_cast<size_t>(b) * N * D;
-  const float* Kb = Kx + boff;
+  const T* Kb = Kx + boff;
+  // a power-of-two scale (d = 16, 64) is folded into q (exact); any other
+  // multiplies each score once, as the canonical score does
+  constexpr bool POW2 = pow2_scale<D>();
 
   // ---- stage the row's keys and transposed values ------------------------
   if (threadIdx.x == 0) flags[0] = 0u;
-  stage_rows<float, D, LDK>(Ks, Kb, N, NP);
-  stage_vt<float, D, 16>(Vt, LDV, V + boff, N, NP);
+  if constexpr (sizeof(T) == 4) {
+    stage_rows<float, D, LDK>(Ks, Kb, N, NP);
+    stage_vt<float, D, D>(Vt, LDV, V + boff, N, NP);
+  } else {
+    stage_rows_widen<D, LDK>(Ks, Kb, N, NP);
+    stage_vt_widen<D>(Vt, LDV, V + boff, N, NP);
+  }
   F frag;
-  frag.load_q(Q + boff + static_cast<size_t>(qi) * D, grp, scale);  // exact: power-of-two scale
+  ld_row<T, F::E>(frag.q, Q + boff + static_cast<size_t>(qi) * D + grp * F::E);
+  if constexpr (POW2) {
+#pragma unroll
+    for (int e = 0; e < F::E; ++e) frag.q[e] *= scale;
+  }
   bool finite_in = true;  // this lane's query elements
 #pragma unroll
   for (int e = 0; e < F::E; ++e) finite_in = finite_in && __builtin_isfinite(frag.q[e]);
   __syncthreads();
   {
-    bool kfin = true;  // the staged keys, a quarter row per thread and pass
-    for (int v = threadIdx.x; v < N * 4; v += blockDim.x) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(Ks + (v >> 2) * LDK + 4 * (v & 3));
+    bool kfin = true;  // the staged keys, four elements per thread and pass
+    constexpr int V4 = D / 4;
+    for (int v = threadIdx.x; v < N * V4; v += blockDim.x) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(Ks + (v / V4) * LDK + 4 * (v % V4));
 #pragma unroll
       for (int e = 0; e < 4; ++e) kfin = kfin && __builtin_isfinite(x[e]);
     }
@@ -319,7 +409,7 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
     for (int t = 0; t < BT; ++t) {
       const int tt = t0 + t;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s[tt][r] = acc[0][t][r];
+      for (int r = 0; r < 4; ++r) s[tt][r] = POW2 ? acc[0][t][r] : acc[0][t][r] * scale;
       if (tt == diag || 16 * tt + 16 > N) {  // wave-uniform
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -397,7 +487,6 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
     run = nrun;
   }
   int tb_l = -1;
-  unsigned above_l = 0u;
   if (qg >= 0) {
     const uint4 w = reinterpret_cast<const uint4*>(hist)[grp * 8 + qg];
     const unsigned hq[4] = {w.x - ((grp == 0 && qg == 0) ? n_masked : 0u), w.y, w.z, w.w};
@@ -405,27 +494,18 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
 #pragma unroll
     for (int e = 3; e >= 0; --e) {
       const unsigned nr = rr + hq[e];
-      if (rr < kq && nr >= kq) {
-        tb_l = 32 * grp + 4 * qg + e;
-        above_l = rr;
-      }
+      if (rr < kq && nr >= kq) tb_l = 32 * grp + 4 * qg + e;
       rr = nr;
     }
   }
   int tb;
-  unsigned above_tb;
   {
-    uint32_t tv[4], av[4];
+    uint32_t tv[4];
     gather_rows(static_cast<uint32_t>(tb_l + 1), tv);
-    gather_rows(above_l, av);
     tb = -1;
-    above_tb = 0u;
 #pragma unroll
     for (int g = 0; g < 4; ++g)
-      if (tv[g] != 0u) {
-        tb = static_cast<int>(tv[g]) - 1;
-        above_tb = av[g];
-      }
+      if (tv[g] != 0u) tb = static_cast<int>(tv[g]) - 1;
   }
   // bins tb - 1 .. tb + 1 bound the list (the margin is under half a bin)
   auto bin_count = [&](int bin) -> unsigned {
@@ -448,9 +528,9 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
                     (inv == 0.f || slack < 0.5f * w);
 
   if (!__all(fast)) {
-    hist_fallback_wave<NT>(Q + boff, Kb, V + boff, O + boff,
-                           Idx ? Idx + static_cast<size_t>(b) * N * topk : nullptr, N, q0, topk,
-                           scale, lane);
+    hist_fallback_wave<NT, T, D>(Q + boff, Kb, V + boff, O + boff,
+                                 Idx ? Idx + static_cast<size_t>(b) * N * topk : nullptr, N, q0,
+                                 topk, scale, lane);
     return;
   }
 
@@ -462,7 +542,9 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   auto expw = [&](float x) {
     return small ? fast_exp2(fmaf(x, kLog2eF, nm)) : fast_exp2((x - mx) * kLog2eF);
   };
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[NH];
+#pragma unroll
+  for (int h = 0; h < NH; ++h) acc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
   float lsum = 0.f;
   constexpr int NB32 = (NT * 4 + 31) / 32;
   uint32_t kept[NB32];  // bit (4 t + r) % 32 of word (4 t + r) / 32: kept key
@@ -481,14 +563,23 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   unsigned nl = 0u;
   wave_lds_sync();
   auto pv_pass = [&](auto exp_small) {
+    // output block h (channels 16 h .. 16 h + 15): V^T rows 16 h + col
     const float* vrow = Vt + col * LDV + 4 * grp;
-    f32x4 vnext = *reinterpret_cast<const f32x4*>(vrow);
+    f32x4 vnext[NH];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) vnext[h] = *reinterpret_cast<const f32x4*>(vrow + 16 * h * LDV);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      // this tile's value fragment was read a tile ahead: the MFMA below does
-      // not wait on the slot writes
-      const f32x4 vv = vnext;
-      if (t + 1 < NT) vnext = *reinterpret_cast<const f32x4*>(vrow + 16 * (t + 1));
+      // this tile's value fragments were read a tile ahead: the MFMAs below
+      // do not wait on the slot writes
+      f32x4 vv[NH];
+#pragma unroll
+      for (int h = 0; h < NH; ++h) vv[h] = vnext[h];
+      if (t + 1 < NT) {
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+          vnext[h] = *reinterpret_cast<const f32x4*>(vrow + 16 * h * LDV + 16 * (t + 1));
+      }
       float p[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -506,7 +597,9 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
         nl += inband ? 1u : 0u;
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) acc = mfma_f32_16x16x4(vv[u], p[u], acc);
+      for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[h] = mfma_f32_16x16x4(vv[h][u], p[u], acc[h]);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -518,9 +611,9 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
     band[i] = static_cast<uint32_t>(opaque(static_cast<int>(band[i])));
   }
   if (!__all(nl < static_cast<unsigned>(kHistSlots))) {  // a lane's share overflowed
-    hist_fallback_wave<NT>(Q + boff, Kb, V + boff, O + boff,
-                           Idx ? Idx + static_cast<size_t>(b) * N * topk : nullptr, N, q0, topk,
-                           scale, lane);
+    hist_fallback_wave<NT, T, D>(Q + boff, Kb, V + boff, O + boff,
+                                 Idx ? Idx + static_cast<size_t>(b) * N * topk : nullptr, N, q0,
+                                 topk, scale, lane);
     return;
   }
 
@@ -548,9 +641,9 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   const unsigned qoff = incl - cnt;
   const unsigned total = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(incl), 15));
   if (total > 512u || !__all(need <= 32u)) {  // beyond the flat list's (16 x 32) or a join list's (32) room
-    hist_fallback_wave<NT>(Q + boff, Kb, V + boff, O + boff,
-                           Idx ? Idx + static_cast<size_t>(b) * N * topk : nullptr, N, q0, topk,
-                           scale, lane);
+    hist_fallback_wave<NT, T, D>(Q + boff, Kb, V + boff, O + boff,
+                                 Idx ? Idx + static_cast<size_t>(b) * N * topk : nullptr, N, q0,
+                                 topk, scale, lane);
     return;
   }
   unsigned* wscr = reinterpret_cast<unsigned*>(region_a) + kHistWaves * 16 * kHistQWords + wave * 32;
@@ -624,7 +717,10 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
       const uint32_t m = static_cast<uint32_t>(static_cast<int>(o.x) >> 31);
       const float pw = expw(__uint_as_float(m ? o.x : (~o.x & 0x7fffffffu)));  // the score back
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = fmaf(pw, Vt[(4 * grp + r) * LDV + o.y], acc[r]);
+      for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[h][r] = fmaf(pw, Vt[(16 * h + 4 * grp + r) * LDV + o.y], acc[h][r]);
       lsum += grp == 0 ? pw : 0.f;
     }
   }
@@ -633,10 +729,13 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   const float l = rows_sum(lsum);
   const float il = 1.f / l;
   if (live) {
-    f32x4 o;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) o[r] = acc[r] * il;
-    *reinterpret_cast<f32x4*>(O + boff + static_cast<size_t>(qi) * D + 4 * grp) = o;
+    for (int h = 0; h < NH; ++h) {
+      float o[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = acc[h][r] * il;
+      st_row<T, 4>(O + boff + static_cast<size_t>(qi) * D + 16 * h + 4 * grp, o);
+    }
   }
   if constexpr (!WITH_IDX) return;
   // ---- retained indices, ascending -----------------------------------------
@@ -724,28 +823,48 @@ topk_hist_kernel(const float* __restrict__ Q, const float* __restrict__ Kx,
   }
 }
 
+// Rows of up to 512 keys at d = 16 and 32, 256 at d = 64: the fp32 key rows
+// and transposed value rows of a batch row then fit one workgroup's LDS.
+static int hist_max_n(int d) { return d == 64 ? 256 : 512; }
+
 bool topk_hist_supported(const TopkArgs& a) {
-  return a.dtype == kF32 && a.d == 16 && a.select == kSelTopk && a.topk > kTopkSmallMax &&
-         a.N <= 512 && (__builtin_bit_cast(uint32_t, a.scale) & 0x007fffffu) == 0u;
+  return (a.dtype == kF32 || a.dtype == kBf16) && (a.d == 16 || a.d == 32 || a.d == 64) &&
+         a.select == kSelTopk && a.topk > kTopkSmallMax && a.N <= hist_max_n(a.d);
 }
 
-template <int NT>
+template <int NT, typename T, int D>
 static hipError_t launch_hist(const TopkArgs& a) {
+  static_assert(hist_lds_bytes<NT, D>() <= 160 * 1024, "one workgroup's LDS");
   const int n_qblk = (a.N + 16 * kHistWaves - 1) / (16 * kHistWaves);
   const int nblocks = a.B * n_qblk;
-  auto kern = a.idx != nullptr ? topk_hist_kernel<NT, true> : topk_hist_kernel<NT, false>;
-  hipLaunchKernelGGL(kern, dim3(nblocks), dim3(64 * kHistWaves), hist_lds_bytes<NT>(),
-                     static_cast<hipStream_t>(a.stream), static_cast<const float*>(a.q),
-                     static_cast<const float*>(a.k), static_cast<const float*>(a.v),
-                     static_cast<float*>(a.out), a.idx, a.N, n_qblk, a.topk, a.scale, nblocks);
+  auto kern = a.idx != nullptr ? topk_hist_kernel<NT, true, T, D> : topk_hist_kernel<NT, false, T, D>;
+  constexpr size_t lds = hist_lds_bytes<NT, D>();
+  hipLaunchKernelGGL(kern, dim3(nblocks), dim3(64 * kHistWaves), lds,
+                     static_cast<hipStream_t>(a.stream), static_cast<const T*>(a.q),
+                     static_cast<const T*>(a.k), static_cast<const T*>(a.v),
+                     static_cast<T*>(a.out), a.idx, a.N, n_qblk, a.topk, a.scale, nblocks);
   return hipGetLastError();
 }
 
+template <typename T, int D>
+static hipError_t run_hist_t(const TopkArgs& a) {
+  if (a.N <= 128) return launch_hist<8, T, D>(a);
+  if (a.N <= 256) return launch_hist<16, T, D>(a);
+  if constexpr (D <= 32) {
+    if (a.N <= 384) return launch_hist<24, T, D>(a);
+    return launch_hist<32, T, D>(a);
+  }
+  return hipErrorInvalidValue;
+}
+
 hipError_t run_topk_hist(const TopkArgs& a) {
-  if (a.N <= 128) return launch_hist<8>(a);
-  if (a.N <= 256) return launch_hist<16>(a);
-  if (a.N <= 384) return launch_hist<24>(a);
-  return launch_hist<32>(a);
+  const bool bf = a.dtype == kBf16;
+  switch (a.d) {
+    case 16: return bf ? run_hist_t<bf16, 16>(a) : run_hist_t<float, 16>(a);
+    case 32: return bf ? run_hist_t<bf16, 32>(a) : run_hist_t<float, 32>(a);
+    case 64: return bf ? run_hist_t<bf16, 64>(a) : run_hist_t<float, 64>(a);
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace tarmac
