@@ -230,7 +230,8 @@ int tarmac_dense_bwd_noalloc(const float* q, const float* k, const float* v, con
  *                   d = 16: x = hi + mid + lo, six bf16 products per score),
  *                   proven against the split error bound;
  *   split32      -- the same on 32-key x 32-query tiles (d = 16, k <= 4,
- *                   N <= 256): two lanes per query instead of four; bf16
+ *                   N <= 256, bf16 N <= 1024): two lanes per query instead
+ *                   of four; bf16
  *                   inputs take one bf16 product per tile (the inputs as
  *                   they are) instead of six split products;
  *   filter       -- all pairs scored on split-bf16 MFMA (fp32 inputs) or
@@ -252,8 +253,8 @@ int tarmac_dense_bwd_noalloc(const float* q, const float* k, const float* v, con
  * MI355X for the shape), 2 = filter where supported (fp32 d = 16, 32, 64;
  * bf16 d = 16), 3 = lists for fp32 (bf16 runs packed), 4 = packed split where
  * supported (fp32 d = 16; packed elsewhere), 5 = split32 where supported
- * (fp32 and bf16, d = 16, k <= 4, N <= 256; packed split, then packed,
- * elsewhere). bf16 retained sets are always
+ * (d = 16, k <= 4, N <= 256 for fp32 and 1024 for bf16; packed split,
+ * then packed, elsewhere). bf16 retained sets are always
  * the exact top k of the canonical fp32 scores of the inputs converted to
  * fp32. Process-wide (an atomic setting: concurrent calls stay safe and get
  * identical results). Returns the previous mode, or -1 (and sets the last

@@ -315,7 +315,8 @@ def test_streaming_topk_bf16_matches_fused_bitwise(N, d, kk, chunk):
 
 @pytest.mark.parametrize("N,kk,chunk", [(6, 2, None), (33, 4, None), (128, 1, None), (200, 3, None),
                                         (256, 2, None), (256, 4, None), (256, 2, 80), (256, 4, 16),
-                                        (130, 3, 64), (256, 1, 128)])
+                                        (130, 3, 64), (256, 1, 128), (512, 4, None), (1024, 2, None),
+                                        (1024, 4, 256), (700, 3, None)])
 def test_bf16_split32_exact(N, kk, chunk):
     """bf16 heads at d = 16 on the 32 x 32 kernel (mode 5: one bf16 MFMA per
     tile, the bf16 accumulation bound in the proof): indices bit-exact against

@@ -126,7 +126,7 @@ hipError_t run_topk(const TopkArgs& a);
 hipError_t run_topk_filter(const TopkArgs& a);
 hipError_t run_topk_packed(const TopkArgs& a, bool split);
 hipError_t run_topk_packed_d128(const TopkArgs& a);  // topk_packed_d128.hip
-bool split32_supported(const TopkArgs& a);  // fp32 / bf16, d = 16, k <= 4, N <= 256, top-k rule
+bool split32_supported(const TopkArgs& a);  // d = 16, k <= 4, N <= 256 (bf16: 1024), top-k rule
 hipError_t run_topk_split32(const TopkArgs& a);
 size_t split32_lds_bytes(int dtype, int kc);
 bool topk_hist_supported(const TopkArgs& a);  // fp32, d = 16, k > 8, N <= 512

@@ -1092,8 +1092,9 @@ enum TopkPath { kPathPacked, kPathPackedSplit, kPathSplit32, kPathFilter, kPathL
 //     17.9 vs 19.9 lists), except at N <= 32, where the one-round-trip list
 //     kernel wins at every k (rocprof, B=1024 N=32 k=4: 7.4 vs 7.8 packed).
 //   fp32, d = 8, 32, 64: register lists for k <= 2 (every k at N <= 32), packed above.
-//   bf16: packed, the 32 x 32 kernel at d = 16, k = 4, N = 193 .. 256 with
-//     two query tiles per wave, or the bf16 filter at d = 16 with N >= 256 and k >= 4
+//   bf16: packed, the 32 x 32 kernel at d = 16 with two query tiles per wave
+//     (k = 4, N = 193 .. 256; k = 2, 3, N = 193 .. 384, B <= 1024), or the bf16
+//     filter at d = 16 with N >= 256 and k >= 4
 //     (B=1024 N=256 k=4: 35.1 vs 40.4) or k = 2, 3 with B <= 1024; at d = 16, rows of up to 64 keys
 //     with k <= 2 and rows of up to 32 keys take the one-round-trip register
 //     lists, which widen bf16 to fp32 and select on the canonical scores
@@ -1121,12 +1122,16 @@ static TopkPath choose_path(const TopkArgs& a, int mode) {
     // (B=32 N=512 k=2/3: 9.4/10.3 vs 15.7/18.5 packed; B=32 N=1024 k=3: 15.2
     // vs 30.9; B=256 N=256 k=2/3: 9.3/10.4 vs 11.0/12.9); at B = 4096 the
     // packed scan's lower cost per score wins (N=512 k=2: 234.9 vs 242.5)
-    // k = 4 on rows of 193 to 256 keys, two query tiles per wave: the
-    // 32 x 32 kernel's single-product form (one bf16 MFMA per tile; B=1024
-    // N=256: 28.7 vs 31.2 filter; B=4096: 101.3 vs 109.9); at k <= 3 and on
-    // shorter rows the filter and packed kernels are faster (B=4096 N=256
-    // k=3: 90.6 vs 83.4; N=192 k=4: 87.8 vs 84.5)
-    if (split32_supported(a) && a.topk == 4 && a.N > 192 && !one_query_tile(a.B, a.N))
+    // the 32 x 32 kernel's single-product form (one bf16 MFMA per tile),
+    // two query tiles per wave: k = 4 on rows of 193 to 256 keys (B=1024
+    // N=256: 28.7 vs 31.2 filter; B=4096: 101.3 vs 109.9), and k = 2, 3 on
+    // rows of 193 to 384 keys where the filter would run (B <= 1024; B=256
+    // N=384 k=2/3: 13.3/14.8 vs 16.0/18.2; B=1024: 40.2/46.5 vs 50.3/61.2);
+    // elsewhere the filter and packed kernels are as fast or faster (B=4096
+    // N=256 k=3: 90.6 vs 83.4 packed; N=192 k=4: 87.8 vs 84.5; N=512 and
+    // 1024: equal to 15% slower)
+    if (split32_supported(a) && a.N > 192 && !one_query_tile(a.B, a.N) &&
+        ((a.topk == 4 && a.N <= 256) || (a.topk >= 2 && a.topk <= 3 && a.N <= 384 && a.B <= 1024)))
       return kPathSplit32;
     if (filt && a.N >= 256 && (a.topk >= 4 || (a.topk >= 2 && a.B <= 1024))) return kPathFilter;
     return kPathPacked;

@@ -1,5 +1,5 @@
-// Exact score-then-select top-k attention (k <= 4) for fp32 inputs at
-// d = 16, on 32-key x 32-query score tiles.
+// Exact score-then-select top-k attention (k <= 4) for fp32 and bf16 inputs
+// at d = 16, on 32-key x 32-query score tiles.
 //
 // Reference behaviour: src/kernels/fused_topk_attention.py:211-333
 // (fused_topk_attention_tiled) and src/kernels/streaming_topk_attention.py:
@@ -387,7 +387,10 @@ size_t split32_lds_bytes(int dtype, int kc) {
 // leave a CU fewer than four four-wave workgroups (N = 512: two), where the
 // 16 x 16 kernel's eight-wave workgroups keep sixteen waves per CU.
 bool split32_supported(const TopkArgs& a) {
-  return (a.dtype == kF32 || a.dtype == kBf16) && a.d == 16 && a.topk <= 4 && a.N <= 256 &&
+  // bf16 rows take 48 bytes a key: a resident row of up to 1024 keys (the
+  // most the packed fields name) leaves three workgroups per CU
+  const int max_n = a.dtype == kBf16 ? 1024 : 256;
+  return (a.dtype == kF32 || a.dtype == kBf16) && a.d == 16 && a.topk <= 4 && a.N <= max_n &&
          a.select == kSelTopk;
 }
 
