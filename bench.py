@@ -530,6 +530,22 @@ def main() -> int:
           harness.time_interleaved(fi, max(10, args.reps // 2), 3, 2).items()}
     detail["d128_B256_N256_us"] = {n: round(s["min_us"], 3) for n, s in si.items()}
     del q8, k8, v8
+    # large k off fp32 d = 16 (the histogram kernel at d = 32, 64 and on bf16)
+    lk = {}
+    for (b9, n9, d9, k9) in ((256, 384, 16, 95), (256, 384, 32, 95), (256, 256, 64, 12),
+                             (1024, 256, 16, 12)):
+        g9 = np.random.default_rng(9 + n9 + d9)
+        base9 = [torch.from_numpy(g9.standard_normal((b9, n9, d9)).astype(np.float32)).to(dev)
+                 for _ in range(3)]
+        for tag, dt in (("f32", torch.float32), ("bf16", torch.bfloat16)):
+            qa, ka, va = (t.to(dt) for t in base9)
+            fi = {"dense": (lambda qa=qa, ka=ka, va=va: fused_dense_attention(qa, ka, va)),
+                  "topk": (lambda qa=qa, ka=ka, va=va, k9=k9: topk_attention(qa, ka, va, k9))}
+            si = {n: harness.stats(s) for n, s in
+                  harness.time_interleaved(fi, max(10, args.reps // 2), 3, 2).items()}
+            lk[f"B{b9}_N{n9}_d{d9}_k{k9}_{tag}"] = {n: round(s["min_us"], 3) for n, s in si.items()}
+        del base9
+    detail["large_k_us"] = lk
     del fi, q7, k7, v7, qh, kh, vh
 
     # ---- streaming top-k, B=256, N in {512, 1024}, fp32 and bf16
