@@ -70,6 +70,55 @@ def test_dense_bf16(N, d):
     assert normwise(out, ref) <= BF16_TOL
 
 
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("B,N", [(4, 256), (128, 256), (64, 100), (1024, 256)])
+@pytest.mark.parametrize("spread", [0.0, 15.0, 60.0])
+def test_dense_loose_offset_bound(dtype, B, N, spread):
+    """A row staged in one chunk takes its exponent offset from |q| max|k|
+    instead of a running maximum. Keys with a large component orthogonal to
+    the queries (`spread`) push that bound far above the true maximum: at 15
+    the terms shrink by about 2^-40 and stay normal; at 60 they underflow,
+    the query's sum falls below 2^-64 and the wave reruns the row with the
+    running maximum. Every other query carries the large component, so waves
+    mix rows that need the rerun with rows that do not; one, two and (bf16)
+    four query tiles per wave (B = 4 / 128 / 1024 at N = 256)."""
+    from tarmac.kernels import fused_dense_attention
+    d = 16
+    g = np.random.default_rng(int(spread) + B + N)
+    q = g.standard_normal((B, N, d)).astype(np.float32) * 0.1
+    k = g.standard_normal((B, N, d)).astype(np.float32) * 0.1
+    v = g.standard_normal((B, N, d)).astype(np.float32)
+    q[:, ::2, 0] = 8.0
+    q[:, 1::2, 0] = g.standard_normal((B, N // 2)).astype(np.float32)
+    k[..., 0] = g.standard_normal((B, N)).astype(np.float32)
+    k[..., 1] = spread
+    if dtype == "bf16":
+        q, k, v = (O.bf16_round(x) for x in (q, k, v))
+        out = host(fused_dense_attention(*dev(q, k, v, dtype=torch.bfloat16)))
+        tol = BF16_TOL
+    else:
+        out = host(fused_dense_attention(*dev(q, k, v)))
+        tol = F32_TOL
+    rows = np.arange(B) if B <= 128 else np.random.default_rng(B).choice(B, 24, replace=False)
+    ref = O.canon_dense(q[rows], k[rows], v[rows])
+    assert np.isfinite(out).all()
+    assert normwise(out[rows], ref) <= tol
+
+
+@pytest.mark.parametrize("B,N,d", [(1024, 256, 16), (4096, 256, 16), (512, 512, 16), (1024, 256, 32),
+                                   (256, 256, 64)])
+def test_dense_bf16_large_batch(B, N, d):
+    """The launch shapes the bench times (two and four query tiles per wave)
+    on sampled rows against float64 evaluation of the bf16 inputs."""
+    from tarmac.kernels import fused_dense_attention
+    q, k, v = qkv(5 * B + N + d, B, N, d)
+    qb, kb, vb = (O.bf16_round(x) for x in (q, k, v))
+    out = host(fused_dense_attention(*dev(q, k, v, dtype=torch.bfloat16)))
+    rows = np.random.default_rng(B + N).choice(B, 16, replace=False)
+    assert np.isfinite(out).all()
+    assert normwise(out[rows], O.canon_dense(qb[rows], kb[rows], vb[rows])) <= BF16_TOL
+
+
 def test_dense_headline_shape():
     from tarmac.kernels import fused_dense_attention
     B, N, d = 1024, 256, 16

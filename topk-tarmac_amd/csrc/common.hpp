@@ -27,6 +27,13 @@ __device__ __forceinline__ float bf16_to_f32(bf16 h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
+// a.lo * b.lo + a.hi * b.hi + c for bf16 pairs in 32-bit words (v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
 // Round-to-nearest-even fp32 -> bf16 (the rounding Tensor.to(torch.bfloat16) uses).
 __device__ __forceinline__ bf16 f32_to_bf16(float f) {
   uint32_t u = __float_as_uint(f);

@@ -12,17 +12,19 @@
 //                                         is its own probability p[u] -- no
 //                                         cross-lane data movement)
 // V is staged transposed in LDS so the A operand of the PV product is a
-// contiguous read. Online softmax per 64-key block: a block's maximum is
-// shared by the 4 lanes of a query with two row swaps (VALU, no LDS), and the
-// running offset is raised -- rescaling the query's sum and accumulator --
-// only when the block's maximum exceeds it by more than 2^8, so after the
-// first block a score costs half a v_max3, one fma and one exp2 (plus, in
-// bf16, half a conversion and half a v_dot2 for the row sum, which adds the
-// bf16-rounded weights the PV product uses). The running sum stays per lane and is
-// combined once at the end. fp32 scores come out of the product already in
-// the log2 domain (q is pre-multiplied by scale*log2(e), exact for the
-// power-of-two scales; c = 1); bf16 scores stay raw and c = scale*log2(e) is
-// applied inside the exponent's argument, fma(s, c, -off).
+// contiguous read. A row staged in one chunk (the default up to the LDS
+// budget) takes a fixed exponent offset per query, c |q| max_j |k_j|, so a
+// score costs one exp2 and no maximum: fp32 products start at -offset and
+// return the exponent itself (q pre-multiplied by c = scale*log2(e)), bf16
+// scores stay raw and take fma(s, c, -offset). A row whose bound sits too far
+// above its true maximum (its softmax sum below 2^-64) is run again with the
+// online softmax that multi-chunk rows use: per 64-key block a maximum shared
+// by the 4 lanes of a query with two row swaps (VALU, no LDS), the running
+// offset raised -- rescaling the query's sum and accumulator -- only when a
+// block's maximum exceeds it by more than 2^8. bf16 probabilities are rounded
+// to bf16 for the PV product, and the row sum adds exactly those weights on
+// the matrix core (an all-ones A operand); fp32 sums stay per lane and are
+// combined once at the end.
 #include "frag.hpp"
 #include "select.hpp"
 #include "tarmac_internal.hpp"
@@ -122,12 +124,166 @@ __device__ __forceinline__ float query_max4(float x) {
   return max_plain(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-// Softmax terms are 2^(c s - off) with off a running maximum of c s that is
-// only raised when a block's maximum exceeds it by more than 2^kDenseLag:
-// terms then stay below 2^kDenseLag (no overflow, no loss of precision in
-// fp32), and after the first block a raise -- a rescale of the query's sum
-// and accumulator -- is rare.
+// Softmax terms are 2^(c s - off). Where the whole row is staged at once
+// (one key chunk), off is fixed per query before the first block:
+// off = c |q| max_j |k_j| >= c s for every key (Cauchy-Schwarz), so no term
+// exceeds 1 and a block needs no maximum. The bound can sit far above the
+// row's true maximum; terms then shrink by 2^-(gap) and the query's sum shows
+// it: a sum below 2^-64 (a gap of more than 64 - log2 N) makes the wave run
+// the row again with the running maximum below, the path every multi-chunk
+// row takes. With the sum at or above 2^-64 the largest term is at least
+// 2^-74 (N <= 1024 keys in one chunk), so only terms below 2^-52 of it can
+// leave the fp32 (and bf16) normal range.
+// The running maximum of c s is only raised when a block's maximum exceeds it
+// by more than 2^kDenseLag: terms then stay below 2^kDenseLag (no overflow,
+// no loss of precision in fp32), and after the first block a raise -- a
+// rescale of the query's sum and accumulator -- is rare.
 constexpr float kDenseLag = 8.f;
+constexpr float kDenseTinySum = 0x1p-64f;
+
+// All-ones bf16 A operand (0x3f80 = 1.0).
+constexpr bf16x8 kOnesBf16x8 = {1.0, 1.0, 1.0, 1.0, 1.0, 1.0, 1.0, 1.0};
+
+// The query's softmax sum: fp32 lanes hold a quarter each (element 0), bf16
+// lanes the whole sum (every element).
+template <typename T>
+__device__ __forceinline__ float row_total(f32x4 l) {
+  if constexpr (sizeof(T) == 2) return l[0];
+  float t = l[0] + __shfl_xor(l[0], 16);
+  return t + __shfl_xor(t, 32);
+}
+
+// Fixed-offset exponents (fp32) of QT query tiles against BT key tiles: the
+// fragments hold c q, and every MFMA chain starts at -off, so the product
+// returns c s - off itself -- no VALU between the product and exp2. (bf16
+// would need c q as a bf16 pair, twice the products: measured slower than the
+// fma it saves.)
+template <typename F, int QT, int BT, typename T>
+__device__ __forceinline__ void block_exponents(const F (&frag)[QT], const T* Ks, int kb, int lane,
+                                                const float (&neg)[QT], f32x4 (&s)[QT][BT]) {
+  const int col = lane & 15, grp = lane >> 4;
+  typename F::KF kf[BT];
+#pragma unroll
+  for (int t = 0; t < BT; ++t) kf[t] = F::load_k(Ks + (kb + 16 * t + col) * F::LDK, grp);
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int t = 0; t < BT; ++t) s[qt][t] = f32x4{neg[qt], neg[qt], neg[qt], neg[qt]};
+#pragma unroll
+  for (int i = 0; i < F::NI; ++i)
+#pragma unroll
+    for (int t = 0; t < BT; ++t)
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) s[qt][t] = frag[qt].step(kf[t], i, s[qt][t]);
+}
+
+// The block loop over one staged chunk (rows [0, cnp) of Ks / Vt, keys
+// c0 + row): scores, the self and chunk-end masks, exponents, row sums and
+// the P.V product. ONLINE: off follows the running maximum; otherwise off
+// is the fixed per-query bound.
+template <bool ONLINE, typename T, int D, int QT>
+__device__ __forceinline__ void dense_blocks(const Frag<T, D> (&frag)[QT], const T* Ks, const T* Vt,
+                                             int ldv, int c0, int cn, int cnp, int q0,
+                                             const bool (&self_r)[4], int lane, int grp, float post,
+                                             f32x4 (&acc)[QT][PvOperand<T, D>::NH],
+                                             float (&off)[QT], f32x4 (&l_run)[QT]) {
+  using F = Frag<T, D>;
+  using PV = PvOperand<T, D>;
+  constexpr int LDK = F::LDK;
+  constexpr int NH = PV::NH;
+  constexpr int BT = kDenseBlockTiles;
+  constexpr int BK = 16 * BT;
+  const int kend = c0 + cn;  // rows past the chunk end are zero padding
+  float neg[QT];             // the exponent's offset
+  if constexpr (!ONLINE) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) neg[qt] = -off[qt];
+  }
+  for (int kb0 = 0; kb0 < cnp; kb0 += BK) {
+    f32x4 s[QT][BT];
+    constexpr bool FOLDED = !ONLINE && sizeof(T) == 4;  // s is already c s - off
+    if constexpr (FOLDED) block_exponents<F, QT, BT>(frag, Ks, kb0, lane, neg, s);
+    else block_scores<F, QT, BT>(frag, Ks, kb0, LDK, lane, s);
+    const int kabs = c0 + kb0;
+    // the self pair (one select per element of a diagonal tile, on the
+    // loop-invariant lane predicates) and keys past the chunk end
+    mask_block<QT, BT>(s, self_r, q0, kabs, kend, grp, -INFINITY);
+    if constexpr (ONLINE) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < BT; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[qt][t][r]);
+        const float m_blk = query_max4(mloc) * post;
+        if (m_blk > off[qt] + kDenseLag) {  // rare after the first block
+          const float alpha = fast_exp2(off[qt] - m_blk);  // 0 while nothing has been seen
+          l_run[qt] *= alpha;
+#pragma unroll
+          for (int h = 0; h < NH; ++h) acc[qt][h] *= alpha;
+          off[qt] = m_blk;
+        }
+        neg[qt] = off[qt] == -INFINITY ? 0.f : -off[qt];  // a block of masked keys only
+      }
+    }
+    constexpr int TS = PV::TILES;
+    static_assert(BT % TS == 0, "whole PV steps per block");
+#pragma unroll
+    for (int t0 = 0; t0 < BT; t0 += TS) {
+      float p[QT][TS][4];
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int t = 0; t < TS; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            p[qt][t][r] = FOLDED ? fast_exp2(s[qt][t0 + t][r])
+                                 : fast_exp2(fmaf(s[qt][t0 + t][r], post, neg[qt]));
+      if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+          for (int t = 0; t < TS; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) l_run[qt][0] += p[qt][t][r];
+        PV::template pv_step<QT>(acc, Vt, ldv, kb0 + 16 * t0, lane, p);
+      } else {
+        bf16x8 pb[QT];
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          pb[qt] = pack_p_pair(p[qt][0], p[qt][1]);
+          // the row sum on the matrix core: an all-ones A operand adds the
+          // step's 32 weights of the query into every output element
+          l_run[qt] = mfma_bf16_16x16x32(kOnesBf16x8, pb[qt], l_run[qt]);
+        }
+        PV::template pv_step_packed<QT>(acc, Vt, ldv, kb0 + 16 * t0, lane, pb);
+      }
+    }
+  }
+}
+
+// Sum of squares of LDS row `row` (D elements, 16-byte aligned).
+template <typename T, int D>
+__device__ __forceinline__ float row_sumsq(const T* row) {
+  constexpr int VE = 16 / sizeof(T);
+  float a = 0.f;
+#pragma unroll
+  for (int c = 0; c < D / VE; ++c) {
+    const uint4 w = *reinterpret_cast<const uint4*>(row + c * VE);
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (sizeof(T) == 4) {
+        const float x = __uint_as_float(ww[e]);
+        a = fmaf(x, x, a);
+      } else {
+        a = dot2_bf16(ww[e], ww[e], a);
+      }
+    }
+  }
+  return a;
+}
 
 template <typename T, int D, int QT>
 __global__ void __launch_bounds__(256)
@@ -138,15 +294,18 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
   using PV = PvOperand<T, D>;
   constexpr int LDK = F::LDK;
   constexpr int NH = PV::NH;
-  constexpr int BT = kDenseBlockTiles;
-  constexpr int BK = 16 * BT;
+  constexpr int BK = 16 * kDenseBlockTiles;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int kcp = (kc + BK - 1) / BK * BK;  // chunk rows padded to whole blocks
   const int ldv = kcp + 4;
   T* Ks = reinterpret_cast<T*>(smem_raw);
   T* Vt = Ks + static_cast<size_t>(kcp) * LDK;
+  // the row's max |k|^2 (bits of a non-negative float), after V^T
+  uint32_t* kmax_slot = reinterpret_cast<uint32_t*>(Vt + static_cast<size_t>(PV::CP) * ldv);
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  // the wave index in an SGPR, so tile tests on q0 are scalar
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
   const int blk = xcd_logical_block(blockIdx.x, nblocks);
   const int b = blk / n_qblk, qblk = blk - b * n_qblk;
   const int q0 = (qblk * nw + wave) * 16 * QT;
@@ -169,95 +328,81 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
   for (int r = 0; r < 4; ++r) self_r[r] = (4 * grp + r == col);
 
   f32x4 acc[QT][NH];
-  float off[QT], l_run[QT];
+  float off[QT];
+  f32x4 l_run[QT];  // fp32: element 0, this lane's share; bf16: the whole sum
+  auto reset = [&]() {
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
 #pragma unroll
-    for (int h = 0; h < NH; ++h) acc[qt][h] = f32x4{0.f, 0.f, 0.f, 0.f};
-    off[qt] = -INFINITY;
-    l_run[qt] = 0.f;
-  }
-
-  for (int c0 = 0; c0 < N; c0 += kc) {
-    const int cn = min(kc, N - c0);
-    const int cnp = (cn + BK - 1) / BK * BK;
-    __syncthreads();
-    // K and V^T in one pass of loads; bf16 rows transpose four at a time
-    // (8-byte stores instead of 2-byte ones), fp32 keeps one store per
-    // element, measured no slower
-    stage_kv<T, D, LDK, PV::CP>(Ks, Vt, ldv, Kx + boff + static_cast<size_t>(c0) * D,
-                                V + boff + static_cast<size_t>(c0) * D, cn, cnp);
-    __syncthreads();
-    if (q0 >= N) continue;
-    const int kend = c0 + cn;  // rows past the chunk end are zero padding
-    for (int kb0 = 0; kb0 < cnp; kb0 += BK) {
-      f32x4 s[QT][BT];
-      block_scores<F, QT, BT>(frag, Ks, kb0, LDK, lane, s);
-      const int kabs = c0 + kb0;
-      // the self pair (one select per element of a diagonal tile, on the
-      // loop-invariant lane predicates) and keys past the chunk end
-      mask_block<QT, BT>(s, self_r, q0, kabs, kend, grp, -INFINITY);
-      float neg[QT];  // the exponent's offset
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < BT; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[qt][t][r]);
-        const float m_blk = query_max4(mloc) * post;
-        if (m_blk > off[qt] + kDenseLag) {  // rare after the first block
-          const float alpha = fast_exp2(off[qt] - m_blk);  // 0 while nothing has been seen
-          l_run[qt] *= alpha;
-#pragma unroll
-          for (int h = 0; h < NH; ++h) acc[qt][h] *= alpha;
-          off[qt] = m_blk;
-        }
-        neg[qt] = off[qt] == -INFINITY ? 0.f : -off[qt];  // a block of masked keys only
-      }
-      constexpr int TS = PV::TILES;
-      static_assert(BT % TS == 0, "whole PV steps per block");
-#pragma unroll
-      for (int t0 = 0; t0 < BT; t0 += TS) {
-        float p[QT][TS][4];
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-          for (int t = 0; t < TS; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) p[qt][t][r] = fast_exp2(fmaf(s[qt][t0 + t][r], post, neg[qt]));
-        if constexpr (sizeof(T) == 4) {
-#pragma unroll
-          for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-            for (int t = 0; t < TS; ++t)
-#pragma unroll
-              for (int r = 0; r < 4; ++r) l_run[qt] += p[qt][t][r];
-          PV::template pv_step<QT>(acc, Vt, ldv, kb0 + 16 * t0, lane, p);
-        } else {
-          bf16x8 pb[QT];
-#pragma unroll
-          for (int qt = 0; qt < QT; ++qt) {
-            pb[qt] = pack_p_pair(p[qt][0], p[qt][1]);
-            l_run[qt] = sum_bf16x8(pb[qt], l_run[qt]);
-          }
-          PV::template pv_step_packed<QT>(acc, Vt, ldv, kb0 + 16 * t0, lane, pb);
-        }
-      }
+      for (int h = 0; h < NH; ++h) acc[qt][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+      off[qt] = -INFINITY;
+      l_run[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+  };
+  reset();
+
+  if (kc >= N) {
+    // the whole row in one chunk: fixed offsets from the row's max |k|
+    if (threadIdx.x == 0) *kmax_slot = 0u;
+    const int cnp = (N + BK - 1) / BK * BK;
+    __syncthreads();
+    stage_kv<T, D, LDK, PV::CP>(Ks, Vt, ldv, Kx + boff, V + boff, N, cnp);
+    __syncthreads();
+    float kn2 = 0.f;  // fmaxf drops a NaN row; its scores fail the check below
+    for (int r = threadIdx.x; r < N; r += blockDim.x) kn2 = fmaxf(kn2, row_sumsq<T, D>(Ks + r * LDK));
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) kn2 = fmaxf(kn2, __shfl_xor(kn2, m));
+    if (lane == 0) atomicMax(kmax_slot, __float_as_uint(kn2));
+    __syncthreads();
+    if (q0 >= N) return;
+    const float kmax2 = __uint_as_float(*kmax_slot);
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float qn2 = frag[qt].sumsq();
+      qn2 += __shfl_xor(qn2, 16);
+      qn2 += __shfl_xor(qn2, 32);
+      off[qt] = post * __builtin_amdgcn_sqrtf(qn2 * kmax2);  // v_sqrt_f32, 1 ulp
+    }
+    dense_blocks<false, T, D, QT>(frag, Ks, Vt, ldv, 0, N, cnp, q0, self_r, lane, grp, post, acc,
+                                  off, l_run);
+    bool low = false;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const float l_tot = row_total<T>(l_run[qt]);
+      low |= !(l_tot >= kDenseTinySum);  // also a NaN sum
+    }
+    if (__any(low)) {  // uniform: the wave runs the row again, online
+      reset();
+      dense_blocks<true, T, D, QT>(frag, Ks, Vt, ldv, 0, N, cnp, q0, self_r, lane, grp, post, acc,
+                                   off, l_run);
+    }
+  } else {
+    for (int c0 = 0; c0 < N; c0 += kc) {
+      const int cn = min(kc, N - c0);
+      const int cnp = (cn + BK - 1) / BK * BK;
+      __syncthreads();
+      // K and V^T in one pass of loads; bf16 rows transpose four at a time
+      // (8-byte stores instead of 2-byte ones), fp32 keeps one store per
+      // element, measured no slower
+      stage_kv<T, D, LDK, PV::CP>(Ks, Vt, ldv, Kx + boff + static_cast<size_t>(c0) * D,
+                                  V + boff + static_cast<size_t>(c0) * D, cn, cnp);
+      __syncthreads();
+      if (q0 >= N) continue;
+      dense_blocks<true, T, D, QT>(frag, Ks, Vt, ldv, c0, cn, cnp, q0, self_r, lane, grp, post, acc,
+                                   off, l_run);
+    }
+    if (q0 >= N) return;
   }
-  if (q0 >= N) return;
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    float l_tot = l_run[qt] + __shfl_xor(l_run[qt], 16);
-    l_tot += __shfl_xor(l_tot, 32);
+    const float l_tot = row_total<T>(l_run[qt]);
     const int qi = q0 + 16 * qt + col;
     if (qi >= N) continue;
     // log2-domain logsumexp of the scaled scores, for the backward pass
     if (lse != nullptr && grp == 0) lse[static_cast<size_t>(b) * 2 * N + qi] = off[qt] + log2f(l_tot);
     // lane l holds O^T[c = 16h + 4*(l/16) + r][q = l%16]; one reciprocal
     // per row instead of a division per channel
-    const float inv = 1.f / l_tot;
+    const float inv = __builtin_amdgcn_rcpf(l_tot);  // v_rcp_f32, 1 ulp
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
       const int cbase = 16 * h + 4 * grp;
@@ -434,6 +579,10 @@ static hipError_t launch_dense_q(const DenseArgs& a) {
 
 // A batch too small to give every SIMD a wave at two query tiles per wave
 // (B * N / 32 below 4 * kCUs) takes one tile per wave: twice the waves.
+// bf16 at d = 16 on rows of 256 keys or more staged whole, with at least
+// four waves per SIMD at four tiles per wave, takes four tiles: the staging,
+// bound and epilogue work of a wave is spread over twice the scores (B=4096,
+// N=256: 55.5 -> 51 us).
 template <typename T, int D>
 static hipError_t launch_dense(const DenseArgs& a) {
   if constexpr (sizeof(T) == 4) {
@@ -441,6 +590,11 @@ static hipError_t launch_dense(const DenseArgs& a) {
     if (dense_reg<D>(a, &e)) return e;
   }
   if (one_query_tile(a.B, a.N)) return launch_dense_q<T, D, 1>(a);
+  if constexpr (sizeof(T) == 2 && D == 16) {
+    if (a.N >= 256 && a.key_chunk >= a.N &&
+        static_cast<long>(a.B) * a.N >= 64L * 4 * 4 * kCUs)
+      return launch_dense_q<T, D, 4>(a);
+  }
   return launch_dense_q<T, D, kDenseQueryTiles>(a);
 }
 
@@ -450,7 +604,8 @@ size_t dense_lds_bytes(int dtype, int d, int kc) {
   const int cp = (d + 15) / 16 * 16;
   const size_t es = dtype == kF32 ? 4 : 2;
   const int ldk = dtype == kF32 ? d + 4 : d + 8;
-  return (static_cast<size_t>(kcp) * ldk + static_cast<size_t>(cp) * (kcp + 4)) * es;
+  // K, V^T, and 16 bytes for the row's max |k|^2
+  return (static_cast<size_t>(kcp) * ldk + static_cast<size_t>(cp) * (kcp + 4)) * es + 16;
 }
 
 hipError_t run_dense(const DenseArgs& a) {

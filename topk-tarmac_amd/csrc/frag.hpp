@@ -67,14 +67,15 @@ __device__ __forceinline__ void ld_bf16(float (&dst)[E], const bf16* src) {
 template <int E>
 __device__ __forceinline__ void st_bf16(bf16* dst, const float (&src)[E]) {
   static_assert(E % 4 == 0, "bf16 vector width");
+  // hardware round to nearest even (v_cvt_pk_bf16_f32, two values per
+  // instruction), the rounding of Tensor.to(torch.bfloat16)
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 #pragma unroll
   for (int i = 0; i < E / 4; ++i) {
-    uint2 v;
-    v.x = static_cast<uint32_t>(f32_to_bf16(src[4 * i])) |
-          (static_cast<uint32_t>(f32_to_bf16(src[4 * i + 1])) << 16);
-    v.y = static_cast<uint32_t>(f32_to_bf16(src[4 * i + 2])) |
-          (static_cast<uint32_t>(f32_to_bf16(src[4 * i + 3])) << 16);
-    *reinterpret_cast<uint2*>(dst + 4 * i) = v;
+    const bf16x2_t lo = {static_cast<__bf16>(src[4 * i]), static_cast<__bf16>(src[4 * i + 1])};
+    const bf16x2_t hi = {static_cast<__bf16>(src[4 * i + 2]), static_cast<__bf16>(src[4 * i + 3])};
+    *reinterpret_cast<uint2*>(dst + 4 * i) =
+        make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
   }
 }
 
@@ -126,6 +127,13 @@ struct Frag<float, D> {
     for (int t = 0; t < NI; ++t) acc = step(kf, t, acc);
     return acc;
   }
+  // sum of squares of this lane's quarter of the (pre-scaled) query row
+  __device__ __forceinline__ float sumsq() const {
+    float a = 0.f;
+#pragma unroll
+    for (int t = 0; t < E; ++t) a = fmaf(q[t], q[t], a);
+    return a;
+  }
 };
 
 // ---- bf16 -----------------------------------------------------------------
@@ -160,6 +168,10 @@ struct Frag<bf16, 16> {
   __device__ __forceinline__ f32x4 score(const bf16* krow, int grp) const {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     return step(load_k(krow, grp), 0, acc);
+  }
+  __device__ __forceinline__ float sumsq() const {
+    const uint2 w = __builtin_bit_cast(uint2, q);
+    return dot2_bf16(w.y, w.y, dot2_bf16(w.x, w.x, 0.f));
   }
 };
 
@@ -207,6 +219,17 @@ struct FragBf16Wide {
 #pragma unroll
     for (int h = 0; h < NI; ++h) acc = step(kf, h, acc);
     return acc;
+  }
+  __device__ __forceinline__ float sumsq() const {
+    float a = 0.f;
+#pragma unroll
+    for (int h = 0; h < NI; ++h) {
+      const uint4 w = __builtin_bit_cast(uint4, q[h]);
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a = dot2_bf16(ww[e], ww[e], a);
+    }
+    return a;
   }
 };
 
