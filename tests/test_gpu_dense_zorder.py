@@ -106,10 +106,12 @@ def test_dense_loose_offset_bound(dtype, B, N, spread):
 
 
 @pytest.mark.parametrize("B,N,d", [(1024, 256, 16), (4096, 256, 16), (512, 512, 16), (1024, 256, 32),
-                                   (256, 256, 64)])
+                                   (2048, 256, 32), (256, 512, 32), (256, 256, 64)])
 def test_dense_bf16_large_batch(B, N, d):
-    """The launch shapes the bench times (two and four query tiles per wave)
-    on sampled rows against float64 evaluation of the bf16 inputs."""
+    """The launch shapes the bench times (two and four query tiles per wave;
+    rows of 512 keys at d = 32 staged whole in 80 KB, of 256 keys at d = 64
+    in two chunks) on sampled rows against float64 evaluation of the bf16
+    inputs."""
     from tarmac.kernels import fused_dense_attention
     q, k, v = qkv(5 * B + N + d, B, N, d)
     qb, kb, vb = (O.bf16_round(x) for x in (q, k, v))

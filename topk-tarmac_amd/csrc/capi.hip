@@ -40,6 +40,12 @@ constexpr size_t kBf16TopkLds = 49 * 1024;
 // 69 KB, so those rows may use up to 80 KB (two workgroups per CU; gfx950
 // has 160 KB of LDS per CU).
 size_t lds_budget(int d) { return d > 64 ? 80 * 1024 : kLdsBudget; }
+// Dense rows staged whole take the fixed exponent offset (no running
+// maximum), so the dense kernel may use 80 KB (two workgroups per CU): rows
+// of 512 keys at d = 32 then fit one chunk (bf16 B=4096 N=512: 334 -> 242
+// us). At d = 64 the 256-key rows that would then fit ran slower at
+// B >= 1024 (156 -> 163 us) than two chunks at 64 KB.
+size_t dense_lds_budget(int d) { return d == 64 ? kLdsBudget : 80 * 1024; }
 constexpr int kZorderMaxN = 4096;  // agents per row the Morton selector sorts
 constexpr size_t kZorderLds = 160 * 1024;  // LDS per workgroup on gfx950
 
@@ -126,11 +132,11 @@ int dense_common(const void* q, const void* k, const void* v, void* out, float* 
   int kc = key_chunk;
   if (kc <= 0) {
     kc = (N + 63) / 64 * 64;
-    while (kc > 64 && tarmac::dense_lds_bytes(dtype, d, kc) > lds_budget(d)) kc -= 64;
+    while (kc > 64 && tarmac::dense_lds_bytes(dtype, d, kc) > dense_lds_budget(d)) kc -= 64;
   } else if (kc % 16 != 0) {
     return fail(TARMAC_ERR_INVALID, "%s: key_chunk must be a multiple of 16 (got %d)", fn, kc);
   }
-  if (tarmac::dense_lds_bytes(dtype, d, kc) > lds_budget(d))
+  if (tarmac::dense_lds_bytes(dtype, d, kc) > dense_lds_budget(d))
     return fail(TARMAC_ERR_UNSUPPORTED, "%s: key_chunk %d exceeds the LDS budget at d=%d", fn, kc, d);
   tarmac::DenseArgs a{q, k, v, out, B, N, d, dtype, kc, inv_sqrt(d), stream, stats};
   return hip_status(tarmac::run_dense(a), fn);

@@ -579,10 +579,10 @@ static hipError_t launch_dense_q(const DenseArgs& a) {
 
 // A batch too small to give every SIMD a wave at two query tiles per wave
 // (B * N / 32 below 4 * kCUs) takes one tile per wave: twice the waves.
-// bf16 at d = 16 on rows of 256 keys or more staged whole, with at least
-// four waves per SIMD at four tiles per wave, takes four tiles: the staging,
-// bound and epilogue work of a wave is spread over twice the scores (B=4096,
-// N=256: 55.5 -> 51 us).
+// bf16 at d = 16 and 32 on rows of 256 keys or more staged whole, with at
+// least four (d = 32: eight) waves per SIMD at four tiles per wave, takes
+// four tiles: the staging, bound and epilogue work of a wave is spread over
+// twice the scores (B=4096, N=256: d = 16 55.5 -> 51 us, d = 32 76 -> 68.5).
 template <typename T, int D>
 static hipError_t launch_dense(const DenseArgs& a) {
   if constexpr (sizeof(T) == 4) {
@@ -590,9 +590,9 @@ static hipError_t launch_dense(const DenseArgs& a) {
     if (dense_reg<D>(a, &e)) return e;
   }
   if (one_query_tile(a.B, a.N)) return launch_dense_q<T, D, 1>(a);
-  if constexpr (sizeof(T) == 2 && D == 16) {
+  if constexpr (sizeof(T) == 2 && D <= 32) {
     if (a.N >= 256 && a.key_chunk >= a.N &&
-        static_cast<long>(a.B) * a.N >= 64L * 4 * 4 * kCUs)
+        static_cast<long>(a.B) * a.N >= (D == 16 ? 4L : 8L) * 64 * 4 * kCUs)
       return launch_dense_q<T, D, 4>(a);
   }
   return launch_dense_q<T, D, kDenseQueryTiles>(a);
