@@ -133,6 +133,10 @@ int dense_common(const void* q, const void* k, const void* v, void* out, float* 
   if (kc <= 0) {
     kc = (N + 63) / 64 * 64;
     while (kc > 64 && tarmac::dense_lds_bytes(dtype, d, kc) > dense_lds_budget(d)) kc -= 64;
+    // a row in several chunks takes equal ones (N = 1024 as 512 + 512, not
+    // 960 + 64): the same rounds, less LDS per workgroup
+    const int nch = (N + kc - 1) / kc;
+    if (nch > 1) kc = ((N + nch - 1) / nch + 63) / 64 * 64;
   } else if (kc % 16 != 0) {
     return fail(TARMAC_ERR_INVALID, "%s: key_chunk must be a multiple of 16 (got %d)", fn, kc);
   }
