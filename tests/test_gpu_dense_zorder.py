@@ -105,6 +105,40 @@ def test_dense_loose_offset_bound(dtype, B, N, spread):
     assert normwise(out[rows], ref) <= tol
 
 
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("where", ["all", "late"])
+@pytest.mark.parametrize("spread", [0.0, 15.0, 60.0])
+def test_dense_loose_offset_bound_chunked(dtype, where, spread):
+    """Rows in four 64-key chunks: the offset is the bound over the keys
+    staged so far and rises with a chunk that holds a longer key. `late` puts
+    the long keys in the last two chunks only, so the first chunks' terms are
+    rescaled by 2^-(rise) (about 2^-33 at spread 15; at 60 they vanish and the
+    workgroup reruns the row online)."""
+    from tarmac.kernels import fused_dense_attention
+    B, N, d = 128, 256, 16
+    g = np.random.default_rng(int(spread) + (7 if where == "late" else 0))
+    q = g.standard_normal((B, N, d)).astype(np.float32) * 0.1
+    k = g.standard_normal((B, N, d)).astype(np.float32) * 0.1
+    v = g.standard_normal((B, N, d)).astype(np.float32)
+    q[:, ::2, 0] = 8.0
+    q[:, 1::2, 0] = g.standard_normal((B, N // 2)).astype(np.float32)
+    k[..., 0] = g.standard_normal((B, N)).astype(np.float32)
+    if where == "all":
+        k[..., 1] = spread
+    else:
+        k[:, N // 2:, 1] = spread
+    if dtype == "bf16":
+        q, k, v = (O.bf16_round(x) for x in (q, k, v))
+        out = host(fused_dense_attention(*dev(q, k, v, dtype=torch.bfloat16), block_kn=64))
+        tol = BF16_TOL
+    else:
+        out = host(fused_dense_attention(*dev(q, k, v), block_kn=64))
+        tol = F32_TOL
+    rows = np.random.default_rng(3).choice(B, 24, replace=False)
+    assert np.isfinite(out).all()
+    assert normwise(out[rows], O.canon_dense(q[rows], k[rows], v[rows])) <= tol
+
+
 @pytest.mark.parametrize("B,N,d", [(1024, 256, 16), (4096, 256, 16), (512, 512, 16), (1024, 256, 32),
                                    (2048, 256, 32), (256, 512, 32), (256, 256, 64)])
 def test_dense_bf16_large_batch(B, N, d):

@@ -263,6 +263,20 @@ __device__ __forceinline__ void dense_blocks(const Frag<T, D> (&frag)[QT], const
   }
 }
 
+// A fixed-offset row whose softmax sum is below 2^-64 (the bound sat too far
+// above its maximum), above 2N (each term is at most 1) or not a number must
+// run again with the online softmax.
+template <typename T, int QT>
+__device__ __forceinline__ bool sum_out_of_range(const f32x4 (&l_run)[QT], int N) {
+  bool out = false;
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const float l_tot = row_total<T>(l_run[qt]);
+    out |= !(l_tot >= kDenseTinySum && l_tot <= 2.f * static_cast<float>(N));
+  }
+  return out;
+}
+
 // Sum of squares of LDS row `row` (D elements, 16-byte aligned).
 template <typename T, int D>
 __device__ __forceinline__ float row_sumsq(const T* row) {
@@ -365,31 +379,83 @@ dense_kernel(const T* __restrict__ Q, const T* __restrict__ Kx, const T* __restr
     }
     dense_blocks<false, T, D, QT>(frag, Ks, Vt, ldv, 0, N, cnp, q0, self_r, lane, grp, post, acc,
                                   off, l_run);
-    bool low = false;
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      const float l_tot = row_total<T>(l_run[qt]);
-      low |= !(l_tot >= kDenseTinySum);  // also a NaN sum
-    }
-    if (__any(low)) {  // uniform: the wave runs the row again, online
+    if (__any(sum_out_of_range<T, QT>(l_run, N))) {  // uniform: the wave runs the row again, online
       reset();
       dense_blocks<true, T, D, QT>(frag, Ks, Vt, ldv, 0, N, cnp, q0, self_r, lane, grp, post, acc,
                                    off, l_run);
     }
   } else {
-    for (int c0 = 0; c0 < N; c0 += kc) {
-      const int cn = min(kc, N - c0);
-      const int cnp = (cn + BK - 1) / BK * BK;
+    // several chunks (d <= 32): the offset is the bound over the keys staged
+    // so far, raised with the chunk that holds a longer key (an exact 2^-x
+    // rescale of the query's sum and accumulator, before the chunk's first
+    // block); a workgroup with a sum out of range runs every chunk again,
+    // online. At d = 64 the per-chunk bound costs more than the running
+    // maximum it removes (fp32 B=256 N=512: 156 -> 167 us), so those rows run
+    // online from the start.
+    bool online = D > 32;
+    if constexpr (D <= 32) {
+      uint32_t* rerun = kmax_slot + 1;
+      if (threadIdx.x == 0) {
+        *kmax_slot = 0u;
+        *rerun = 0u;
+      }
+      float qn2[QT];
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        qn2[qt] = frag[qt].sumsq();
+        qn2[qt] += __shfl_xor(qn2[qt], 16);
+        qn2[qt] += __shfl_xor(qn2[qt], 32);
+      }
+      for (int c0 = 0; c0 < N; c0 += kc) {
+        const int cn = min(kc, N - c0);
+        const int cnp = (cn + BK - 1) / BK * BK;
+        __syncthreads();
+        stage_kv<T, D, LDK, PV::CP>(Ks, Vt, ldv, Kx + boff + static_cast<size_t>(c0) * D,
+                                    V + boff + static_cast<size_t>(c0) * D, cn, cnp);
+        __syncthreads();
+        float kn2 = 0.f;  // the running maximum in LDS only grows
+        for (int r = threadIdx.x; r < cn; r += blockDim.x)
+          kn2 = fmaxf(kn2, row_sumsq<T, D>(Ks + r * LDK));
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) kn2 = fmaxf(kn2, __shfl_xor(kn2, m));
+        if (lane == 0) atomicMax(kmax_slot, __float_as_uint(kn2));
+        __syncthreads();
+        if (q0 >= N) continue;
+        const float kmax2 = __uint_as_float(*kmax_slot);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          const float o = post * __builtin_amdgcn_sqrtf(qn2[qt] * kmax2);
+          if (o > off[qt]) {  // first chunk: off = -inf, alpha = 0 on zeros
+            const float alpha = fast_exp2(off[qt] - o);
+            l_run[qt] *= alpha;
+#pragma unroll
+            for (int h = 0; h < NH; ++h) acc[qt][h] *= alpha;
+            off[qt] = o;
+          }
+        }
+        dense_blocks<false, T, D, QT>(frag, Ks, Vt, ldv, c0, cn, cnp, q0, self_r, lane, grp, post,
+                                      acc, off, l_run);
+      }
+      if (q0 < N && __any(sum_out_of_range<T, QT>(l_run, N)) && lane == 0) atomicOr(rerun, 1u);
       __syncthreads();
-      // K and V^T in one pass of loads; bf16 rows transpose four at a time
-      // (8-byte stores instead of 2-byte ones), fp32 keeps one store per
-      // element, measured no slower
-      stage_kv<T, D, LDK, PV::CP>(Ks, Vt, ldv, Kx + boff + static_cast<size_t>(c0) * D,
-                                  V + boff + static_cast<size_t>(c0) * D, cn, cnp);
-      __syncthreads();
-      if (q0 >= N) continue;
-      dense_blocks<true, T, D, QT>(frag, Ks, Vt, ldv, c0, cn, cnp, q0, self_r, lane, grp, post, acc,
-                                   off, l_run);
+      online = *rerun != 0u;  // uniform across the workgroup
+    }
+    if (online) {
+      reset();
+      for (int c0 = 0; c0 < N; c0 += kc) {
+        const int cn = min(kc, N - c0);
+        const int cnp = (cn + BK - 1) / BK * BK;
+        __syncthreads();
+        // K and V^T in one pass of loads; bf16 rows transpose four at a time
+        // (8-byte stores instead of 2-byte ones), fp32 keeps one store per
+        // element, measured no slower
+        stage_kv<T, D, LDK, PV::CP>(Ks, Vt, ldv, Kx + boff + static_cast<size_t>(c0) * D,
+                                    V + boff + static_cast<size_t>(c0) * D, cn, cnp);
+        __syncthreads();
+        if (q0 >= N) continue;
+        dense_blocks<true, T, D, QT>(frag, Ks, Vt, ldv, c0, cn, cnp, q0, self_r, lane, grp, post,
+                                     acc, off, l_run);
+      }
     }
     if (q0 >= N) return;
   }
