@@ -1117,23 +1117,36 @@ static TopkPath choose_path(const TopkArgs& a, int mode) {
     // 11.5 vs 12.5 packed; N=32 k=1/4: 5.5/10.5 vs 8.0/12.2; at d = 32 the
     // fp32 chain's 8 steps per tile lose: N=64 k=1 21.9 vs 16.6)
     if (topk_reg_supported(a) && a.d == 16 && (a.topk <= 2 || a.N <= 32)) return kPathLists;
-    // k = 2, 3 up to B = 1024: the filter's proof leaves fewer queries to the
-    // per-query exact pass, whose tail sets the time of a launch this small
-    // (B=32 N=512 k=2/3: 9.4/10.3 vs 15.7/18.5 packed; B=32 N=1024 k=3: 15.2
-    // vs 30.9; B=256 N=256 k=2/3: 9.3/10.4 vs 11.0/12.9); at B = 4096 the
-    // packed scan's lower cost per score wins (N=512 k=2: 234.9 vs 242.5)
-    // the 32 x 32 kernel's single-product form (one bf16 MFMA per tile),
-    // two query tiles per wave: k = 4 on rows of 193 to 256 keys (B=1024
-    // N=256: 28.7 vs 31.2 filter; B=4096: 101.3 vs 109.9), and k = 2, 3 on
-    // rows of 193 to 384 keys where the filter would run (B <= 1024; B=256
-    // N=384 k=2/3: 13.3/14.8 vs 16.0/18.2; B=1024: 40.2/46.5 vs 50.3/61.2);
-    // elsewhere the filter and packed kernels are as fast or faster (B=4096
-    // N=256 k=3: 90.6 vs 83.4 packed; N=192 k=4: 87.8 vs 84.5; N=512 and
-    // 1024: equal to 15% slower)
-    if (split32_supported(a) && a.N > 192 && !one_query_tile(a.B, a.N) &&
-        ((a.topk == 4 && a.N <= 256) || (a.topk >= 2 && a.topk <= 3 && a.N <= 384 && a.B <= 1024)))
-      return kPathSplit32;
-    if (filt && a.N >= 256 && (a.topk >= 4 || (a.topk >= 2 && a.B <= 1024))) return kPathFilter;
+    // k <= 4 (measured per cell at d = 16, B = 32 .. 4096, N = 128 .. 1024,
+    // graph-batched calls): the filter where the packed pass's per-query
+    // exact tail sets a small launch's time -- rows of 512 keys and more at
+    // B <= 128, of 1024 at k >= 3 up to B = 256 (B=32 N=1024 k=3/4: 13.4/15.3
+    // vs 21.9/24.7 packed; B=256: 60.7/70.9 vs 65.5/77.3); the 32 x 32
+    // kernel's single-product form (one bf16 MFMA per tile, two query tiles
+    // per wave) at k = 4 on rows of 193-512 keys up to B = 1024 (B=256
+    // N=384: 15.8 vs 16.6 packed, 20.7 filter; B=1024 N=384/512: 50.3/79.4
+    // vs 50.3/80.1 packed, 70.2/84.5 filter) and at k = 2, 3 on rows of
+    // 193-384 keys up to B = 256 (B=128 N=256 k=2/3: 6.0/6.6 vs 6.4/7.1
+    // packed); the packed pass elsewhere (B=1024 N=256 k=2/3: 20.0/23.5 vs
+    // 21.3/24.6 on 32 x 32 tiles; B=4096 N=384 k=4: 181.8 vs 185.6, 266.2
+    // filter; B=1024 N=1024 k=2/3: 184.6/220.2 vs 189.8/230.2 filter)
+    // Where the 32 x 32 kernel would run but the batch takes one query tile
+    // per wave, the filter runs: its outputs equal the 32 x 32 kernel's bit
+    // for bit (both take the softmax of the exact scores; the packed pass's
+    // runs on its proof-bounded ones), so the launch shape never changes a
+    // result.
+    if (a.topk <= 4) {
+      if (filt && a.N >= 512 && (a.B <= 128 || (a.N >= 1024 && a.B <= 256 && a.topk >= 3)))
+        return kPathFilter;
+      if (split32_supported(a) && a.N > 192 &&
+          ((a.topk == 4 && a.N <= 512 && a.B <= 1024) ||
+           (a.topk >= 2 && a.topk <= 3 && a.N <= 384 && a.B <= 256)))
+        return !one_query_tile(a.B, a.N) ? kPathSplit32 : (filt ? kPathFilter : kPathPacked);
+      return kPathPacked;
+    }
+    // k > 4 (not part of that sweep) keeps the earlier rule: the filter from
+    // 256 keys
+    if (filt && a.N >= 256) return kPathFilter;
     return kPathPacked;
   }
   // split-bf16 scores on 32 x 32 tiles for rows of 128 to 256 keys once the
