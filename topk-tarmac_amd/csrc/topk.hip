@@ -1149,6 +1149,17 @@ static TopkPath choose_path(const TopkArgs& a, int mode) {
     if (filt && a.N >= 256) return kPathFilter;
     return kPathPacked;
   }
+  // k <= 4 on batches that take one query tile per wave, rows of 65-256
+  // keys or B * N up to 16384: the packed pass on exact fp32 scores (B=32,
+  // graph-batched calls: N=128 k=1/2: 4.2/4.4 vs 4.6/5.7 lists; N=256
+  // k=1/2/4: 5.5/5.7/6.9 vs 5.9/6.2/7.3 on split-bf16 scores; N=384:
+  // 6.9/7.1/8.4 vs 7.2/7.5/8.8; at B=64 N=384 the split-bf16 scores win
+  // again, 8.3 vs 9.0 at k = 1)
+  if (a.topk <= 4 && a.N > 64 && (a.N <= 256 || a.B * a.N <= 16384) && one_query_tile(a.B, a.N))
+    return kPathPacked;
+  // the lists at k <= 2 on rows of up to 128 keys up to B = 256 (B=256
+  // N=128 k=1/2: 4.8/5.9 vs 5.4/6.1 on 32 x 32 tiles)
+  if (a.topk <= 2 && a.N <= 128 && a.B <= 256) return kPathLists;
   // split-bf16 scores on 32 x 32 tiles for rows of 128 to 256 keys once the
   // batch gives every SIMD a wave of 32 queries (B=1024 N=256 k=1/2/4:
   // 24.3/27.3/35.2 vs 26.2/28.6/35.9 on 16 x 16 tiles; N=128: 10.4/11.7/16.2
