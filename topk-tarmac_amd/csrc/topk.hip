@@ -1157,6 +1157,12 @@ static TopkPath choose_path(const TopkArgs& a, int mode) {
   // again, 8.3 vs 9.0 at k = 1)
   if (a.topk <= 4 && a.N > 64 && (a.N <= 256 || a.B * a.N <= 16384) && one_query_tile(a.B, a.N))
     return kPathPacked;
+  // k = 1 at d = 32, 64 on rows of 512-1023 keys from B = 256: the filter
+  // (B=256 N=512/768 d=32: 44.1/88.1 vs 46.3/95.3 lists; d=64: 80.1/144.2 vs
+  // 83.2/167.0; at d = 16 the split-bf16 scores stay ahead, N=768: 40.4 vs
+  // 47.7)
+  if (filt && a.d >= 32 && a.topk == 1 && a.N >= 512 && a.N < 1024 && a.B >= 256)
+    return kPathFilter;
   // the lists at k <= 2 on rows of up to 128 keys up to B = 256 (B=256
   // N=128 k=1/2: 4.8/5.9 vs 5.4/6.1 on 32 x 32 tiles)
   if (a.topk <= 2 && a.N <= 128 && a.B <= 256) return kPathLists;
