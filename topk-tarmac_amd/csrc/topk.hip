@@ -1163,6 +1163,11 @@ static TopkPath choose_path(const TopkArgs& a, int mode) {
   // 47.7)
   if (filt && a.d >= 32 && a.topk == 1 && a.N >= 512 && a.N < 1024 && a.B >= 256)
     return kPathFilter;
+  // d = 64, k >= 3 on rows of 512 keys and more from B = 1024: the register
+  // lists (B=1024 N=512 k=3/4/6: 383.1/461.7/524.7 vs 408.1/514.2/580.0
+  // packed; B=2048 k=4: 862.8 vs 1016.0; at B = 256 packed stays ahead,
+  // 122.9 vs 124.0 at k = 4)
+  if (a.d == 64 && a.topk >= 3 && a.N >= 512 && a.B >= 1024) return kPathLists;
   // the lists at k <= 2 on rows of up to 128 keys up to B = 256 (B=256
   // N=128 k=1/2: 4.8/5.9 vs 5.4/6.1 on 32 x 32 tiles)
   if (a.topk <= 2 && a.N <= 128 && a.B <= 256) return kPathLists;
