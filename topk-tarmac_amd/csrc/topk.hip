@@ -1144,9 +1144,13 @@ static TopkPath choose_path(const TopkArgs& a, int mode) {
         return !one_query_tile(a.B, a.N) ? kPathSplit32 : (filt ? kPathFilter : kPathPacked);
       return kPathPacked;
     }
-    // k > 4 (not part of that sweep) keeps the earlier rule: the filter from
-    // 256 keys
-    if (filt && a.N >= 256) return kPathFilter;
+    // k = 5-8: the filter at small batches (B=32 N=384 k=5: 7.9 vs 10.8
+    // packed) and on 1024-key rows up to B = 256 at k <= 6 (B=256 k=5/6:
+    // 82.4/91.9 vs 87.2/99.7), the packed pass elsewhere (B=256 N=384
+    // k=5/6/8: 19.9/20.9/36.9 vs 28.8/27.2/38.1 filter; B=4096 N=384 k=8:
+    // 310.9 vs 451.3)
+    if (filt && a.N >= 256 && (a.B <= 128 || (a.N >= 1024 && a.B <= 256 && a.topk <= 6)))
+      return kPathFilter;
     return kPathPacked;
   }
   // k <= 4 on batches that take one query tile per wave, rows of 65-256
