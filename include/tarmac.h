@@ -272,8 +272,9 @@ int tarmac_set_topk_filter(int mode);
 /*
  * 16-query tiles per wavefront in the dense kernel, the packed top-k pass
  * (topk <= 4, N <= 1024) and the bf16 filter kernel: 0 = automatic (default:
- * two, or one when B * ceil(N / 32) < 1024, which would leave SIMDs idle),
- * 1 = one tile per wave, 2 = two tiles per wave. Results are identical either
+ * two, or one when B * ceil(N / 32) < 1024, which would leave SIMDs idle;
+ * bf16 dense at d <= 32 takes four on rows of 256+ keys staged whole at
+ * large batches), 1 = one tile per wave, 2 = two tiles per wave. Results are identical either
  * way, bit for bit; only the time differs (it lets a small test batch run the
  * instantiation a large batch uses). Process-wide, atomic. Returns the
  * previous mode, or -1 (and sets the last error) for an invalid mode. No

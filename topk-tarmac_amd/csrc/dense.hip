@@ -657,7 +657,7 @@ static hipError_t launch_dense(const DenseArgs& a) {
   }
   if (one_query_tile(a.B, a.N)) return launch_dense_q<T, D, 1>(a);
   if constexpr (sizeof(T) == 2 && D <= 32) {
-    if (a.N >= 256 && a.key_chunk >= a.N &&
+    if (query_tiles_mode() == kTilesAuto && a.N >= 256 && a.key_chunk >= a.N &&
         static_cast<long>(a.B) * a.N >= (D == 16 ? 4L : 8L) * 64 * 4 * kCUs)
       return launch_dense_q<T, D, 4>(a);
   }

@@ -143,6 +143,7 @@ int set_topk_filter_mode(int mode);  // returns the previous mode
 constexpr int kTilesAuto = 0, kTilesOne = 1, kTilesTwo = 2;
 int set_query_tiles_mode(int mode);  // returns the previous mode
 bool one_query_tile(int B, int N);   // the launch shape under the current mode
+int query_tiles_mode();              // kTilesAuto, kTilesOne or kTilesTwo
 hipError_t run_dense(const DenseArgs& a);
 hipError_t run_fixedset(const FixedsetArgs& a);
 hipError_t run_morton_window(const MortonArgs& a);

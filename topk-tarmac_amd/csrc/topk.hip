@@ -1064,6 +1064,7 @@ int set_topk_filter_mode(int mode) { return g_topk_filter_mode.exchange(mode); }
 static std::atomic<int> g_query_tiles_mode{kTilesAuto};
 
 int set_query_tiles_mode(int mode) { return g_query_tiles_mode.exchange(mode); }
+int query_tiles_mode() { return g_query_tiles_mode.load(std::memory_order_relaxed); }
 
 bool one_query_tile(int B, int N) {
   switch (g_query_tiles_mode.load(std::memory_order_relaxed)) {
